@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""Benchmark of the circulant attention hot path on one MI355X.
+
+A step is one fused forward + backward of circulant multi-head attention
+(circatt_fused_fwd, circatt_fused_bwd_dq, circatt_fused_bwd_dkdv) over one
+batch of synthetic N(0,1) float32 inputs already resident in HBM, at the
+configuration BASELINE.json's metric is quoted on (cfg3: DotSimilarity,
+256x256x64x4, 4 heads, ws = 15).  Prints one JSON line.
+
+Roofline: every kernel of the step is priced at its algorithmic FLOPs
+(U = 2*P*K*dh*nheads*B per window contraction; forward 2U, dq pass 2U for
+dP and dQ, dk/dv pass 2U for dV and dK; recomputation and softmax work not
+counted) against MI355X's dense FP32 MFMA peak, 157.3 TFLOP/s.  Kernel times
+come from HIP events on the stream the kernels run on.
+
+cpu_baseline: the oracle's float32 build (oracle/circatt_oracle.c: the
+reference's unfused algorithm, OpenMP over all host cores) timed on a bounded
+sample of the same workload (a few (head, batch) units).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "circulantattention.jl_amd"))
+
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense FP32 (matrix) peak
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    # name: (spatial fastest-first, C, B, nheads, ws, kind, complex)
+    "cfg3": ((256, 256), 64, 4, 4, 15, 0, False),
+    "cfg4a": ((512, 512), 32, 1, 1, 31, 1, False),
+    "cfg4b": ((262144,), 32, 2, 1, 63, 1, False),
+    "cfg5": ((320, 320), 32, 2, 2, 11, 0, True),
+}
+
+
+def describe(name):
+    dims, C, B, nh, ws, kind, cplx = CONFIGS[name]
+    sim = "Distance" if kind else "Dot"
+    typ = "ComplexF32" if cplx else "Float32"
+    sp = "x".join(str(d) for d in dims)
+    return (f"{name}: fused circulant_mh_attention fwd+bwd, {sim}Similarity, {typ}, "
+            f"{sp}x{C}x{B}, nheads={nh}, ws={ws}, A not materialised")
+
+
+def cpu_baseline(name, budget_s=12.0):
+    """Time the float32 oracle (reference's unfused algorithm, OpenMP) on
+    whole (head, batch) units of the workload until ~budget_s of CPU work."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import oracle as O
+
+    dims, C, B, nh, ws, kind, cplx = CONFIGS[name]
+    dh = C // nh
+    P = int(math.prod(dims))
+    rng = np.random.default_rng(1000 + 3)
+    shape = (1, dh, *reversed(dims))
+
+    def signal():
+        if cplx:
+            return ((rng.standard_normal(shape) + 1j * rng.standard_normal(shape)) /
+                    np.sqrt(2)).astype(np.complex64)
+        return rng.standard_normal(shape).astype(np.float32)
+
+    units, total = 0, 0.0
+    while units < nh * B and total < budget_s:
+        q, k, v, dy = (signal() for _ in range(4))
+        t0 = time.perf_counter()
+        _, A = O.attention_fwd(kind, q, k, v, ws, 1, precision="f32")
+        O.attention_bwd(kind, q, k, v, dy, ws, 1, precision="f32", A=A)
+        total += time.perf_counter() - t0
+        units += 1
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    pixels = units / nh * P  # one pixel of the metric carries all nh heads
+    return {
+        "value": pixels / total / 1e6,
+        "unit": "Mpixel/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"{units} of {nh * B} (head,batch) units of {name}, fwd+bwd of the "
+                   f"reference's unfused algorithm (float32 C/OpenMP restatement), "
+                   f"{total:.1f} s"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; the (head, batch) units "
+                                   "shard across GPUs without communication, see DESIGN.md"}))
+        sys.exit(2)
+
+    import torch
+
+    from circulant_attention import _lib as L
+    from circulant_attention._functions import ptr
+
+    base = json.load(open(os.path.join(ROOT, "BASELINE.json")))
+    dims, C, B, nh, ws, kind, cplx = CONFIGS[args.config]
+    nsp = len(dims)
+    n1, n2 = dims[0], (dims[1] if nsp == 2 else 1)
+    P = int(math.prod(dims))
+    K = ws ** nsp
+    dh = C // nh
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1003)
+    dtype = torch.complex64 if cplx else torch.float32
+    shape = (B, C, *reversed(dims))
+    q, k, v, dy = (torch.randn(shape, device=dev, dtype=dtype, generator=g) for _ in range(4))
+    y = torch.empty_like(q)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    lse = torch.empty((B * nh, P), device=dev, dtype=torch.float32)
+    wbytes = L.lib.circatt_fused_bwd_workspace_bytes(nsp, n1, n2, nh, B)
+    work = torch.empty((wbytes // 4,), device=dev, dtype=torch.float32)
+    dt = L.C32 if cplx else L.F32
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def fwd():
+        L.check(L.lib.circatt_fused_fwd(kind, dt, nsp, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
+                                        ptr(v), ptr(y), ptr(lse), sp))
+
+    def bwd_dq():
+        L.check(L.lib.circatt_fused_bwd_dq(kind, dt, nsp, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
+                                           ptr(v), ptr(y), ptr(dy), ptr(lse), ptr(dq),
+                                           ptr(work), wbytes, sp))
+
+    def bwd_dkdv():
+        L.check(L.lib.circatt_fused_bwd_dkdv(kind, dt, nsp, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
+                                             ptr(v), ptr(dy), ptr(lse), ptr(dk), ptr(dv),
+                                             ptr(work), wbytes, sp))
+
+    kernels = [("fwd", fwd), ("bwd_dq", bwd_dq), ("bwd_dkdv", bwd_dkdv)]
+    for _ in range(args.warmup):
+        for _, f in kernels:
+            f()
+    torch.cuda.synchronize()
+
+    # timed region: K steps, HIP events around every launch on `stream`
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in kernels] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        for (_, f), (e0, e1) in zip(kernels, evs[s]):
+            e0.record(stream)
+            f()
+            e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    kern_ms = {name: sum(evs[s][i][0].elapsed_time(evs[s][i][1]) for s in range(args.steps)) /
+               args.steps for i, (name, _) in enumerate(kernels)}
+
+    mpix = B * P / (ms_step / 1e3) / 1e6
+    cfac = 2 if cplx else 1
+    U = 2.0 * P * K * dh * nh * B * cfac
+    flops = {"fwd": 2 * U, "bwd_dq": 2 * U, "bwd_dkdv": 2 * U}
+    kern = {n: {"avg_ms": kern_ms[n], "alg_gflop": flops[n] / 1e9,
+                "tflops": flops[n] / (kern_ms[n] / 1e3) / 1e12} for n in kern_ms}
+    dom = max(kern_ms, key=kern_ms.get)
+    achieved = kern[dom]["tflops"]
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get(dom)
+    out = {
+        "metric": base["metric"],
+        "value": round(mpix, 3),
+        "unit": "Mpixel/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "c32" if cplx else "f32",
+        "data": "synthetic N(0,1), seeded, resident in HBM",
+        "config": {"workload": describe(args.config), "spatial": list(dims), "C": C, "B": B,
+                   "nheads": nh, "ws": ws, "similarity": "Distance" if kind else "Dot"},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 3),
+                     "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": traffic},
+        "step_roofline": {"alg_tflop_per_step": 6 * U / 1e12,
+                          "achieved_tflops": round(6 * U / (ms_step / 1e3) / 1e12, 3),
+                          "frac": round(6 * U / (ms_step / 1e3) / 1e12 / PEAK_FP32_TFLOPS, 4),
+                          "ceiling_mpixel_s": round(B * P / (6 * U / (PEAK_FP32_TFLOPS * 1e12))
+                                                    / 1e6, 1)},
+        "kernels": {n: {kk: round(vv, 4) for kk, vv in d.items()} for n, d in kern.items()},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.config)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,34 @@
+"""MI355X circulant attention: host binding of libcircatt mirroring the
+exports of CirculantAttention.jl (src/CirculantAttention.jl:18-25).
+
+Julia name              -> here
+  Circulant, circulant  -> Circulant, circulant
+  circulant_similarity(!), DotSimilarity, DistanceSimilarity
+                        -> circulant_similarity(_), DotSimilarity, DistanceSimilarity
+  circulant_adjacency(!)-> circulant_adjacency(_)
+  circulant_attention, circulant_mh_attention, circulant_mh_adjacency
+                        -> same names
+  ⊗, ⨷                  -> otimes (also ``A @ x``), Otimes
+  NNlib.softmax(!)      -> softmax(_)
+  CirculantAttention.scale, sum(A; dims), +, -, *
+                        -> scale, Circulant.sum, operators
+Gradients flow through torch.autograd with the reference's rrules
+(src/rrules.jl); Zygote.accum's role is played by autograd accumulation.
+"""
+from . import _lib
+from .circulant import (AbstractSimilarity, Circulant, DistanceSimilarity, DotSimilarity, Otimes,
+                        circulant, circulant_adjacency, circulant_adjacency_, circulant_attention,
+                        circulant_mh_adjacency, circulant_mh_attention,
+                        circulant_mh_transposed_attention, circulant_similarity,
+                        circulant_similarity_, circulant_transposed_attention, otimes, scale,
+                        softmax, softmax_)
+
+Circulant.__matmul__ = lambda A, x: otimes(A, x)
+
+__all__ = [
+    "AbstractSimilarity", "Circulant", "DistanceSimilarity", "DotSimilarity", "Otimes",
+    "circulant", "circulant_adjacency", "circulant_adjacency_", "circulant_attention",
+    "circulant_mh_adjacency", "circulant_mh_attention", "circulant_mh_transposed_attention",
+    "circulant_similarity", "circulant_similarity_", "circulant_transposed_attention", "otimes",
+    "scale", "softmax", "softmax_",
+]

@@ -1,0 +1,242 @@
+"""torch.autograd.Functions over the libcircatt C ABI.
+
+Each Function's forward calls one entry point and its backward restates the
+matching ChainRules rrule of the reference (src/rrules.jl) with libcircatt
+calls.  Tensors are device tensors in the reference's memory order: a Julia
+signal of size (N1[, N2], C, nb) is a torch tensor (nb, C[, N2], N1); a
+Circulant's nzVal (P*K, nb) is a tensor (nb, P, K).  torch provides device
+memory and the current HIP stream only.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib as L
+
+
+def stream_ptr(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def require(t: torch.Tensor, name: str):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must live on a HIP device (libcircatt has no CPU path)")
+    if t.dtype not in (torch.float32, torch.complex64):
+        raise TypeError(f"{name} must be float32 or complex64, got {t.dtype}")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    return L.C32 if t.is_complex() else L.F32
+
+
+def geometry(spatial):
+    """(nsp, n1, n2) for fastest-first spatial dims."""
+    if len(spatial) == 1:
+        return 1, spatial[0], 1
+    if len(spatial) == 2:
+        return 2, spatial[0], spatial[1]
+    raise AssertionError(f"{len(spatial)} spatial dims; only 1 and 2 are supported")
+
+
+def _c(t):
+    return t.contiguous()
+
+
+def similarity_raw(kind, x, y, spatial, ws, scale):
+    """nzval (nb, P, K) = scale * sim(x, y); x, y: (nb, C, *spatial-reversed)."""
+    nsp, n1, n2 = geometry(spatial)
+    nb, C = x.shape[0], x.shape[1]
+    P = int(math.prod(spatial))
+    K = ws ** nsp
+    nz = torch.empty((nb, P, K), dtype=torch.float32, device=x.device)
+    L.check(L.lib.circatt_similarity(kind, dtype_code(x), nsp, n1, n2, ws, C, nb, scale,
+                                     ptr(x), ptr(y), ptr(nz), stream_ptr(x.device)),
+            "circatt_similarity")
+    return nz
+
+
+def apply_raw(nz, x, spatial, ws, trans):
+    nsp, n1, n2 = geometry(spatial)
+    nb, C = x.shape[0], x.shape[1]
+    y = torch.empty_like(x)
+    L.check(L.lib.circatt_apply(1 if trans else 0, dtype_code(x), nsp, n1, n2, ws, C, nb,
+                                ptr(nz), ptr(x), ptr(y), stream_ptr(x.device)), "circatt_apply")
+    return y
+
+
+def axpby_raw(alpha, X, beta=None, Y=None, nb=1):
+    """Z = alpha_b X + beta_b Y; alpha/beta are floats or (nb,) device tensors."""
+    Z = torch.empty_like(X)
+    nnz = X.numel() // nb
+    a_t = alpha if isinstance(alpha, torch.Tensor) else None
+    b_t = beta if isinstance(beta, torch.Tensor) else None
+    a0 = 0.0 if a_t is not None else float(alpha)
+    b0 = 0.0 if (b_t is not None or beta is None) else float(beta)
+    L.check(L.lib.circatt_axpby(nnz, nb, ptr(a_t), a0, ptr(X), ptr(b_t), b0, ptr(Y), ptr(Z),
+                                stream_ptr(X.device)), "circatt_axpby")
+    return Z
+
+
+class SimilarityFn(torch.autograd.Function):
+    """nzval = scale * circulant_similarity(kind, x, y, ws): forward
+    src/similarity.jl:31-103, pullback src/rrules.jl:1-32."""
+
+    @staticmethod
+    def forward(ctx, kind, x, y, spatial, ws, scale):
+        x, y = _c(x), _c(y)
+        ctx.save_for_backward(x, y)
+        ctx.meta = (kind, spatial, ws, scale)
+        return similarity_raw(kind, x, y, spatial, ws, scale)
+
+    @staticmethod
+    def backward(ctx, dS):
+        x, y = ctx.saved_tensors
+        kind, spatial, ws, scale = ctx.meta
+        nsp, n1, n2 = geometry(spatial)
+        dS = _c(dS)
+        nb, C = x.shape[0], x.shape[1]
+        dx = torch.empty_like(x) if ctx.needs_input_grad[1] else None
+        dy = torch.empty_like(y) if ctx.needs_input_grad[2] else None
+        L.check(L.lib.circatt_similarity_bwd(kind, dtype_code(x), nsp, n1, n2, ws, C, nb, scale,
+                                             ptr(dS), ptr(x), ptr(y), ptr(dx), ptr(dy),
+                                             stream_ptr(x.device)), "circatt_similarity_bwd")
+        return None, dx, dy, None, None, None
+
+
+class SoftmaxFn(torch.autograd.Function):
+    """Row softmax of nzval: src/similarity.jl:105-126, pullback src/rrules.jl:42-56."""
+
+    @staticmethod
+    def forward(ctx, nz):
+        nz = _c(nz)
+        K = nz.shape[-1]
+        out = torch.empty_like(nz)
+        L.check(L.lib.circatt_softmax(K, nz.numel() // K, ptr(nz), ptr(out),
+                                      stream_ptr(nz.device)), "circatt_softmax")
+        ctx.save_for_backward(out)
+        return out
+
+    @staticmethod
+    def backward(ctx, dA):
+        (A,) = ctx.saved_tensors
+        dA = _c(dA)
+        K = A.shape[-1]
+        dS = torch.empty_like(A)
+        L.check(L.lib.circatt_softmax_bwd(K, A.numel() // K, ptr(A), ptr(dA), ptr(dS),
+                                          stream_ptr(A.device)), "circatt_softmax_bwd")
+        return dS
+
+
+class ApplyFn(torch.autograd.Function):
+    """y = A ⊗ x (trans False) or Aᵀ ⊗ x (trans True): src/attention.jl:53-80;
+    pullbacks src/rrules.jl:58-88:
+      ⊗:  ∂A = sim_Dot(Δy, x),  ∂x = Aᵀ ⊗ Δy
+      ⊗ᵀ: ∂A = sim_Dot(x, Δy),  ∂x = A ⊗ Δy"""
+
+    @staticmethod
+    def forward(ctx, nz, x, spatial, ws, trans):
+        nz, x = _c(nz), _c(x)
+        ctx.save_for_backward(nz, x)
+        ctx.meta = (spatial, ws, trans)
+        return apply_raw(nz, x, spatial, ws, trans)
+
+    @staticmethod
+    def backward(ctx, dy):
+        nz, x = ctx.saved_tensors
+        spatial, ws, trans = ctx.meta
+        dy = _c(dy)
+        dA = dx = None
+        if ctx.needs_input_grad[0]:
+            a, b = (x, dy) if trans else (dy, x)
+            dA = similarity_raw(L.DOT, a, b, spatial, ws, 1.0).view_as(nz)
+        if ctx.needs_input_grad[1]:
+            dx = apply_raw(nz, dy, spatial, ws, not trans)
+        return dA, dx, None, None, None
+
+
+class AxpbyFn(torch.autograd.Function):
+    """Z = alpha_b X + beta_b Y over nzval batches (src/array.jl:66-81, 179-189),
+    pullback of scale as src/rrules.jl:94-114."""
+
+    @staticmethod
+    def forward(ctx, alpha, X, beta, Y, nb):
+        X = _c(X)
+        Y = _c(Y) if Y is not None else None
+        ctx.save_for_backward(X, Y, alpha if isinstance(alpha, torch.Tensor) else None,
+                              beta if isinstance(beta, torch.Tensor) else None)
+        ctx.scalars = (alpha if not isinstance(alpha, torch.Tensor) else None,
+                       beta if not isinstance(beta, torch.Tensor) else None)
+        ctx.nb = nb
+        return axpby_raw(alpha, X, beta, Y, nb)
+
+    @staticmethod
+    def backward(ctx, dZ):
+        X, Y, a_t, b_t = ctx.saved_tensors
+        a_s, b_s = ctx.scalars
+        nb = ctx.nb
+        dZ = _c(dZ)
+        alpha = a_t if a_t is not None else a_s
+        beta = b_t if b_t is not None else b_s
+        dX = axpby_raw(alpha, dZ, None, None, nb) if ctx.needs_input_grad[1] else None
+        dY = None
+        if Y is not None and ctx.needs_input_grad[3]:
+            dY = axpby_raw(beta, dZ, None, None, nb)
+        da = batch_dot(dZ, X, nb) if (a_t is not None and ctx.needs_input_grad[0]) else None
+        db = None
+        if b_t is not None and Y is not None and ctx.needs_input_grad[2]:
+            db = batch_dot(dZ, Y, nb)
+        return da, dX, db, dY, None
+
+
+def batch_dot(A, B, nb):
+    """(nb,) per-batch sums of A .* B over nzval slices (the ∂c of the scale
+    rrule, src/rrules.jl:101-104).  Uses circatt_rowsum-free torch reduction of
+    a device product: one elementwise product (circatt_axpby is linear, so the
+    product itself is formed by torch) and a per-batch sum."""
+    return (A.reshape(nb, -1) * B.reshape(nb, -1)).sum(dim=1)
+
+
+class FusedAttentionFn(torch.autograd.Function):
+    """y = softmax(scale*sim(q,k)) ⊗ v without materialising A
+    (circatt_fused_fwd / circatt_fused_bwd).  Same value and gradients as the
+    composition circulant_adjacency -> ⊗ of src/attention.jl:19-42."""
+
+    @staticmethod
+    def forward(ctx, kind, q, k, v, spatial, ws, nheads):
+        q, k, v = _c(q), _c(k), _c(v)
+        nsp, n1, n2 = geometry(spatial)
+        B, C = q.shape[0], q.shape[1]
+        P = int(math.prod(spatial))
+        y = torch.empty_like(q)
+        lse = torch.empty((B * nheads, P), dtype=torch.float32, device=q.device)
+        L.check(L.lib.circatt_fused_fwd(kind, dtype_code(q), nsp, n1, n2, ws, C, nheads, B,
+                                        ptr(q), ptr(k), ptr(v), ptr(y), ptr(lse),
+                                        stream_ptr(q.device)), "circatt_fused_fwd")
+        ctx.save_for_backward(q, k, v, y, lse)
+        ctx.meta = (kind, spatial, ws, nheads)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        q, k, v, y, lse = ctx.saved_tensors
+        kind, spatial, ws, nheads = ctx.meta
+        nsp, n1, n2 = geometry(spatial)
+        B, C = q.shape[0], q.shape[1]
+        dy = _c(dy)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        wbytes = L.lib.circatt_fused_bwd_workspace_bytes(nsp, n1, n2, nheads, B)
+        ws_buf = torch.empty((wbytes // 4,), dtype=torch.float32, device=q.device)
+        L.check(L.lib.circatt_fused_bwd(kind, dtype_code(q), nsp, n1, n2, ws, C, nheads, B,
+                                        ptr(q), ptr(k), ptr(v), ptr(y), ptr(dy), ptr(lse),
+                                        ptr(dq), ptr(dk), ptr(dv), ptr(ws_buf), wbytes,
+                                        stream_ptr(q.device)), "circatt_fused_bwd")
+        return None, dq, dk, dv, None, None, None

@@ -1,0 +1,536 @@
+"""Circulant type and the circulant attention API, mirroring
+CirculantAttention.jl (names, argument meaning, assertion messages).
+
+Memory order follows the reference's Julia arrays (column-major): a Julia
+signal of size (N1, N2, C, B) is a torch tensor of shape (B, C, N2, N1) and a
+1D signal (L, C, B) is (B, C, L).  ``spatial_size`` is reported fastest-first
+like Julia, i.e. (N1, N2).  A Circulant of Julia size (P, P, nh, B) stores
+nzVal as a tensor (B, nh, P, K); rowPtr / colVal are the reference's Int32
+1-based CSR indices, built on the device on first access.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib as L
+from ._functions import (AxpbyFn, ApplyFn, FusedAttentionFn, SimilarityFn, SoftmaxFn, geometry,
+                         ptr, require, stream_ptr)
+
+
+class AbstractSimilarity:
+    kind = None
+
+    def __repr__(self):
+        return f"{type(self).__name__}()"
+
+    def __eq__(self, other):
+        return type(self) is type(other)
+
+    def __hash__(self):
+        return hash(type(self))
+
+
+class DotSimilarity(AbstractSimilarity):
+    """S_ij = Real(q[i]^H k[j])  (src/similarity.jl:3-15)."""
+    kind = L.DOT
+
+
+class DistanceSimilarity(AbstractSimilarity):
+    """S_ij = -sum(abs2, q[i] - k[j]) / 2  (src/similarity.jl:17-29, :71-75;
+    the reference docstring omits the minus sign, its kernel has it)."""
+    kind = L.DISTANCE
+
+
+def _kind(simfun) -> int:
+    if isinstance(simfun, type) and issubclass(simfun, AbstractSimilarity):
+        simfun = simfun()
+    if not isinstance(simfun, AbstractSimilarity):
+        raise TypeError(f"simfun must be DotSimilarity() or DistanceSimilarity(), got {simfun!r}")
+    return simfun.kind
+
+
+def _spatial(x: torch.Tensor):
+    """Fastest-first spatial size of a (nb, C, *reversed spatial) tensor."""
+    return tuple(reversed(x.shape[2:]))
+
+
+_PATTERNS: dict = {}
+
+
+def _pattern(spatial, ws, device):
+    """(rowptr (P+1,), colval (P*K,)) Int32 1-based, one batch, cached per device."""
+    key = (str(device), tuple(spatial), ws)
+    if key not in _PATTERNS:
+        nsp, n1, n2 = geometry(spatial)
+        P = int(math.prod(spatial))
+        K = ws ** nsp
+        rowptr = torch.empty((P + 1,), dtype=torch.int32, device=device)
+        colval = torch.empty((P * K,), dtype=torch.int32, device=device)
+        L.check(L.lib.circatt_pattern(nsp, n1, n2, ws, 1, ptr(rowptr), ptr(colval),
+                                      stream_ptr(device)), "circatt_pattern")
+        _PATTERNS[key] = (rowptr, colval)
+    return _PATTERNS[key]
+
+
+@dataclass
+class CSRData:
+    """The fields of CUDA.jl's CuSparseArrayCSR that the reference and its tests
+    touch (test/utils.jl:1-5, test/rrule.jl:10): rowPtr (B.., P+1), colVal
+    (B.., P*K), nzVal (B.., P*K), dims (Julia size), nnz (total stored)."""
+    rowPtr: torch.Tensor
+    colVal: torch.Tensor
+    nzVal: torch.Tensor
+    dims: tuple
+    nnz: int
+
+
+class Circulant:
+    """Circulant{T,N,M,S} (src/array.jl:1-18): a batched circulant-sparse CSR
+    matrix of Julia size (P, P, batch...) with window `kernel_length` over
+    `spatial_size`.  `nzval` (torch, (*reversed(batch), P, K)) is the only
+    differentiable field, as in test/utils.jl:13-30."""
+
+    def __init__(self, nzval: torch.Tensor, kernel_length: int, spatial_size):
+        self.nzval = nzval
+        self.kernel_length = int(kernel_length)
+        self.spatial_size = tuple(int(s) for s in spatial_size)
+        nsp = len(self.spatial_size)
+        if nsp not in (1, 2):
+            raise AssertionError("only 1 or 2 spatial dims are supported")
+        if tuple(nzval.shape[-2:]) != (self.P, self.K):
+            raise AssertionError(f"nzval trailing shape {tuple(nzval.shape[-2:])} != (P, K) = "
+                                 f"{(self.P, self.K)}")
+
+    # ---- constructors (src/array.jl:6-17, :29) ----
+    @classmethod
+    def new(cls, ws: int, dims, device="cuda", dtype=torch.float32):
+        """Circulant{T}(M, dims): dims = (spatial..., batch...) in Julia order;
+        nzVal initialised to ones (src/circulant.jl:69,91)."""
+        if ws % 2 != 1:
+            raise AssertionError(f"filter size M={ws} must be odd.")
+        dims = tuple(int(d) for d in dims)
+        spatial, batch = dims[:-2], dims[-2:]
+        P = int(math.prod(spatial))
+        K = ws ** len(spatial)
+        nz = torch.ones((*reversed(batch), P, K), dtype=torch.float32, device=device)
+        return cls(nz, ws, spatial)
+
+    # ---- metadata ----
+    @property
+    def nsp(self):
+        return len(self.spatial_size)
+
+    @property
+    def P(self):
+        return int(math.prod(self.spatial_size))
+
+    @property
+    def K(self):
+        return self.kernel_length ** self.nsp
+
+    @property
+    def batch(self):
+        """Julia-order batch dims, e.g. (nheads, B)."""
+        return tuple(reversed(self.nzval.shape[:-2]))
+
+    @property
+    def nb(self):
+        return int(math.prod(self.batch)) if self.batch else 1
+
+    @property
+    def device(self):
+        return self.nzval.device
+
+    def size(self, i=None):
+        """Julia size (P, P, batch...); i is 1-based like Julia."""
+        s = (self.P, self.P, *self.batch)
+        return s if i is None else s[i - 1]
+
+    @property
+    def shape(self):
+        return self.size()
+
+    def ndims(self):
+        return len(self.size())
+
+    @property
+    def data(self) -> CSRData:
+        rowptr, colval = _pattern(self.spatial_size, self.kernel_length, self.device)
+        rb = tuple(reversed(self.batch))
+        return CSRData(rowPtr=rowptr.expand(*rb, rowptr.numel()),
+                       colVal=colval.expand(*rb, colval.numel()),
+                       nzVal=self.nzval.reshape(*rb, self.P * self.K),
+                       dims=self.size(), nnz=self.nzval.numel())
+
+    def __repr__(self):
+        return (f"Circulant{{Float32, {self.ndims()}, {self.kernel_length}, {self.nsp}}} with "
+                f"kernel-length {self.kernel_length}, spatial-size {self.spatial_size}, "
+                f"size {self.size()}")
+
+    # ---- shape utilities (src/array.jl:49-60) ----
+    def reshape(self, *dims):
+        """reshape(A, :, :, dims...): the first two dims stay (P, P); the
+        batch dims are re-split (Julia order; one -1 or ':' allowed)."""
+        dims = [(-1 if d in (":", Ellipsis, None) else int(d)) for d in dims]
+        if len(dims) < 3:
+            raise AssertionError("reshape needs at least 3 dims")
+        for d in dims[:2]:
+            if d not in (-1, self.P):
+                raise AssertionError(f"the first two dims of a Circulant are {self.P}")
+        batch = dims[2:]
+        if batch.count(-1) > 1:
+            raise AssertionError("only one batch dim can be inferred")
+        if -1 in batch:
+            known = int(math.prod(d for d in batch if d != -1))
+            batch[batch.index(-1)] = self.nb // known
+        if int(math.prod(batch)) != self.nb:
+            raise AssertionError(f"cannot reshape batch {self.batch} to {tuple(batch)}")
+        nz = self.nzval.reshape(*reversed(batch), self.P, self.K)
+        return Circulant(nz, self.kernel_length, self.spatial_size)
+
+    def copy(self):
+        return Circulant(self.nzval.clone(), self.kernel_length, self.spatial_size)
+
+    def similar(self):
+        return Circulant(torch.empty_like(self.nzval), self.kernel_length, self.spatial_size)
+
+    def _same(self, other):
+        if not isinstance(other, Circulant):
+            return False
+        return (other.kernel_length == self.kernel_length
+                and other.spatial_size == self.spatial_size and other.batch == self.batch)
+
+    # ---- algebra on nzVal (src/array.jl:66-81, 179-189) ----
+    def __add__(self, other):
+        if not self._same(other):
+            raise AssertionError("Circulant + Circulant needs equal kernel length, spatial "
+                                 "size and batch dims")
+        nz = AxpbyFn.apply(1.0, self.nzval, 1.0, other.nzval, self.nb)
+        return Circulant(nz, self.kernel_length, self.spatial_size)
+
+    def __sub__(self, other):
+        if not self._same(other):
+            raise AssertionError("Circulant - Circulant needs equal kernel length, spatial "
+                                 "size and batch dims")
+        nz = AxpbyFn.apply(1.0, self.nzval, -1.0, other.nzval, self.nb)
+        return Circulant(nz, self.kernel_length, self.spatial_size)
+
+    def __neg__(self):
+        return (-1.0) * self
+
+    def __mul__(self, c):
+        if isinstance(c, (int, float)):
+            return self.__rmul__(c)
+        return NotImplemented
+
+    def __rmul__(self, c):
+        if isinstance(c, (int, float)):
+            nz = AxpbyFn.apply(float(c), self.nzval, None, None, self.nb)
+            return Circulant(nz, self.kernel_length, self.spatial_size)
+        if isinstance(c, torch.Tensor):
+            return scale(c, self)
+        return NotImplemented
+
+    def dot(self, other):
+        """dot(X, Y) = dot(X.nzVal, Y.nzVal) (src/array.jl:83-85)."""
+        if not self._same(other):
+            raise AssertionError("dot needs matching Circulants")
+        return (self.nzval * other.nzval).sum()
+
+    def sum(self, dims=None):
+        """sum(A; dims) (src/array.jl:156-177): dims=None (:) -> scalar,
+        1 -> (1, P, batch..), 2 -> (P, 1, batch..), (1, 2) -> (1, 1, batch..),
+        batch dims (>2) -> Circulant summed over them."""
+        nsp, n1, n2 = geometry(self.spatial_size)
+        rb = tuple(reversed(self.batch))
+        if dims is None:
+            return self.sum(2).sum()
+        if isinstance(dims, int):
+            dims = (dims,)
+        dims = tuple(dims)
+        if dims in ((1,), (2,)):
+            return CirculantSum.apply(self.nzval, self.spatial_size, self.kernel_length,
+                                      dims[0] == 1).reshape(
+                *rb, *((self.P, 1) if dims[0] == 1 else (1, self.P)))
+        if dims == (1, 2):
+            return self.sum(2).reshape(*rb, -1).sum(dim=-1).reshape(*rb, 1, 1)
+        if all(d > 2 for d in dims):
+            nz = self.nzval
+            axes = tuple(len(rb) - (d - 2) for d in dims)  # Julia dim d -> torch axis
+            for ax in sorted(axes, reverse=True):
+                nz = _sum_batch_axis(nz, ax)
+            return Circulant(nz, self.kernel_length, self.spatial_size)
+        raise NotImplementedError(f"dims={dims} not implemented.")
+
+
+def _sum_batch_axis(nz, ax):
+    """Sum nzval over one batch axis with circatt_axpby (keepdim)."""
+    n = nz.shape[ax]
+    out = nz.select(ax, 0).unsqueeze(ax)
+    for i in range(1, n):
+        out = AxpbyFn.apply(1.0, out, 1.0, nz.select(ax, i).unsqueeze(ax), 1)
+    return out
+
+
+class CirculantSum(torch.autograd.Function):
+    """sum(A; dims=1) (colsum) / sum(A; dims=2) (rowsum), src/array.jl:119-130."""
+
+    @staticmethod
+    def forward(ctx, nz, spatial, ws, col):
+        nsp, n1, n2 = geometry(spatial)
+        nz = nz.contiguous()
+        P = int(math.prod(spatial))
+        nb = nz.numel() // (P * ws ** nsp)
+        out = torch.empty((nb, P), dtype=torch.float32, device=nz.device)
+        fn = L.lib.circatt_colsum if col else L.lib.circatt_rowsum
+        L.check(fn(nsp, n1, n2, ws, nb, ptr(nz), ptr(out), stream_ptr(nz.device)), "sum")
+        ctx.meta = (spatial, ws, col, nz.shape)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        # d/dnz of a row (column) sum is the row's (column's) cotangent
+        # broadcast to its entries: the dS of the Distance rrule pattern.
+        spatial, ws, col, shape = ctx.meta
+        nsp = len(spatial)
+        P = int(math.prod(spatial))
+        K = ws ** nsp
+        g = g.contiguous().reshape(-1, P)
+        if not col:
+            return g.unsqueeze(-1).expand(-1, P, K).reshape(shape), None, None, None
+        # column sums: entry (r, t) has column c(r, t); gather g at colVal
+        _, colval = _pattern(spatial, ws, g.device)
+        idx = (colval.long() - 1).reshape(1, P * K).expand(g.shape[0], -1)
+        return torch.gather(g, 1, idx).reshape(shape), None, None, None
+
+
+# ---------------------------------------------------------------------------
+# API (src/similarity.jl, src/attention.jl)
+# ---------------------------------------------------------------------------
+
+def circulant(M: int, x: torch.Tensor) -> Circulant:
+    """circulant(M, x): Float32 Circulant of x's spatial size with batch
+    (1, B) (src/array.jl:29)."""
+    require(x, "x")
+    return Circulant.new(M, (*_spatial(x), 1, x.shape[0]), device=x.device)
+
+
+def _check_pair(x, y):
+    require(x, "x")
+    require(y, "y")
+    if x.shape != y.shape:
+        raise AssertionError(f"x and y must have equal sizes, got {tuple(x.shape)} and "
+                             f"{tuple(y.shape)}")
+    if x.dtype != y.dtype:
+        raise AssertionError("x and y must have equal element types")
+    if x.dim() not in (3, 4):
+        raise AssertionError("signals must be (B, C, L) or (B, C, N2, N1)")
+
+
+def circulant_similarity(simfun, x, y, W: int) -> Circulant:
+    """circulant_similarity(simfun, x, y, W) (src/similarity.jl:128-142).
+    Row i of the result is pixel i of x, columns are pixels of y; the result
+    is a Float32 Circulant of Julia size (P, P, 1, B)."""
+    _check_pair(x, y)
+    if W % 2 != 1:
+        raise AssertionError(f"filter size M={W} must be odd.")
+    spatial = _spatial(x)
+    nz = SimilarityFn.apply(_kind(simfun), x, y, spatial, W, 1.0)
+    return Circulant(nz.reshape(x.shape[0], 1, *nz.shape[1:]), W, spatial)
+
+
+def circulant_similarity_(A: Circulant, simfun, x, y) -> Circulant:
+    """circulant_similarity!(A, simfun, x, y) (src/similarity.jl:31-53): writes
+    into A.nzval (not differentiable)."""
+    _check_pair(x, y)
+    spatial = _spatial(x)
+    if A.nsp != len(spatial):
+        raise AssertionError(f"spatial_dims ({A.nsp}) of circulant matrix must match those of "
+                             f"data signal ({len(spatial)}).")
+    if A.nb != x.shape[0]:
+        raise AssertionError(f"batchdim of circulant matrix ({A.nb}) must match that of x, y "
+                             f"({x.shape[0]}).")
+    with torch.no_grad():
+        nz = SimilarityFn.apply(_kind(simfun), x, y, spatial, A.kernel_length, 1.0)
+        A.nzval.copy_(nz.reshape(A.nzval.shape))
+    return A
+
+
+def softmax(A: Circulant) -> Circulant:
+    """NNlib.softmax(A::Circulant): row softmax (src/similarity.jl:118-126)."""
+    return Circulant(SoftmaxFn.apply(A.nzval), A.kernel_length, A.spatial_size)
+
+
+def softmax_(A: Circulant, B: Circulant = None) -> Circulant:
+    """NNlib.softmax!(A, B=A) (src/similarity.jl:113-116), not differentiable."""
+    B = A if B is None else B
+    with torch.no_grad():
+        A.nzval.copy_(SoftmaxFn.apply(B.nzval))
+    return A
+
+
+def circulant_adjacency(simfun, x, y, W: int) -> Circulant:
+    """softmax ∘ circulant_similarity (src/similarity.jl:151-161)."""
+    return softmax(circulant_similarity(simfun, x, y, W))
+
+
+def circulant_adjacency_(A: Circulant, simfun, x, y) -> Circulant:
+    """circulant_adjacency!(A, simfun, x, y) (src/similarity.jl:144-148)."""
+    circulant_similarity_(A, simfun, x, y)
+    return softmax_(A)
+
+
+def _splitheads(x, nheads):
+    """splitheads (src/attention.jl:44): (B, C, ...) -> (B*nheads, C/nheads, ...);
+    head g of batch b becomes flattened batch g + nheads*b."""
+    B, C = x.shape[0], x.shape[1]
+    if C % nheads != 0:
+        raise AssertionError(f"channels ({C}) must be divisible by nheads ({nheads})")
+    return x.reshape(B * nheads, C // nheads, *x.shape[2:])
+
+
+def circulant_attention(*args, materialize: bool = True):
+    """Two forms, as in the reference:
+
+    * ``y, A = circulant_attention(simfun, q, k, v, W)`` / ``(q, k, v, W)``
+      (src/attention.jl:19-26): q and k are scaled by 1/sqrt(sqrt(C)), A is the
+      row-softmax adjacency (Julia size (P, P, 1, B)) and y = A ⊗ v.  With
+      ``materialize=False`` the fused kernels compute y without forming A and
+      ``None`` is returned in A's place.
+    * ``y = circulant_attention(A, x)`` = ``A ⊗ x`` (src/attention.jl:53-70).
+    """
+    if len(args) == 2 and isinstance(args[0], Circulant):
+        return _apply(args[0], args[1], trans=False)
+    if len(args) == 4:
+        args = (DotSimilarity(),) + tuple(args)
+    if len(args) != 5:
+        raise TypeError("circulant_attention(simfun, q, k, v, W), (q, k, v, W) or (A, x)")
+    simfun, q, k, v, W = args
+    return _attention(_kind(simfun), q, k, v, W, 1, materialize)
+
+
+def _attention(kind, q, k, v, W, nheads, materialize):
+    _check_pair(q, k)
+    _check_pair(q, v)
+    if W % 2 != 1:
+        raise AssertionError(f"filter size M={W} must be odd.")
+    spatial = _spatial(q)
+    if not materialize:
+        return FusedAttentionFn.apply(kind, q, k, v, spatial, W, nheads), None
+    qr, kr, vr = (_splitheads(t, nheads) for t in (q, k, v))
+    dh = qr.shape[1]
+    tau = math.sqrt(dh)
+    # q ./ sqrt(tau), k ./ sqrt(tau) fold into a similarity scale of 1/tau
+    S = SimilarityFn.apply(kind, qr, kr, spatial, W, 1.0 / tau)
+    A = SoftmaxFn.apply(S)
+    y = ApplyFn.apply(A, vr, spatial, W, False)
+    B = q.shape[0]
+    A = Circulant(A.reshape(B, nheads, *A.shape[1:]), W, spatial)
+    return y.reshape(q.shape), A
+
+
+def circulant_mh_attention(*args, materialize: bool = True, honor_simfun: bool = False):
+    """Two forms, as in the reference:
+
+    * ``y, A = circulant_mh_attention(simfun, q, k, v, W, nheads)``
+      (src/attention.jl:38-42): attention per head of C/nheads channels; A has
+      Julia size (P, P, nheads, B).  The reference ignores ``simfun`` and
+      always uses DotSimilarity (src/attention.jl:40); that is reproduced
+      unless ``honor_simfun=True``.  ``materialize=False`` selects the fused
+      kernels (A is not formed, ``None`` is returned in its place).
+    * ``y = circulant_mh_attention(A, x)`` = ``A ⨷ x`` (src/attention.jl:89-96).
+    """
+    if len(args) == 2 and isinstance(args[0], Circulant):
+        return _mh_apply(args[0], args[1], trans=False)
+    if len(args) == 5:
+        # src/attention.jl:43 forwards to a method that does not exist in the
+        # reference (MethodError); here it means DotSimilarity.
+        args = (DotSimilarity(),) + tuple(args)
+    if len(args) != 6:
+        raise TypeError("circulant_mh_attention(simfun, q, k, v, W, nheads) or (A, x)")
+    simfun, q, k, v, W, nheads = args
+    kind = _kind(simfun) if honor_simfun else L.DOT
+    return _attention(kind, q, k, v, W, int(nheads), materialize)
+
+
+def circulant_mh_adjacency(simfun, x, y, W: int, nheads: int) -> Circulant:
+    """circulant_mh_adjacency (src/attention.jl:46-51): adjacency per head,
+    Julia size (P, P, nheads, B)."""
+    xr, yr = _splitheads(x, nheads), _splitheads(y, nheads)
+    A = circulant_adjacency(simfun, xr, yr, W)
+    return A.reshape(":", ":", nheads, x.shape[0])
+
+
+def _apply(A: Circulant, x: torch.Tensor, trans: bool):
+    require(x, "x")
+    spatial = _spatial(x)
+    if A.nsp != len(spatial):
+        raise AssertionError(f"spatial-dims ({A.nsp}) of A must match spatial dims of x "
+                             f"({len(spatial)})")
+    if tuple(spatial) != A.spatial_size:
+        raise AssertionError(f"spatial size {tuple(spatial)} of x does not match A's "
+                             f"{A.spatial_size}")
+    if A.nb != x.shape[0]:
+        raise AssertionError(f"batch of A ({A.nb}) must match that of x ({x.shape[0]})")
+    nz = A.nzval.reshape(A.nb, A.P, A.K)
+    return ApplyFn.apply(nz, x, spatial, A.kernel_length, trans)
+
+
+def otimes(A: Circulant, x: torch.Tensor) -> torch.Tensor:
+    """A ⊗ x = circulant_attention(A, x) (src/attention.jl:53-70)."""
+    return _apply(A, x, trans=False)
+
+
+def circulant_transposed_attention(A: Circulant, x: torch.Tensor) -> torch.Tensor:
+    """Aᵀ ⊗ x (src/attention.jl:72-80)."""
+    return _apply(A, x, trans=True)
+
+
+def _mh_apply(A: Circulant, x, trans):
+    if len(A.batch) != 2:
+        raise AssertionError("⨷ needs a Circulant of Julia size (P, P, nheads, B)")
+    nheads = A.batch[0]
+    y = _apply(A.reshape(":", ":", ":"), _splitheads(x, nheads), trans)
+    return y.reshape(x.shape)
+
+
+def Otimes(A: Circulant, x: torch.Tensor) -> torch.Tensor:
+    """A ⨷ x = circulant_mh_attention(A, x) (src/attention.jl:89-96)."""
+    return _mh_apply(A, x, trans=False)
+
+
+def circulant_mh_transposed_attention(A: Circulant, x: torch.Tensor) -> torch.Tensor:
+    """(src/attention.jl:98-103)."""
+    return _mh_apply(A, x, trans=True)
+
+
+def scale(c: torch.Tensor, A: Circulant) -> Circulant:
+    """scale(c, A) = c .* A with c of Julia size (1, 1, batch...) broadcast over
+    A's batch dims (src/array.jl:179-189).  c is a torch tensor of shape
+    (*reversed(batch), 1, 1)."""
+    require(c, "c")
+    if c.is_complex():
+        raise NotImplementedError("complex scale factors are not supported")
+    if c.dim() < 2 or c.shape[-1] != 1 or c.shape[-2] != 1:
+        raise AssertionError("Scaling of non-batchdims of CuSparseArrayCSR not implemented")
+    cb = tuple(reversed(c.shape[:-2]))  # Julia batch dims of c
+    ab = A.batch
+    nd = max(len(cb), len(ab))
+    cb = cb + (1,) * (nd - len(cb))
+    ab = ab + (1,) * (nd - len(ab))
+    out = []
+    for ci, ai in zip(cb, ab):
+        if ci != ai and 1 not in (ci, ai):
+            raise AssertionError(f"cannot broadcast scale factor {cb} against batch {ab}")
+        out.append(max(ci, ai))
+    rb = tuple(reversed(out))
+    nz = A.nzval.reshape(*tuple(reversed(ab)), A.P, A.K)
+    if tuple(nz.shape[:-2]) != rb:
+        nz = nz.expand(*rb, A.P, A.K)  # materialised by AxpbyFn's contiguous()
+    alpha = c.reshape(*tuple(reversed(cb))).expand(*rb).reshape(-1)
+    nb = int(math.prod(rb))
+    z = AxpbyFn.apply(alpha.contiguous(), nz, None, None, nb)
+    return Circulant(z.reshape(*rb, A.P, A.K), A.kernel_length, A.spatial_size)

@@ -1,0 +1,49 @@
+// Kernel launchers shared between the kernel sources and the C-ABI layer.
+#pragma once
+
+#include "circatt_common.h"
+
+namespace circatt {
+
+hipError_t launch_pattern(const Geom &g, int64_t nb, int32_t *rowptr, int32_t *colval,
+                          hipStream_t s);
+hipError_t launch_softmax(int K, int64_t rows, const float *in, float *out, hipStream_t s);
+hipError_t launch_softmax_bwd(int K, int64_t rows, const float *A, const float *dA, float *dS,
+                              hipStream_t s);
+// y = scale * (op(A) ⊗ x - [corr] sums(A) .* z), op = identity or transpose
+hipError_t launch_apply(bool trans, bool corr, int ncomp, const Geom &g, int C, int64_t nb,
+                        float scale, const float *nz, const float *x, const float *z, float *y,
+                        hipStream_t s);
+hipError_t launch_similarity(bool dist, int ncomp, const Geom &g, int C, int64_t nb, float scale,
+                             const float *x, const float *y, float *nz, hipStream_t s);
+hipError_t launch_sum(bool col, const Geom &g, int64_t nb, const float *nz, float *out,
+                      hipStream_t s);
+hipError_t launch_axpby(int64_t nnz, int64_t nb, const float *alpha, float alpha0,
+                        const float *X, const float *beta, float beta0, const float *Y, float *Z,
+                        hipStream_t s);
+
+// Fused (MFMA) kernels.  Modes of the windowed-tile kernel family:
+enum FusedMode {
+    MODE_FWD = 0,   // y, lse                         (flash forward)
+    MODE_SIM = 1,   // nzval = scale * sim, CSR order (unfused similarity)
+    MODE_BWDQ = 2,  // dq and D = <dy, y>             (query-centric backward)
+    MODE_BWDKV = 3  // dk, dv                         (key-centric backward)
+};
+
+struct FusedProblem {
+    Geom g;
+    int kind;     // CIRCATT_DOT / CIRCATT_DISTANCE
+    int ncomp;    // 1 real, 2 complex
+    int dh;       // channels per head (per unit)
+    int64_t nunits;
+    float scale;  // similarity scale
+    const float *q, *k, *v, *y, *dy, *lse;
+    float *yout, *lse_out, *dq, *dk, *dv, *dbuf, *nz;
+};
+
+// Returns hipErrorNotSupported (never launching) if the shape is outside the
+// supported range: dh*ncomp > 64 or a 1D halo that exceeds LDS.
+hipError_t launch_fused(FusedMode mode, const FusedProblem &pr, hipStream_t s);
+bool fused_supported(FusedMode mode, const FusedProblem &pr);
+
+}  // namespace circatt

@@ -1,0 +1,309 @@
+// Unfused kernels: pattern, softmax (+ pullback), sparse apply (N and T),
+// similarity pullback, row/column sums, nzVal algebra.
+//
+// Every kernel walks window offsets rather than colVal, using the slot <->
+// offset bijection of circatt_common.h, so the transposed products gather
+// without atomics.  These kernels are memory/latency bound; the fused
+// MFMA kernels (fused.hip) carry the north-star path.
+#include "circatt_common.h"
+#include "circatt_kernels.h"
+
+namespace circatt {
+
+// ---------------------------------------------------------------------------
+// Pattern: src/circulant.jl:46-106 + repeat over batches (src/array.jl:9)
+// ---------------------------------------------------------------------------
+__global__ void pattern_kernel(Geom g, int64_t nb, int32_t *__restrict__ rowptr,
+                               int32_t *__restrict__ colval) {
+    const int64_t PK = g.P * g.K;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t n = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; n < PK; n += stride) {
+        const int64_t r = n / g.K;
+        const int t = (int)(n - r * g.K);
+        int d1, d2;
+        slot_offsets(g, r, t, d1, d2);
+        const int32_t col = (int32_t)(offset_pixel(g, r, d1, d2) + 1);
+        for (int64_t b = 0; b < nb; ++b) colval[n + b * PK] = col;
+    }
+    for (int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; r <= g.P; r += stride) {
+        const int32_t v = (int32_t)(1 + (int64_t)g.K * r);
+        for (int64_t b = 0; b < nb; ++b) rowptr[r + b * (g.P + 1)] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Row softmax and its pullback: one wavefront per row of K slots.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__global__ __launch_bounds__(256) void softmax_kernel(int K, int64_t rows,
+                                                      const float *__restrict__ in,
+                                                      float *__restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *a = in + row * K;
+    float *o = out + row * K;
+    float m = -INFINITY;
+    for (int t = lane; t < K; t += 64) m = fmaxf(m, a[t]);
+    m = wave_max(m);
+    float s = 0.f;
+    for (int t = lane; t < K; t += 64) s += __expf(a[t] - m);
+    s = wave_sum(s);
+    const float inv = 1.f / s;
+    for (int t = lane; t < K; t += 64) o[t] = __expf(a[t] - m) * inv;
+}
+
+__global__ __launch_bounds__(256) void softmax_bwd_kernel(int K, int64_t rows,
+                                                          const float *__restrict__ A,
+                                                          const float *dA, float *dS) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *a = A + row * K;
+    const float *da = dA + row * K;
+    float s = 0.f;
+    for (int t = lane; t < K; t += 64) s += a[t] * da[t];
+    s = wave_sum(s);
+    for (int t = lane; t < K; t += 64) dS[row * K + t] = a[t] * (da[t] - s);
+}
+
+// ---------------------------------------------------------------------------
+// Sparse apply.  One thread per (row, batch, chunk of CH channels).
+//   TRANS = false: y[r] = sum_t A[r,t] x[col(r,t)]          (A ⊗ x)
+//   TRANS = true : y[c] = sum_d A[r=c-d, slot(r,d)] x[r]     (Aᵀ ⊗ x)
+//   CORR        : y -= (sum of the A entries used) .* z     (Distance rrule)
+// Result is multiplied by `scale`.
+// ---------------------------------------------------------------------------
+template <int NCOMP, bool TRANS, bool CORR, int CH>
+__global__ __launch_bounds__(256) void apply_kernel(Geom g, int C, int64_t nb, float scale,
+                                                    const float *__restrict__ nz,
+                                                    const float *__restrict__ x,
+                                                    const float *__restrict__ z,
+                                                    float *__restrict__ y) {
+    const int nchunk = (C + CH - 1) / CH;
+    const int64_t total = g.P * nb * nchunk;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tid >= total) return;
+    const int64_t r = tid % g.P;
+    const int64_t rest = tid / g.P;
+    const int64_t b = rest % nb;
+    const int c0 = (int)(rest / nb) * CH;
+    const int cn = min(CH, C - c0);
+    const float *nzb = nz + b * g.P * g.K;
+    const float *xb = x + (int64_t)NCOMP * g.P * ((int64_t)C * b + c0);
+    float acc[CH * NCOMP];
+#pragma unroll
+    for (int i = 0; i < CH * NCOMP; ++i) acc[i] = 0.f;
+    float asum = 0.f;
+    const int p = g.p;
+    const int p2 = g.nsp == 1 ? 0 : p;
+    for (int d2 = -p2; d2 <= p2; ++d2) {
+        for (int d1 = -p; d1 <= p; ++d1) {
+            int64_t src;
+            float a;
+            if (!TRANS) {
+                src = offset_pixel(g, r, d1, d2);
+                a = nzb[r * g.K + offset_slot(g, r, d1, d2)];
+            } else {
+                src = offset_pixel(g, r, -d1, -d2);
+                a = nzb[src * g.K + offset_slot(g, src, d1, d2)];
+            }
+            asum += a;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                if (c < cn) {
+#pragma unroll
+                    for (int e = 0; e < NCOMP; ++e)
+                        acc[c * NCOMP + e] += a * xb[NCOMP * (src + g.P * c) + e];
+                }
+            }
+        }
+    }
+    const float *zb = z ? z + (int64_t)NCOMP * g.P * ((int64_t)C * b + c0) : nullptr;
+    float *yb = y + (int64_t)NCOMP * g.P * ((int64_t)C * b + c0);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        if (c < cn) {
+#pragma unroll
+            for (int e = 0; e < NCOMP; ++e) {
+                float v = acc[c * NCOMP + e];
+                if (CORR) v -= asum * zb[NCOMP * (r + g.P * c) + e];
+                yb[NCOMP * (r + g.P * c) + e] = v * scale;
+            }
+        }
+    }
+}
+
+// Similarity for shapes outside the fused kernels' range (more than 64 real
+// components per pixel): one thread per (nz, batch), sequential channel sum
+// in the order of src/similarity.jl:96-100.
+template <int NCOMP, bool DIST>
+__global__ __launch_bounds__(256) void similarity_kernel(Geom g, int C, int64_t nb, float scale,
+                                                         const float *__restrict__ x,
+                                                         const float *__restrict__ y,
+                                                         float *__restrict__ nz) {
+    const int64_t PK = g.P * g.K;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tid >= PK * nb) return;
+    const int64_t n = tid % PK, b = tid / PK;
+    const int64_t r = n / g.K;
+    int d1, d2;
+    slot_offsets(g, r, (int)(n - r * g.K), d1, d2);
+    const int64_t col = offset_pixel(g, r, d1, d2);
+    const float *xb = x + (int64_t)NCOMP * g.P * C * b;
+    const float *yb = y + (int64_t)NCOMP * g.P * C * b;
+    float s = 0.f;
+    for (int c = 0; c < C; ++c) {
+#pragma unroll
+        for (int e = 0; e < NCOMP; ++e) {
+            const float xv = xb[NCOMP * (r + g.P * c) + e];
+            const float yv = yb[NCOMP * (col + g.P * c) + e];
+            if (DIST) {
+                const float d = xv - yv;
+                s -= d * d;
+            } else {
+                s += xv * yv;
+            }
+        }
+    }
+    if (DIST) s *= 0.5f;
+    nz[tid] = s * scale;
+}
+
+// sum over a row's slots (dims=2) or a column's entries (dims=1)
+template <bool COL>
+__global__ void sum_kernel(Geom g, int64_t nb, const float *__restrict__ nz,
+                           float *__restrict__ out) {
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tid >= g.P * nb) return;
+    const int64_t r = tid % g.P, b = tid / g.P;
+    const float *nzb = nz + b * g.P * g.K;
+    float s = 0.f;
+    if (!COL) {
+        for (int t = 0; t < g.K; ++t) s += nzb[r * g.K + t];
+    } else {
+        const int p = g.p, p2 = g.nsp == 1 ? 0 : g.p;
+        for (int d2 = -p2; d2 <= p2; ++d2)
+            for (int d1 = -p; d1 <= p; ++d1) {
+                int64_t src = offset_pixel(g, r, -d1, -d2);
+                s += nzb[src * g.K + offset_slot(g, src, d1, d2)];
+            }
+    }
+    out[tid] = s;
+}
+
+__global__ void axpby_kernel(int64_t nnz, int64_t nb, const float *__restrict__ alpha,
+                             float alpha0, const float *X, const float *__restrict__ beta,
+                             float beta0, const float *Y, float *Z) {
+    const int64_t total = nnz * nb;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int64_t b = i / nnz;
+        const float a = alpha ? alpha[b] : alpha0;
+        float v = a * X[i];
+        if (Y) v += (beta ? beta[b] : beta0) * Y[i];
+        Z[i] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+static inline unsigned grid_for(int64_t n, int threads, int64_t cap = 1 << 20) {
+    int64_t b = (n + threads - 1) / threads;
+    if (b > cap) b = cap;
+    if (b < 1) b = 1;
+    return (unsigned)b;
+}
+
+hipError_t launch_pattern(const Geom &g, int64_t nb, int32_t *rowptr, int32_t *colval,
+                          hipStream_t s) {
+    hipLaunchKernelGGL(pattern_kernel, dim3(grid_for(g.P * g.K, 256)), dim3(256), 0, s, g, nb,
+                       rowptr, colval);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax(int K, int64_t rows, const float *in, float *out, hipStream_t s) {
+    hipLaunchKernelGGL(softmax_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, K,
+                       rows, in, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax_bwd(int K, int64_t rows, const float *A, const float *dA, float *dS,
+                              hipStream_t s) {
+    hipLaunchKernelGGL(softmax_bwd_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s,
+                       K, rows, A, dA, dS);
+    return hipGetLastError();
+}
+
+template <int NCOMP, bool TRANS, bool CORR>
+static hipError_t launch_apply_t(const Geom &g, int C, int64_t nb, float scale, const float *nz,
+                                 const float *x, const float *z, float *y, hipStream_t s) {
+    constexpr int CH = 8;
+    const int64_t total = g.P * nb * ((C + CH - 1) / CH);
+    hipLaunchKernelGGL((apply_kernel<NCOMP, TRANS, CORR, CH>), dim3(grid_for(total, 256, 1LL << 31)),
+                       dim3(256), 0, s, g, C, nb, scale, nz, x, z, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_apply(bool trans, bool corr, int ncomp, const Geom &g, int C, int64_t nb,
+                        float scale, const float *nz, const float *x, const float *z, float *y,
+                        hipStream_t s) {
+#define CIRCATT_APPLY_CASE(NC, T, CR)                                       \
+    if (ncomp == NC && trans == T && corr == CR)                            \
+        return launch_apply_t<NC, T, CR>(g, C, nb, scale, nz, x, z, y, s);
+    CIRCATT_APPLY_CASE(1, false, false)
+    CIRCATT_APPLY_CASE(1, true, false)
+    CIRCATT_APPLY_CASE(1, false, true)
+    CIRCATT_APPLY_CASE(1, true, true)
+    CIRCATT_APPLY_CASE(2, false, false)
+    CIRCATT_APPLY_CASE(2, true, false)
+    CIRCATT_APPLY_CASE(2, false, true)
+    CIRCATT_APPLY_CASE(2, true, true)
+#undef CIRCATT_APPLY_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_similarity(bool dist, int ncomp, const Geom &g, int C, int64_t nb, float scale,
+                             const float *x, const float *y, float *nz, hipStream_t s) {
+    const unsigned grid = grid_for(g.P * g.K * nb, 256, 1LL << 31);
+    if (ncomp == 1 && !dist)
+        hipLaunchKernelGGL((similarity_kernel<1, false>), dim3(grid), dim3(256), 0, s, g, C, nb, scale, x, y, nz);
+    else if (ncomp == 1 && dist)
+        hipLaunchKernelGGL((similarity_kernel<1, true>), dim3(grid), dim3(256), 0, s, g, C, nb, scale, x, y, nz);
+    else if (!dist)
+        hipLaunchKernelGGL((similarity_kernel<2, false>), dim3(grid), dim3(256), 0, s, g, C, nb, scale, x, y, nz);
+    else
+        hipLaunchKernelGGL((similarity_kernel<2, true>), dim3(grid), dim3(256), 0, s, g, C, nb, scale, x, y, nz);
+    return hipGetLastError();
+}
+
+hipError_t launch_sum(bool col, const Geom &g, int64_t nb, const float *nz, float *out,
+                      hipStream_t s) {
+    const unsigned grid = grid_for(g.P * nb, 256, 1LL << 31);
+    if (col)
+        hipLaunchKernelGGL(sum_kernel<true>, dim3(grid), dim3(256), 0, s, g, nb, nz, out);
+    else
+        hipLaunchKernelGGL(sum_kernel<false>, dim3(grid), dim3(256), 0, s, g, nb, nz, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_axpby(int64_t nnz, int64_t nb, const float *alpha, float alpha0,
+                        const float *X, const float *beta, float beta0, const float *Y, float *Z,
+                        hipStream_t s) {
+    hipLaunchKernelGGL(axpby_kernel, dim3(grid_for(nnz * nb, 256, 1 << 16)), dim3(256), 0, s,
+                       nnz, nb, alpha, alpha0, X, beta, beta0, Y, Z);
+    return hipGetLastError();
+}
+
+}  // namespace circatt

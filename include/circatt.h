@@ -1,0 +1,193 @@
+/*
+ * circatt.h -- C ABI of libcircatt, the MI355X (gfx950) circulant attention
+ * library.  Drop-in compute layer for CirculantAttention.jl's hot path: the
+ * reference reaches these operations through @cuda kernels, NNlib and
+ * CUSPARSE.bmm!; a host binding (Julia ccall, Python ctypes) calls these
+ * entry points instead.  Citations are file:line in the reference repository.
+ *
+ * Conventions
+ *  - All array pointers are device pointers owned by the caller.  Nothing in
+ *    an entry point allocates device memory; the fused backward takes a
+ *    caller-provided workspace (size from circatt_fused_bwd_workspace_bytes).
+ *  - Arrays use the reference's Julia column-major layout.  A signal of Julia
+ *    size (N1[,N2], C, nb) holds (pixel r, channel c, batch b) at
+ *    r + P*(c + C*b), P = N1*N2, r = i1 + N1*i2.  dtype CIRCATT_C32 signals
+ *    are ComplexF32, interleaved (re, im).
+ *  - A Circulant of size (P, P, nb) is CSR with K = ws^nsp slots per row:
+ *    rowPtr (P+1, nb) and colVal (P*K, nb) Int32 1-based, nzVal (P*K, nb)
+ *    Float32 (src/circulant.jl:64-106, src/array.jl:1-18).  Entry points that
+ *    take nzVal use the circulant pattern implied by (nsp, n1, n2, ws).
+ *  - nsp is 1 or 2; for nsp == 1, n2 is ignored.  ws must be odd
+ *    (src/circulant.jl:65,87).
+ *  - stream is a hipStream_t (NULL = default stream).  Launches are
+ *    asynchronous; arguments are validated on the host before any launch.
+ *  - Return value: CIRCATT_OK or a negative error code; circatt_last_error()
+ *    returns a message for the calling thread's last failure.
+ */
+#ifndef CIRCATT_H
+#define CIRCATT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CIRCATT_OK 0
+#define CIRCATT_ERR_INVALID (-1)     /* bad argument (the reference's @assert) */
+#define CIRCATT_ERR_UNSUPPORTED (-2) /* valid but not implemented here */
+#define CIRCATT_ERR_HIP (-3)         /* HIP runtime error */
+
+/* Similarity kinds: DotSimilarity / DistanceSimilarity (src/similarity.jl:1-29). */
+#define CIRCATT_DOT 0
+#define CIRCATT_DISTANCE 1
+
+/* Element types of signals: Float32, ComplexF32. */
+#define CIRCATT_F32 0
+#define CIRCATT_C32 1
+
+/* Library version (major*10000 + minor*100 + patch). */
+int circatt_version(void);
+
+/* Message describing the calling thread's last error ("" if none). */
+const char *circatt_last_error(void);
+
+/*
+ * Circulant sparsity pattern, replicated over nb batches.
+ * Replaces cucirculant(M,N) / cucirculant(M,N1,N2) + its kernel
+ * (src/circulant.jl:46-106) and the batch repeat in Circulant{T}(M, dims)
+ * (src/array.jl:6-11).  rowptr: (P+1, nb), colval: (P*K, nb), Int32 1-based,
+ * bit-identical to the reference, also for ws > N.
+ */
+int circatt_pattern(int nsp, int64_t n1, int64_t n2, int32_t ws, int64_t nb, int32_t *rowptr,
+                    int32_t *colval, void *stream);
+
+/*
+ * nzval[:, b] = scale * similarity(x[..., b], y[..., b]) on the pattern.
+ * Replaces circulant_similarity! and its Dot / Distance kernels
+ * (src/similarity.jl:31-103, :138-142).  x is the row (query) argument, y the
+ * column (key) argument; Dot: Re(sum_c x*conj(y)), Distance:
+ * -sum_c |x-y|^2 / 2.  x, y: (P, C, nb) of dtype; nzval: (P*K, nb) Float32.
+ * circulant_attention (src/attention.jl:19-23) uses scale = 1/sqrt(C).
+ */
+int circatt_similarity(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int32_t ws,
+                       int64_t C, int64_t nb, float scale, const void *x, const void *y,
+                       float *nzval, void *stream);
+
+/*
+ * Row softmax over the K slots of each of `rows` rows (rows = P*nb); in == out
+ * allowed.  Replaces circulant_softmax! / NNlib.softmax(::Circulant)
+ * (src/similarity.jl:105-126).
+ */
+int circatt_softmax(int64_t K, int64_t rows, const float *in, float *out, void *stream);
+
+/*
+ * dS = A .* (dA .- sum(A .* dA, dims=slots)).  Replaces the softmax pullback
+ * (src/rrules.jl:42-56, NNlib.∇softmax_data).  dS may alias dA.
+ */
+int circatt_softmax_bwd(int64_t K, int64_t rows, const float *A, const float *dA, float *dS,
+                        void *stream);
+
+/*
+ * y = A ⊗ x (trans = 0) or y = Aᵀ ⊗ x (trans = 1) with A = nzval on the
+ * pattern; x, y: (P, C, nb) of dtype (real A times complex x is the promotion
+ * of src/batchedmul.jl:72-75).  Replaces circulant_attention!(y, A, x) /
+ * circulant_transposed_attention! (src/attention.jl:53-80) and their
+ * CUSPARSE.bmm! calls (src/batchedmul.jl:82-110).  Multi-head ⨷
+ * (src/attention.jl:89-103) is the same call with C = channels/nheads and
+ * nb = nheads*B.
+ */
+int circatt_apply(int trans, int dtype, int nsp, int64_t n1, int64_t n2, int32_t ws, int64_t C,
+                  int64_t nb, const float *nzval, const void *x, void *y, void *stream);
+
+/*
+ * Pullback of nzval = scale * similarity(x, y):
+ *   Dot:      dx = scale * dS ⊠ y,            dy = scale * dSᵀ ⊠ x
+ *   Distance: dx = scale * (dS ⊠ y - rowsum(dS) .* x),
+ *             dy = scale * (dSᵀ ⊠ x - colsum(dS) .* y)
+ * Replaces the similarity rrules (src/rrules.jl:1-32) including their
+ * sum(ΔS; dims=1/2) (src/array.jl:119-130).  dx or dy may be NULL.
+ */
+int circatt_similarity_bwd(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int32_t ws,
+                           int64_t C, int64_t nb, float scale, const float *dS, const void *x,
+                           const void *y, void *dx, void *dy, void *stream);
+
+/*
+ * sum(A; dims=2) (out: (P, nb)) and sum(A; dims=1) (out: (P, nb)) of a
+ * Circulant's nzval (src/array.jl:119-130, :156-177).
+ */
+int circatt_rowsum(int nsp, int64_t n1, int64_t n2, int32_t ws, int64_t nb, const float *nzval,
+                   float *out, void *stream);
+int circatt_colsum(int nsp, int64_t n1, int64_t n2, int32_t ws, int64_t nb, const float *nzval,
+                   float *out, void *stream);
+
+/*
+ * Z[:, b] = alpha_b * X[:, b] + beta_b * Y[:, b] over nzval slices of nnz
+ * entries, alpha_b = alpha ? alpha[b] : alpha0 (same for beta; Y may be NULL).
+ * Covers X + Y, X - Y, c*X, -X (src/array.jl:66-81) and scale(c, A) with c of
+ * size (1,1,nh,B) (src/array.jl:179-189); Z may alias X or Y.
+ */
+int circatt_axpby(int64_t nnz, int64_t nb, const float *alpha, float alpha0, const float *X,
+                  const float *beta, float beta0, const float *Y, float *Z, void *stream);
+
+/*
+ * Fused forward of circulant (multi-head) attention without materialising A:
+ * for head g of batch b (channels g*dh .. g*dh+dh-1, dh = C/nheads),
+ *   y = softmax_rows(scale * sim(q, k)) ⊗ v,   scale = 1/sqrt(dh),
+ * and lse[r, g + nheads*b] = log(sum_c exp(scale * sim(q_r, k_c))).
+ * Equals circulant_attention (src/attention.jl:19-26, nheads = 1) and
+ * circulant_mh_attention (src/attention.jl:38-42) for the returned y.
+ * q, k, v, y: (P, C, B) of dtype; lse: (P, nheads*B) Float32.
+ */
+int circatt_fused_fwd(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int32_t ws,
+                      int64_t C, int64_t nheads, int64_t B, const void *q, const void *k,
+                      const void *v, void *y, float *lse, void *stream);
+
+/* Bytes of workspace circatt_fused_bwd needs (per-row D = <dy, y>). */
+int64_t circatt_fused_bwd_workspace_bytes(int nsp, int64_t n1, int64_t n2, int64_t nheads,
+                                          int64_t B);
+
+/*
+ * Fused backward matching the composition of the rrules of similarity,
+ * softmax and ⊗ (src/rrules.jl:1-72) and the q, k scaling of
+ * src/attention.jl:21: given dy, returns dq, dk, dv.  lse from
+ * circatt_fused_fwd.  No atomics: a query-centric pass writes dq, a
+ * key-centric pass writes dk and dv.
+ */
+int circatt_fused_bwd(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int32_t ws,
+                      int64_t C, int64_t nheads, int64_t B, const void *q, const void *k,
+                      const void *v, const void *y, const void *dy, const float *lse, void *dq,
+                      void *dk, void *dv, void *workspace, int64_t workspace_bytes,
+                      void *stream);
+
+/*
+ * The two passes of circatt_fused_bwd, for callers that time or schedule them
+ * separately.  circatt_fused_bwd_dq writes dq and the per-row D = <dy, y>
+ * into workspace; circatt_fused_bwd_dkdv reads that D and writes dk, dv, so
+ * it must follow circatt_fused_bwd_dq on the same stream with the same
+ * workspace.
+ */
+int circatt_fused_bwd_dq(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int32_t ws,
+                         int64_t C, int64_t nheads, int64_t B, const void *q, const void *k,
+                         const void *v, const void *y, const void *dy, const float *lse,
+                         void *dq, void *workspace, int64_t workspace_bytes, void *stream);
+int circatt_fused_bwd_dkdv(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int32_t ws,
+                           int64_t C, int64_t nheads, int64_t B, const void *q, const void *k,
+                           const void *v, const void *dy, const float *lse, void *dk, void *dv,
+                           const void *workspace, int64_t workspace_bytes, void *stream);
+
+/*
+ * Device memory helpers for hosts without a GPU array package (the reference
+ * gets these from CUDA.jl).  kind: 0 host->device, 1 device->host,
+ * 2 device->device.
+ */
+int circatt_malloc(void **ptr, int64_t bytes);
+int circatt_free(void *ptr);
+int circatt_memcpy(void *dst, const void *src, int64_t bytes, int kind);
+int circatt_stream_synchronize(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CIRCATT_H */
