@@ -20,7 +20,8 @@ INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
-SOURCES = ["api.cpp", "unfused.hip", "fused.hip"]
+SOURCES = ["api.cpp", "unfused.hip", "fused.hip", "fused_fwd.hip", "fused_sim.hip",
+           "fused_bwdq.hip", "fused_bwdkv.hip"]
 FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -29,6 +30,9 @@ FLAGS = [
     "-Wall",
     # packed FP32 VALU ops are kept out of every code object
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the softmax rescale and the B-operand reuse
+    # of the accumulator then need no AGPR copies
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]

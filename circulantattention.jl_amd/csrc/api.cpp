@@ -9,7 +9,7 @@
 #include <cstdio>
 #include <string>
 
-#include "../../include/circatt.h"
+#include "circatt.h"
 #include "circatt_kernels.h"
 
 using namespace circatt;

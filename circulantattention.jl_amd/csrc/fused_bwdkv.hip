@@ -1,0 +1,10 @@
+// Instantiations of the windowed-tile kernels for MODE_BWDKV (fused_impl.h).
+#include "fused_impl.h"
+
+namespace circatt {
+
+hipError_t launch_fused_bwdkv(const FusedPlan &pl, int nsp, bool dist, hipStream_t s) {
+    return launch_mode_all<MODE_BWDKV>(pl, nsp, dist, s);
+}
+
+}  // namespace circatt

@@ -1,0 +1,10 @@
+// Instantiations of the windowed-tile kernels for MODE_FWD (fused_impl.h).
+#include "fused_impl.h"
+
+namespace circatt {
+
+hipError_t launch_fused_fwd(const FusedPlan &pl, int nsp, bool dist, hipStream_t s) {
+    return launch_mode_all<MODE_FWD>(pl, nsp, dist, s);
+}
+
+}  // namespace circatt
