@@ -1,5 +1,6 @@
 // Host planning and dispatch of the windowed-tile MFMA kernels (kernels in
 // fused_impl.h, one translation unit per mode in fused_<mode>.hip).
+#include "fused2d_impl.h"
 #include "fused_impl.h"
 
 namespace circatt {
@@ -76,7 +77,43 @@ bool fused_supported(FusedMode mode, const FusedProblem &pr) {
     return pl.ok;
 }
 
+// Compile-time-window 2D kernels (fused2d_impl.h) for the shapes they cover;
+// hipErrorNotSupported otherwise.
+hipError_t launch_f2d(FusedMode mode, const FusedProblem &pr, hipStream_t s) {
+    const int ncr = pr.dh * pr.ncomp;
+    if (mode == MODE_SIM || !f2d::supported(pr.g.nsp, pr.g.p, ncr)) return hipErrorNotSupported;
+    f2d::Args a{};
+    a.q = pr.q; a.k = pr.k; a.v = pr.v; a.y = pr.y; a.dy = pr.dy; a.lse = pr.lse;
+    a.yout = pr.yout; a.lse_out = pr.lse_out; a.dq = pr.dq; a.dk = pr.dk; a.dv = pr.dv;
+    a.dbuf = pr.dbuf;
+    a.n1 = pr.g.n1;
+    a.n2 = pr.g.n2;
+    a.P = pr.g.P;
+    a.unit_stride = pr.g.P * ncr;
+    a.scale = pr.scale;
+    a.c2 = pr.scale * kLog2e;
+    a.tiles_h = (pr.g.n1 + 7) / 8;
+    a.tiles_w = (pr.g.n2 + 7) / 8;
+    const int64_t nitems = (int64_t)a.tiles_h * a.tiles_w * pr.nunits;
+    if (nitems <= 0 || nitems > INT32_MAX / 2) return hipErrorNotSupported;
+    a.nitems = (int)nitems;
+    a.per_xcd = (int)((nitems + 7) / 8);
+    const int nt = ncr / 16;
+    const bool cplx = pr.ncomp == 2, dist = pr.kind == 1;
+    const int cus = device_cus();
+    switch (mode) {
+    case MODE_FWD: return launch_f2d_fwd(pr.g.p, nt, cplx, dist, a, cus, s);
+    case MODE_BWDQ: return launch_f2d_bwdq(pr.g.p, nt, cplx, dist, a, cus, s);
+    case MODE_BWDKV: return launch_f2d_bwdkv(pr.g.p, nt, cplx, dist, a, cus, s);
+    default: return hipErrorNotSupported;
+    }
+}
+
 hipError_t launch_fused(FusedMode mode, const FusedProblem &pr, hipStream_t s) {
+    if (mode != MODE_SIM && f2d::supported(pr.g.nsp, pr.g.p, pr.dh * pr.ncomp)) {
+        hipError_t e = launch_f2d(mode, pr, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     Plan pl = make_plan(mode, pr);
     if (!pl.ok) return hipErrorNotSupported;
     const bool dist = pr.kind == 1;

@@ -156,6 +156,14 @@ ATT_CASES = [
     ((36, 30), 11, 32, 2, 2, 1005),  # cfg5 geometry, reduced size
     ((70, 40), 31, 32, 1, 1, 1004),  # cfg4a geometry, reduced size
     ((300,), 63, 32, 2, 1, 1014),    # cfg4b geometry, reduced size
+    # compile-time-window 2D kernels (16 or 32 real components per head):
+    # partial tiles, halos that wrap more than once, ws > N
+    ((9, 7), 5, 16, 2, 1, 107),
+    ((5, 13), 3, 32, 1, 2, 108),
+    ((20, 11), 15, 16, 1, 1, 109),
+    ((8, 8), 15, 32, 1, 2, 110),
+    ((17, 26), 11, 64, 1, 4, 111),
+    ((24, 16), 7, 32, 2, 1, 112),
 ]
 
 
