@@ -81,23 +81,20 @@ bool fused_supported(FusedMode mode, const FusedProblem &pr) {
 // hipErrorNotSupported otherwise.
 hipError_t launch_f2d(FusedMode mode, const FusedProblem &pr, hipStream_t s) {
     const int ncr = pr.dh * pr.ncomp;
-    if (mode == MODE_SIM || !f2d::supported(pr.g.nsp, pr.g.p, ncr)) return hipErrorNotSupported;
+    if (mode == MODE_SIM || !f2d::supported(pr.g.nsp, pr.g.p, ncr, pr.g.P) ||
+        pr.nunits > INT32_MAX)
+        return hipErrorNotSupported;
     f2d::Args a{};
     a.q = pr.q; a.k = pr.k; a.v = pr.v; a.y = pr.y; a.dy = pr.dy; a.lse = pr.lse;
     a.yout = pr.yout; a.lse_out = pr.lse_out; a.dq = pr.dq; a.dk = pr.dk; a.dv = pr.dv;
     a.dbuf = pr.dbuf;
     a.n1 = pr.g.n1;
     a.n2 = pr.g.n2;
-    a.P = pr.g.P;
-    a.unit_stride = pr.g.P * ncr;
+    a.P = (int)pr.g.P;
+    a.unit_stride = (int)(pr.g.P * ncr);
     a.scale = pr.scale;
     a.c2 = pr.scale * kLog2e;
-    a.tiles_h = (pr.g.n1 + 7) / 8;
-    a.tiles_w = (pr.g.n2 + 7) / 8;
-    const int64_t nitems = (int64_t)a.tiles_h * a.tiles_w * pr.nunits;
-    if (nitems <= 0 || nitems > INT32_MAX / 2) return hipErrorNotSupported;
-    a.nitems = (int)nitems;
-    a.per_xcd = (int)((nitems + 7) / 8);
+    a.nunits = (int)pr.nunits;
     const int nt = ncr / 16;
     const bool cplx = pr.ncomp == 2, dist = pr.kind == 1;
     const int cus = device_cus();
@@ -110,7 +107,7 @@ hipError_t launch_f2d(FusedMode mode, const FusedProblem &pr, hipStream_t s) {
 }
 
 hipError_t launch_fused(FusedMode mode, const FusedProblem &pr, hipStream_t s) {
-    if (mode != MODE_SIM && f2d::supported(pr.g.nsp, pr.g.p, pr.dh * pr.ncomp)) {
+    if (mode != MODE_SIM) {
         hipError_t e = launch_f2d(mode, pr, s);
         if (e != hipErrorNotSupported) return e;
     }

@@ -18,19 +18,26 @@
 //     as its initial accumulator (the -lse row term of the backward, the -D
 //     term of dP - D, the Distance key bias), so P = exp2(acc) and
 //     dS = P * acc2 cost one exp and one multiply per value;
-//   * the forward keeps all scores of its 16 queries in registers (22 blocks
-//     x 4 values at ws = 15), takes the exact row maximum, and never rescales.
+//   * the forward keeps the scores of its 16 queries in registers, one or two
+//     chunks of blocks at a time, and takes each chunk's exact maximum (one
+//     rescale between the two chunks);
+//   * global loads are buffer loads whose channel stride is a scalar offset,
+//     so staging a pixel costs no vector address arithmetic.
 //
-// Work decomposition (as in fused_impl.h): persistent workgroups of four
-// wavefronts walk XCD-contiguous runs of (8x8 tile, unit) items; the
-// circularly wrapped halo of the other side is staged in LDS with the next
-// item's global loads issued into registers before the current item is
-// computed.  Wavefront w holds the 8 (dim 1) x 2 (dim 2) register pixels at
-// tile columns 2w, 2w+1 (lane j -> (j % 8, j / 8)) and walks the 2 x 8 LDS
-// blocks covering their windows (element e -> (e % 2, e / 2)).
+// Work decomposition (as in fused_impl.h): persistent workgroups walk
+// XCD-contiguous runs of (tile, unit) items; the circularly wrapped halo of
+// the other side is staged in LDS, with the next item's global loads issued
+// into registers before the current item is computed.  A workgroup is a
+// WH x WW grid of wavefronts over a (8 WH) x (2 WW) tile; wavefront (wh, ww)
+// holds the 8 (dim 1) x 2 (dim 2) register pixels at tile rows 8 wh ..
+// 8 wh + 7, columns 2 ww, 2 ww + 1 (lane j -> (j % 8, j / 8)) and walks the
+// 2 x 8 LDS blocks covering their windows (element e -> (e % 2, e / 2)).
+// The wave grid is the largest of 2x8, 1x8 and 1x4 whose halo fits LDS
+// (2x8, four waves per SIMD, for 16 components per pixel).
 #pragma once
 #include <stdint.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "circatt_common.h"
@@ -46,48 +53,84 @@ typedef float f2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr size_t kLdsCap = 160 * 1024;
+constexpr unsigned kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data
 
 __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// compile-time loop: f(std::integral_constant<int, I>) for I in [0, N)
-template <int I, int N>
+// compile-time loop: f(std::integral_constant<int, I>) for I in [B, E)
+template <int I, int E>
 struct SFor {
     template <typename F>
     __device__ __forceinline__ static void run(F &f) {
         f(std::integral_constant<int, I>{});
-        SFor<I + 1, N>::run(f);
+        SFor<I + 1, E>::run(f);
     }
 };
-template <int N>
-struct SFor<N, N> {
+template <int E>
+struct SFor<E, E> {
     template <typename F>
     __device__ __forceinline__ static void run(F &) {}
 };
-template <int N, typename F>
+template <int B, int E, typename F>
 __device__ __forceinline__ void static_for(F &&f) {
-    SFor<0, N>::run(f);
+    SFor<B, E>::run(f);
 }
 
-// Geometry of one (P, NT) instantiation.
-template <int P_, int NT_>
+// Geometry of a (P, NT) window on a WH x WW wave grid.
+template <int P_, int NT_, int WH_, int WW_>
 struct Geo {
     static constexpr int P = P_;
     static constexpr int NT = NT_;          // 16-component tiles per pixel
+    static constexpr int WH = WH_, WW = WW_;
+    static constexpr int THREADS = 64 * WH * WW;
     static constexpr int NC = 16 * NT;      // real components per pixel
     static constexpr int NS = 4 * NT;       // MFMA k-steps per product
     static constexpr int PS = NC + 4;       // LDS floats per staged pixel
-    static constexpr int TH = 8, TW = 8;    // register tile of a workgroup
-    static constexpr int NKH = 4 + P;       // 2-row LDS blocks along dim 1
-    static constexpr int NKW = (2 + 2 * P + 7) / 8;  // 8-column LDS blocks along dim 2
+    static constexpr int TH = 8 * WH, TW = 2 * WW;   // register tile of a workgroup
+    static constexpr int NKH = 4 + P;       // 2-row LDS blocks per wave along dim 1
+    static constexpr int NKW = (2 + 2 * P + 7) / 8;  // 8-column LDS blocks per wave along dim 2
     static constexpr int NBLK = NKH * NKW;
-    static constexpr int HH = 2 * NKH;      // staged rows (= TH + 2P)
-    static constexpr int HWD = 6 + 8 * NKW; // staged columns (>= TW + 2P)
+    static constexpr int HH = TH + 2 * P;   // staged rows
+    static constexpr int HWD = 2 * (WW - 1) + 8 * NKW;  // staged columns (>= TW + 2P)
     static constexpr int CR = HH + ((2 - HH % 4) + 4) % 4;  // LDS column stride, 2 mod 4
     static constexpr int NPX = HH * HWD;    // staged pixels
     static constexpr int LPX = CR * HWD;    // LDS pixel slots per tensor
-    static constexpr int PPT = (NPX + 255) / 256;  // staged pixels per thread
+    static constexpr int PPT = (NPX + THREADS - 1) / THREADS;  // staged pixels per thread
+};
+
+enum { FWD = 0, BWDQ = 1, BWDKV = 2 };
+
+template <int MODE, bool DIST>
+struct ModeCfg {
+    static constexpr int NSCAL = MODE == BWDKV ? 2 : (DIST ? 1 : 0);  // staged scalars
+};
+
+template <int P, int NT, int WH, int WW, bool DIST, int MODE>
+constexpr size_t lds_bytes() {
+    using G = Geo<P, NT, WH, WW>;
+    return (size_t)(2 * G::LPX * G::PS + ModeCfg<MODE, DIST>::NSCAL * G::LPX) * 4;
+}
+
+#ifndef CIRCATT_F2D_NCH
+#define CIRCATT_F2D_NCH 3
+#endif
+#ifndef CIRCATT_F2D_BIG_WW
+#define CIRCATT_F2D_BIG_WW 8
+#endif
+// Wave grid of an instantiation: 2xBIG, else 1x8, else 1x4 (the first whose LDS fits).
+template <int P, int NT, bool DIST, int MODE>
+struct Grid {
+    static constexpr int BW = CIRCATT_F2D_BIG_WW;
+    static constexpr bool big = lds_bytes<P, NT, 2, BW, DIST, MODE>() <= kLdsCap;
+    static constexpr bool mid = lds_bytes<P, NT, 1, 8, DIST, MODE>() <= kLdsCap;
+    static constexpr int WH = big ? 2 : 1;
+    static constexpr int WW = big ? BW : mid ? 8 : 4;
+    static constexpr size_t bytes = lds_bytes<P, NT, WH, WW, DIST, MODE>();
+    static constexpr int THREADS = 64 * WH * WW;
+    static constexpr int MINWG = bytes <= 80 * 1024 ? 2 : 1;
 };
 
 // Lane mask of valid (query, key) pairs for element r of block (bi, bj):
@@ -119,6 +162,17 @@ __device__ __forceinline__ float mask_sel(float v, float alt) {
     }
 }
 
+// Scheduling fence between the blocks of a walk: keeps the compiler from
+// hoisting later blocks' LDS reads (and their registers) into earlier blocks.
+#ifndef CIRCATT_F2D_FENCE
+#define CIRCATT_F2D_FENCE 1
+#endif
+#if CIRCATT_F2D_FENCE
+#define BLOCK_FENCE() __builtin_amdgcn_sched_barrier(0)
+#else
+#define BLOCK_FENCE() ((void)0)
+#endif
+
 // Sum / max over the four lane groups holding the same register pixel
 // (lanes j, j^16, j^32, j^48).
 __device__ __forceinline__ float gsum(float v) {
@@ -142,15 +196,27 @@ struct Args {
     const float *q, *k, *v, *y, *dy, *lse;
     float *yout, *lse_out, *dq, *dk, *dv, *dbuf;
     int n1, n2;
-    int64_t P;            // pixels per image
-    int64_t unit_stride;  // floats per (head, batch) unit = P * NC
+    int P;                // pixels per image
+    int unit_stride;      // floats per (head, batch) unit = P * NC
     float scale, c2;      // similarity scale, scale * log2(e)
-    int tiles_h, tiles_w, nitems, per_xcd;
+    int nunits;           // (head, batch) units
+    int tiles_h, tiles_w, nitems, per_xcd;  // set by launch()
 };
 
-// Real component `comp` of pixel `pix` in a unit of NC components.
+// Buffer resource over `bytes` bytes at p (loads beyond it return 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const float *p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), (short)0, bytes, kRsrcWord3);
+}
+__device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ f2 bload2(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(f2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+
+// Real component `comp` of pixel `pix` in a unit (float index).
 template <bool CPLX>
-__device__ __forceinline__ int64_t comp_off(int64_t P, int64_t pix, int comp) {
+__device__ __forceinline__ int comp_off(int P, int pix, int comp) {
     if constexpr (CPLX) return 2 * (pix + P * (comp >> 1)) + (comp & 1);
     return pix + P * comp;
 }
@@ -163,50 +229,58 @@ __device__ __forceinline__ int item_of(const Args &a, int k) {
     return it < min(a.nitems, (xcd + 1) * a.per_xcd) ? it : a.nitems;
 }
 
-enum { FWD = 0, BWDQ = 1, BWDKV = 2 };
-
-template <int MODE, bool DIST>
-struct ModeCfg {
-    static constexpr int NTEN = 2;                                       // staged tensors
-    static constexpr int NSCAL = MODE == BWDKV ? 2 : (DIST ? 1 : 0);     // staged scalars
-};
-
 template <int P, int NT, bool CPLX, bool DIST, int MODE>
-struct LdsSize {
-    using G = Geo<P, NT>;
-    using M = ModeCfg<MODE, DIST>;
-    static constexpr int floats = M::NTEN * G::LPX * G::PS + M::NSCAL * G::LPX;
-    static constexpr size_t bytes = (size_t)floats * 4;
-};
-
-template <int P, int NT, bool CPLX, bool DIST, int MODE>
-__global__ __launch_bounds__(256, (LdsSize<P, NT, CPLX, DIST, MODE>::bytes <= 80 * 1024) ? 2 : 1)
+__global__ __launch_bounds__((Grid<P, NT, DIST, MODE>::THREADS), (Grid<P, NT, DIST, MODE>::MINWG))
 void kernel2d(Args a) {
-    using G = Geo<P, NT>;
-    using M = ModeCfg<MODE, DIST>;
+    constexpr int WH = Grid<P, NT, DIST, MODE>::WH, WW = Grid<P, NT, DIST, MODE>::WW;
+    using G = Geo<P, NT, WH, WW>;
     constexpr int NC = G::NC, NS = G::NS, PS = G::PS, CR = G::CR, HH = G::HH, NKW = G::NKW;
     constexpr int NBLK = G::NBLK, PPT = G::PPT, NPX = G::NPX, LPX = G::LPX;
-    constexpr int NTEN = M::NTEN, NSCAL = M::NSCAL;
+    constexpr int THREADS = G::THREADS;
+    // forward: chunks of blocks whose scores are held in registers at once
+    // (three when the wave grid leaves <= 128 VGPRs per lane)
+    constexpr int NCH = MODE != FWD ? 1 : (THREADS >= 768 && NBLK > 12) ? CIRCATT_F2D_NCH : (NBLK > 12 ? 2 : 1);
+    constexpr int CHB = (NBLK + NCH - 1) / NCH;
+    // block at which the next item's loads are issued: the start of the
+    // forward's last chunk, the middle of the backward walks
+    constexpr int PFB = MODE == FWD ? (NCH - 1) * CHB : NBLK / 2;
     // LDS layout (floats): tensor 0, tensor 1 ([slot][PS]), then scalars ([slot])
     constexpr int OT1 = LPX * PS;
-    constexpr int OS0 = NTEN * LPX * PS;
+    constexpr int OS0 = 2 * LPX * PS;
     constexpr int OS1 = OS0 + LPX;
     float *const lds = circatt_lds2;
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int wh = wv % WH, ww = wv / WH;
     const int j = lane & 15, g = lane >> 4;
     const int jh = j & 7, jw = j >> 3;
 
     // lane bases (LDS pixel slots): block (bi, bj) of this wave starts at
-    // slot 2 bi + CR (2 wv + 8 bj); element e sits (e % 2) + CR (e / 2) further
-    const int slotA = (j & 1) + CR * (2 * wv + (j >> 1));  // element j (A rows of products 1)
-    const int slotE = CR * (2 * wv + 2 * g);               // element 4g (r = 0)
+    // slot 8 wh + 2 bi + CR (2 ww + 8 bj); element e sits (e % 2) + CR (e / 2)
+    // further
+    const int slotA = 8 * wh + (j & 1) + CR * (2 * ww + (j >> 1));  // element j
+    const int slotE = 8 * wh + CR * (2 * ww + 2 * g);               // element 4g
     const int baseA = slotA * PS + 4 * g;
     const int baseT = slotE * PS + j;
+    // Per-lane region bases, hidden from constant folding so that every
+    // block offset stays a ds_read immediate (the regions lie up to 150 KB
+    // apart, beyond the 64 KB immediate range).
+    auto opaque = [](int v) {
+        asm volatile("" : "+v"(v));
+        return v;
+    };
+    const float *const pA0 = lds + opaque(baseA);            // product-1 rows, tensor 0
+    const float *const pA1 = lds + opaque(OT1 + baseA);      // product-1 rows, tensor 1
+    const float *const pT0 = lds + opaque(baseT);            // product-2 rows, tensor 0
+    const float *const pT1 = lds + opaque(OT1 + baseT);      // product-2 rows, tensor 1
+    const float *const pS0 = lds + opaque(OS0 + slotE);      // scalars 0 of element 4g
+    const float *const pS1 = lds + opaque(OS1 + slotE);      // scalars 1 of element 4g
+
+    const int ubytes = a.unit_stride * 4;
 
     // ---- prefetch registers ----
-    float hv[PPT][NTEN][NC];
-    float hs[PPT][NSCAL > 0 ? NSCAL : 1];
+    float hv[PPT][2][NC];
+    float hs[PPT][2];
     int hslot[PPT];
     float nr0[NS], nr1[NS], nry[NS];
     float nlse = 0.f;
@@ -220,43 +294,55 @@ void kernel2d(Args a) {
         w0 = (tile - th) / a.tiles_h * G::TW;
     };
 
+    const bool big = a.n1 >= HH && a.n2 >= G::HWD;
     auto load_stage = [&](int item) {
         int unit, h0, w0;
         decode(item, unit, h0, w0);
+        const int hs0 = pmod(h0 - P, a.n1), ws0 = pmod(w0 - P, a.n2);  // uniform
         const int64_t uoff = (int64_t)unit * a.unit_stride;
-        const float *src0 = (MODE == BWDKV ? a.q : a.k) + uoff;
-        const float *src1 = (MODE == BWDKV ? a.dy : a.v) + uoff;
+        const auto r0 = rsrc((MODE == BWDKV ? a.q : a.k) + uoff, ubytes);
+        const auto r1 = rsrc((MODE == BWDKV ? a.dy : a.v) + uoff, ubytes);
 #pragma unroll
         for (int pp = 0; pp < PPT; ++pp) {
-            const int px0 = threadIdx.x + 256 * pp;
+            const int px0 = threadIdx.x + THREADS * pp;
             const bool pv = px0 < NPX;
             const int px = pv ? px0 : 0;
             const int kw = px / HH, kh = px - kw * HH;
             hslot[pp] = pv ? kh + CR * kw : -1;
-            const int64_t gp = pmod(h0 - P + kh, a.n1) + (int64_t)a.n1 * pmod(w0 - P + kw, a.n2);
+            // wrapped halo position; one conditional subtraction when the
+            // image is at least as large as the halo, a modulo otherwise
+            int gh = hs0 + kh, gw = ws0 + kw;
+            if (big) {
+                gh -= gh >= a.n1 ? a.n1 : 0;
+                gw -= gw >= a.n2 ? a.n2 : 0;
+            } else {
+                gh %= a.n1;
+                gw %= a.n2;
+            }
+            const int gp = gh + a.n1 * gw;
             if constexpr (CPLX) {
-                const float2 *s0 = reinterpret_cast<const float2 *>(src0) + gp;
-                const float2 *s1 = reinterpret_cast<const float2 *>(src1) + gp;
 #pragma unroll
                 for (int c = 0; c < NC / 2; ++c) {
-                    const float2 x0 = s0[(int64_t)c * a.P];
-                    const float2 x1 = s1[(int64_t)c * a.P];
-                    hv[pp][0][2 * c] = x0.x;
-                    hv[pp][0][2 * c + 1] = x0.y;
-                    hv[pp][1][2 * c] = x1.x;
-                    hv[pp][1][2 * c + 1] = x1.y;
+                    const f2 x0 = bload2(r0, gp * 8, c * a.P * 8);
+                    const f2 x1 = bload2(r1, gp * 8, c * a.P * 8);
+                    hv[pp][0][2 * c] = x0[0];
+                    hv[pp][0][2 * c + 1] = x0[1];
+                    hv[pp][1][2 * c] = x1[0];
+                    hv[pp][1][2 * c + 1] = x1[1];
                 }
             } else {
 #pragma unroll
                 for (int c = 0; c < NC; ++c) {
-                    hv[pp][0][c] = src0[gp + (int64_t)c * a.P];
-                    hv[pp][1][c] = src1[gp + (int64_t)c * a.P];
+                    hv[pp][0][c] = bload(r0, gp * 4, c * a.P * 4);
+                    hv[pp][1][c] = bload(r1, gp * 4, c * a.P * 4);
                 }
             }
             if constexpr (MODE == BWDKV) {
                 const int64_t soff = (int64_t)unit * a.P;
-                hs[pp][0] = a.lse[soff + gp];
-                hs[pp][1] = a.dbuf[soff + gp];
+                const auto rl = rsrc(a.lse + soff, a.P * 4);
+                const auto rd = rsrc(a.dbuf + soff, a.P * 4);
+                hs[pp][0] = bload(rl, gp * 4, 0);
+                hs[pp][1] = bload(rd, gp * 4, 0);
             }
         }
     };
@@ -264,21 +350,24 @@ void kernel2d(Args a) {
     auto load_regs = [&](int item) {
         int unit, h0, w0;
         decode(item, unit, h0, w0);
-        const int rh = h0 + jh, rw = w0 + 2 * wv + jw;
+        const int rh = h0 + 8 * wh + jh, rw = w0 + 2 * ww + jw;
         const bool rvalid = rh < a.n1 && rw < a.n2;
-        const int64_t rpix = rvalid ? (int64_t)rh + (int64_t)a.n1 * rw : 0;
+        const int rpix = rvalid ? rh + a.n1 * rw : 0;
         const int64_t uoff = (int64_t)unit * a.unit_stride;
-        const float *b0 = (MODE == BWDKV ? a.k : a.q) + uoff;
-        const float *b1 = (MODE == BWDKV ? a.v : a.dy) + uoff;
+        const auto r0 = rsrc((MODE == BWDKV ? a.k : a.q) + uoff, ubytes);
+        const auto r1 = rsrc((MODE == BWDKV ? a.v : a.dy) + uoff, ubytes);
+        // component 16 t + 4 g + c of the lane's pixel: lane part 4 g,
+        // scalar part 16 t + c
+        const int vo = comp_off<CPLX>(a.P, rpix, 4 * g) * 4;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            const int comp = 16 * (s >> 2) + 4 * g + (s & 3);
-            const int64_t o = comp_off<CPLX>(a.P, rpix, comp);
-            nr0[s] = b0[o];
-            if constexpr (MODE != FWD) nr1[s] = b1[o];
-            if constexpr (MODE == BWDQ) nry[s] = a.y[uoff + o];
+            const int sc = 16 * (s >> 2) + (s & 3);
+            const int so = (CPLX ? 2 * a.P * (sc >> 1) + (sc & 1) : a.P * sc) * 4;
+            nr0[s] = bload(r0, vo, so);
+            if constexpr (MODE != FWD) nr1[s] = bload(r1, vo, so);
+            if constexpr (MODE == BWDQ) nry[s] = bload(rsrc(a.y + uoff, ubytes), vo, so);
         }
-        if constexpr (MODE == BWDQ) nlse = a.lse[(int64_t)unit * a.P + rpix];
+        if constexpr (MODE == BWDQ) nlse = bload(rsrc(a.lse + (int64_t)unit * a.P, a.P * 4), rpix * 4, 0);
     };
 
     int k = 0;
@@ -290,9 +379,9 @@ void kernel2d(Args a) {
     while (true) {
         int unit, h0, w0;
         decode(item, unit, h0, w0);
-        const int rh = h0 + jh, rw = w0 + 2 * wv + jw;
+        const int rh = h0 + 8 * wh + jh, rw = w0 + 2 * ww + jw;
         const bool rvalid = rh < a.n1 && rw < a.n2;
-        const int64_t rpix = rvalid ? (int64_t)rh + (int64_t)a.n1 * rw : 0;
+        const int rpix = rvalid ? rh + a.n1 * rw : 0;
         const int64_t uoff = (int64_t)unit * a.unit_stride;
         const int64_t soff = (int64_t)unit * a.P;
         const float c2 = a.c2;
@@ -329,7 +418,7 @@ void kernel2d(Args a) {
         float raw2 = 0.f;  // |x|^2 of the (unscaled) register pixel
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            raw2 += nr0[s] * nr0[s];
+            if constexpr (DIST) raw2 += nr0[s] * nr0[s];
             reg0[s] = nr0[s] * c2;
             if constexpr (MODE != FWD) reg1[s] = nr1[s];
         }
@@ -344,74 +433,100 @@ void kernel2d(Args a) {
         const float sq = DIST ? gsum(raw2) : 0.f;
         __syncthreads();  // halo staged
 
-        // ---- issue the next item's global loads ----
+        // The next item's global loads are issued part-way through this
+        // item's block walk (at block PFB), which keeps their destination
+        // registers out of the first blocks' register budget.
         const int nitem = item_of(a, k + 1);
         const bool has_next = nitem < a.nitems;
-        if (has_next) {
-            load_stage(nitem);
-            load_regs(nitem);
-        }
+        auto prefetch = [&]() {
+            if (has_next) {
+                load_stage(nitem);
+                load_regs(nitem);
+            }
+        };
 
         if constexpr (MODE == FWD) {
-            // scores of all blocks: S[b][r] = c2 q.k (+ Distance key bias)
-            f4 S[NBLK];
-            static_for<NBLK>([&](auto B) {
-                constexpr int b = decltype(B)::value;
-                constexpr int bi = b / NKW, bj = b % NKW;
-                constexpr int boff = 2 * bi + CR * 8 * bj;  // block slot offset
-                f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-                if constexpr (DIST) {
-                    const f2 lo = *reinterpret_cast<const f2 *>(&lds[OS0 + slotE + boff]);
-                    const f2 hi = *reinterpret_cast<const f2 *>(&lds[OS0 + slotE + boff + CR]);
-                    acc = f4{lo[0], lo[1], hi[0], hi[1]};
-                }
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const f4 x = *reinterpret_cast<const f4 *>(&lds[baseA + boff * PS + 16 * t]);
-                    acc = mfma(x[0], reg0[4 * t + 0], acc);
-                    acc = mfma(x[1], reg0[4 * t + 1], acc);
-                    acc = mfma(x[2], reg0[4 * t + 2], acc);
-                    acc = mfma(x[3], reg0[4 * t + 3], acc);
-                }
-                S[b] = acc;
-            });
-            // window mask and exact row maximum
-            float mx = -INFINITY;
-            static_for<NBLK>([&](auto B) {
-                constexpr int b = decltype(B)::value;
-                constexpr int bi = b / NKW, bj = b % NKW;
-                S[b][0] = mask_sel<lane_mask(P, bi, bj, 0)>(S[b][0], -INFINITY);
-                S[b][1] = mask_sel<lane_mask(P, bi, bj, 1)>(S[b][1], -INFINITY);
-                S[b][2] = mask_sel<lane_mask(P, bi, bj, 2)>(S[b][2], -INFINITY);
-                S[b][3] = mask_sel<lane_mask(P, bi, bj, 3)>(S[b][3], -INFINITY);
-                mx = fmaxf(mx, fmaxf(fmaxf(S[b][0], S[b][1]), fmaxf(S[b][2], S[b][3])));
-            });
-            const float m = gmax(mx);
-            float lsum = 0.f;
+            // running maximum starts finite: a chunk may hold no valid key of
+            // a query (then its scores are all -inf and exp2 gives 0, not NaN)
+            float m = -1e30f, lsum = 0.f;
             f4 acc[2][NT];
 #pragma unroll
             for (int u = 0; u < 2; ++u)
 #pragma unroll
                 for (int t = 0; t < NT; ++t) acc[u][t] = f4{0.f, 0.f, 0.f, 0.f};
-            static_for<NBLK>([&](auto B) {
-                constexpr int b = decltype(B)::value;
-                constexpr int bi = b / NKW, bj = b % NKW;
-                constexpr int boff = 2 * bi + CR * 8 * bj;
-                float p[4];
+            auto chunk = [&](auto CH) {
+                constexpr int ci = decltype(CH)::value;
+                constexpr int cb = ci * CHB;
+                constexpr int ce = cb + CHB < NBLK ? cb + CHB : NBLK;
+                if constexpr (cb == PFB) prefetch();
+                // scores of the chunk: S[b][r] = c2 q.k (+ Distance key bias)
+                f4 S[CHB];
+                static_for<cb, ce>([&](auto B) {
+                    constexpr int b = decltype(B)::value;
+                    constexpr int bi = b / NKW, bj = b % NKW;
+                    constexpr int boff = 2 * bi + CR * 8 * bj;  // block slot offset
+                    BLOCK_FENCE();
+                    f4 acc0 = f4{0.f, 0.f, 0.f, 0.f};
+                    if constexpr (DIST) {
+                        const f2 lo = *reinterpret_cast<const f2 *>(&pS0[boff]);
+                        const f2 hi = *reinterpret_cast<const f2 *>(&pS0[boff + CR]);
+                        acc0 = f4{lo[0], lo[1], hi[0], hi[1]};
+                    }
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    p[r] = __builtin_amdgcn_exp2f(S[b][r] - m);
-                    lsum += p[r];
+                    for (int t = 0; t < NT; ++t) {
+                        const f4 x = *reinterpret_cast<const f4 *>(&pA0[boff * PS + 16 * t]);
+                        acc0 = mfma(x[0], reg0[4 * t + 0], acc0);
+                        acc0 = mfma(x[1], reg0[4 * t + 1], acc0);
+                        acc0 = mfma(x[2], reg0[4 * t + 2], acc0);
+                        acc0 = mfma(x[3], reg0[4 * t + 3], acc0);
+                    }
+                    S[b - cb] = acc0;
+                });
+                // window mask and the chunk's exact row maximum
+                float mx = m;
+                static_for<cb, ce>([&](auto B) {
+                    constexpr int b = decltype(B)::value;
+                    constexpr int bi = b / NKW, bj = b % NKW;
+                    f4 &s = S[b - cb];
+                    s[0] = mask_sel<lane_mask(P, bi, bj, 0)>(s[0], -INFINITY);
+                    s[1] = mask_sel<lane_mask(P, bi, bj, 1)>(s[1], -INFINITY);
+                    s[2] = mask_sel<lane_mask(P, bi, bj, 2)>(s[2], -INFINITY);
+                    s[3] = mask_sel<lane_mask(P, bi, bj, 3)>(s[3], -INFINITY);
+                    mx = fmaxf(fmaxf(mx, s[0]), s[1]);
+                    mx = fmaxf(fmaxf(mx, s[2]), s[3]);
+                });
+                const float mn = gmax(mx);
+                if constexpr (ci > 0) {
+                    const float alpha = __builtin_amdgcn_exp2f(m - mn);
+                    lsum *= alpha;
+#pragma unroll
+                    for (int u = 0; u < 2; ++u)
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) acc[u][t] *= alpha;
                 }
+                m = mn;
+                static_for<cb, ce>([&](auto B) {
+                    constexpr int b = decltype(B)::value;
+                    constexpr int bi = b / NKW, bj = b % NKW;
+                    constexpr int boff = 2 * bi + CR * 8 * bj;
+                    BLOCK_FENCE();
+                    float p[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int roff = ((r & 1) + CR * (r >> 1)) * PS;
+                    for (int r = 0; r < 4; ++r) {
+                        p[r] = __builtin_amdgcn_exp2f(S[b - cb][r] - m);
+                        lsum += p[r];
+                    }
 #pragma unroll
-                    for (int t = 0; t < NT; ++t)
-                        acc[b & 1][t] = mfma(lds[OT1 + baseT + boff * PS + roff + 16 * t], p[r],
-                                             acc[b & 1][t]);
-                }
-            });
+                    for (int r = 0; r < 4; ++r) {
+                        const int roff = ((r & 1) + CR * (r >> 1)) * PS;
+#pragma unroll
+                        for (int t = 0; t < NT; ++t)
+                            acc[b & 1][t] = mfma(pT1[boff * PS + roff + 16 * t],
+                                                 p[r], acc[b & 1][t]);
+                    }
+                });
+            };
+            static_for<0, NCH>(chunk);
             const float l = gsum(lsum);
             const float inv = 1.f / l;
             if (rvalid) {
@@ -437,21 +552,23 @@ void kernel2d(Args a) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) acc[u][t] = f4{0.f, 0.f, 0.f, 0.f};
             float corr = 0.f;
-            static_for<NBLK>([&](auto B) {
+            static_for<0, NBLK>([&](auto B) {
                 constexpr int b = decltype(B)::value;
                 constexpr int bi = b / NKW, bj = b % NKW;
                 constexpr int boff = 2 * bi + CR * 8 * bj;
+                BLOCK_FENCE();
+                if constexpr (b == PFB) prefetch();
                 f4 s = cS, dp = cD;
                 if constexpr (DIST) {
-                    const f2 lo = *reinterpret_cast<const f2 *>(&lds[OS0 + slotE + boff]);
-                    const f2 hi = *reinterpret_cast<const f2 *>(&lds[OS0 + slotE + boff + CR]);
+                    const f2 lo = *reinterpret_cast<const f2 *>(&pS0[boff]);
+                    const f2 hi = *reinterpret_cast<const f2 *>(&pS0[boff + CR]);
                     s = s + f4{lo[0], lo[1], hi[0], hi[1]};
                 }
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    const f4 x = *reinterpret_cast<const f4 *>(&lds[baseA + boff * PS + 16 * t]);
+                    const f4 x = *reinterpret_cast<const f4 *>(&pA0[boff * PS + 16 * t]);
                     const f4 w =
-                        *reinterpret_cast<const f4 *>(&lds[OT1 + baseA + boff * PS + 16 * t]);
+                        *reinterpret_cast<const f4 *>(&pA1[boff * PS + 16 * t]);
                     s = mfma(x[0], reg0[4 * t + 0], s);
                     dp = mfma(w[0], reg1[4 * t + 0], dp);
                     s = mfma(x[1], reg0[4 * t + 1], s);
@@ -473,7 +590,7 @@ void kernel2d(Args a) {
 #pragma unroll
                     for (int t = 0; t < NT; ++t)
                         acc[b & 1][t] =
-                            mfma(lds[baseT + boff * PS + roff + 16 * t], ds[r], acc[b & 1][t]);
+                            mfma(pT0[boff * PS + roff + 16 * t], ds[r], acc[b & 1][t]);
                 }
             });
             const float rs = DIST ? gsum(corr) : 0.f;
@@ -501,22 +618,24 @@ void kernel2d(Args a) {
                     acck[u][t] = f4{0.f, 0.f, 0.f, 0.f};
                 }
             float corr = 0.f;
-            static_for<NBLK>([&](auto B) {
+            static_for<0, NBLK>([&](auto B) {
                 constexpr int b = decltype(B)::value;
                 constexpr int bi = b / NKW, bj = b % NKW;
                 constexpr int boff = 2 * bi + CR * 8 * bj;
-                const f2 alo = *reinterpret_cast<const f2 *>(&lds[OS0 + slotE + boff]);
-                const f2 ahi = *reinterpret_cast<const f2 *>(&lds[OS0 + slotE + boff + CR]);
-                const f2 dlo = *reinterpret_cast<const f2 *>(&lds[OS1 + slotE + boff]);
-                const f2 dhi = *reinterpret_cast<const f2 *>(&lds[OS1 + slotE + boff + CR]);
+                BLOCK_FENCE();
+                if constexpr (b == PFB) prefetch();
+                const f2 alo = *reinterpret_cast<const f2 *>(&pS0[boff]);
+                const f2 ahi = *reinterpret_cast<const f2 *>(&pS0[boff + CR]);
+                const f2 dlo = *reinterpret_cast<const f2 *>(&pS1[boff]);
+                const f2 dhi = *reinterpret_cast<const f2 *>(&pS1[boff + CR]);
                 f4 s = f4{alo[0], alo[1], ahi[0], ahi[1]};
                 if constexpr (DIST) s = s + f4{kb, kb, kb, kb};
                 f4 dp = f4{dlo[0], dlo[1], dhi[0], dhi[1]};
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    const f4 x = *reinterpret_cast<const f4 *>(&lds[baseA + boff * PS + 16 * t]);
+                    const f4 x = *reinterpret_cast<const f4 *>(&pA0[boff * PS + 16 * t]);
                     const f4 w =
-                        *reinterpret_cast<const f4 *>(&lds[OT1 + baseA + boff * PS + 16 * t]);
+                        *reinterpret_cast<const f4 *>(&pA1[boff * PS + 16 * t]);
                     s = mfma(x[0], reg0[4 * t + 0], s);
                     dp = mfma(w[0], reg1[4 * t + 0], dp);
                     s = mfma(x[1], reg0[4 * t + 1], s);
@@ -539,10 +658,10 @@ void kernel2d(Args a) {
                     const int roff = ((r & 1) + CR * (r >> 1)) * PS;
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
-                        accv[b & 1][t] = mfma(lds[OT1 + baseT + boff * PS + roff + 16 * t], p[r],
+                        accv[b & 1][t] = mfma(pT1[boff * PS + roff + 16 * t], p[r],
                                               accv[b & 1][t]);
                         acck[b & 1][t] =
-                            mfma(lds[baseT + boff * PS + roff + 16 * t], ds[r], acck[b & 1][t]);
+                            mfma(pT0[boff * PS + roff + 16 * t], ds[r], acck[b & 1][t]);
                     }
                 }
             });
@@ -555,7 +674,7 @@ void kernel2d(Args a) {
                 for (int t = 0; t < NT; ++t)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int64_t o = comp_off<CPLX>(a.P, rpix, 16 * t + 4 * g + r);
+                        const int o = comp_off<CPLX>(a.P, rpix, 16 * t + 4 * g + r);
                         vb[o] = accv[0][t][r] + accv[1][t][r];
                         float val = acck[0][t][r] + acck[1][t][r];
                         if constexpr (DIST) val -= cs * reg0[4 * t + r] * invc2;
@@ -575,22 +694,29 @@ void kernel2d(Args a) {
 // ---------------------------------------------------------------------------
 template <int P, int NT, bool CPLX, bool DIST, int MODE>
 hipError_t launch(const Args &a0, int cus, hipStream_t s) {
-    using LS = LdsSize<P, NT, CPLX, DIST, MODE>;
+    using GR = Grid<P, NT, DIST, MODE>;
+    using G = Geo<P, NT, GR::WH, GR::WW>;
+    static_assert(GR::bytes <= kLdsCap, "halo does not fit LDS");
     auto kern = kernel2d<P, NT, CPLX, DIST, MODE>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)LS::bytes);
+                                           (int)GR::bytes);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
     Args a = a0;
-    const int wg_per_cu = LS::bytes <= 80 * 1024 ? 2 : 1;
-    int64_t grid = (int64_t)cus * wg_per_cu;
+    a.tiles_h = (a.n1 + G::TH - 1) / G::TH;
+    a.tiles_w = (a.n2 + G::TW - 1) / G::TW;
+    const int64_t nitems = (int64_t)a.tiles_h * a.tiles_w * a.nunits;
+    if (nitems <= 0 || nitems > INT32_MAX / 2) return hipErrorNotSupported;
+    a.nitems = (int)nitems;
+    a.per_xcd = (int)((nitems + 7) / 8);
+    int64_t grid = (int64_t)cus * GR::MINWG;
     grid = std::min<int64_t>(grid, 8LL * a.per_xcd);
     grid = std::max<int64_t>(8, grid / 8 * 8);
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), LS::bytes, s, a);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(G::THREADS), GR::bytes, s, a);
     return hipGetLastError();
 }
 
@@ -621,8 +747,11 @@ hipError_t dispatch(int p, int nt, bool cplx, bool dist, const Args &a, int cus,
     return hipErrorNotSupported;
 }
 
-inline bool supported(int nsp, int p, int ncr) {
-    return nsp == 2 && (p == 1 || p == 2 || p == 3 || p == 5 || p == 7) && (ncr == 16 || ncr == 32);
+// Shapes the compile-time-window kernels cover.  Offsets are 32-bit: a unit
+// of P * 16 NT floats must stay below 2^31 bytes.
+inline bool supported(int nsp, int p, int ncr, int64_t P) {
+    return nsp == 2 && (p == 1 || p == 2 || p == 3 || p == 5 || p == 7) &&
+           (ncr == 16 || ncr == 32) && P * ncr * 4 < (int64_t)INT32_MAX;
 }
 
 }  // namespace f2d
