@@ -115,7 +115,7 @@ constexpr size_t lds_bytes() {
 }
 
 #ifndef CIRCATT_F2D_NCH
-#define CIRCATT_F2D_NCH 3
+#define CIRCATT_F2D_NCH 2
 #endif
 #ifndef CIRCATT_F2D_BIG_WW
 #define CIRCATT_F2D_BIG_WW 8
@@ -124,7 +124,11 @@ constexpr size_t lds_bytes() {
 template <int P, int NT, bool DIST, int MODE>
 struct Grid {
     static constexpr int BW = CIRCATT_F2D_BIG_WW;
+#ifdef CIRCATT_F2D_NO_BIG
+    static constexpr bool big = false;
+#else
     static constexpr bool big = lds_bytes<P, NT, 2, BW, DIST, MODE>() <= kLdsCap;
+#endif
     static constexpr bool mid = lds_bytes<P, NT, 1, 8, DIST, MODE>() <= kLdsCap;
     static constexpr int WH = big ? 2 : 1;
     static constexpr int WW = big ? BW : mid ? 8 : 4;
