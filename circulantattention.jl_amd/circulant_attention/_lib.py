@@ -23,6 +23,9 @@ DISTANCE = 1
 F32 = 0
 C32 = 1
 
+MATH_SPLIT_F16 = 0
+MATH_F32 = 1
+
 _i32 = ctypes.c_int32
 _int = ctypes.c_int
 _i64 = ctypes.c_int64
@@ -33,6 +36,8 @@ _p = ctypes.c_void_p
 SIGNATURES = {
     "circatt_version": (_int, []),
     "circatt_last_error": (ctypes.c_char_p, []),
+    "circatt_set_math": (_int, [_int]),
+    "circatt_get_math": (_int, []),
     "circatt_pattern": (_int, [_int, _i64, _i64, _i32, _i64, _p, _p, _p]),
     "circatt_similarity": (_int, [_int, _int, _int, _i64, _i64, _i32, _i64, _i64, _f32, _p, _p,
                                   _p, _p]),

@@ -4,6 +4,7 @@
 // No entry point allocates device memory.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -13,6 +14,13 @@
 #include "circatt_kernels.h"
 
 using namespace circatt;
+
+namespace circatt {
+namespace {
+std::atomic<int> g_math{CIRCATT_MATH_SPLIT_F16};
+}
+int math_mode() { return g_math.load(std::memory_order_relaxed); }
+}  // namespace circatt
 
 namespace {
 
@@ -87,6 +95,15 @@ int check_kind(int kind) {
 extern "C" {
 
 int circatt_version(void) { return 10000; }
+
+int circatt_set_math(int mode) {
+    if (mode != CIRCATT_MATH_SPLIT_F16 && mode != CIRCATT_MATH_F32)
+        return fail(CIRCATT_ERR_INVALID, "unknown math mode %d", mode);
+    g_math.store(mode, std::memory_order_relaxed);
+    return ok();
+}
+
+int circatt_get_math(void) { return math_mode(); }
 
 const char *circatt_last_error(void) { return g_last_error.c_str(); }
 

@@ -1,6 +1,7 @@
 // Kernel launchers shared between the kernel sources and the C-ABI layer.
 #pragma once
 
+#include "circatt.h"
 #include "circatt_common.h"
 
 namespace circatt {
@@ -21,6 +22,10 @@ hipError_t launch_sum(bool col, const Geom &g, int64_t nb, const float *nz, floa
 hipError_t launch_axpby(int64_t nnz, int64_t nb, const float *alpha, float alpha0,
                         const float *X, const float *beta, float beta0, const float *Y, float *Z,
                         hipStream_t s);
+
+// Arithmetic of the fused kernels' matrix products (circatt_set_math):
+// CIRCATT_MATH_SPLIT_F16 or CIRCATT_MATH_F32.
+int math_mode();
 
 // Fused (MFMA) kernels.  Modes of the windowed-tile kernel family:
 enum FusedMode {

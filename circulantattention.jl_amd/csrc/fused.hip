@@ -1,6 +1,7 @@
 // Host planning and dispatch of the windowed-tile MFMA kernels (kernels in
 // fused_impl.h, one translation unit per mode in fused_<mode>.hip).
 #include "fused2d_impl.h"
+#include "fused2h_impl.h"
 #include "fused_impl.h"
 
 namespace circatt {
@@ -98,6 +99,10 @@ hipError_t launch_f2d(FusedMode mode, const FusedProblem &pr, hipStream_t s) {
     const int nt = ncr / 16;
     const bool cplx = pr.ncomp == 2, dist = pr.kind == 1;
     const int cus = device_cus();
+    if (mode == MODE_FWD && nt == 1 && math_mode() == CIRCATT_MATH_SPLIT_F16) {
+        hipError_t e = launch_f2h_fwd(pr.g.p, cplx, dist, a, cus, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     switch (mode) {
     case MODE_FWD: return launch_f2d_fwd(pr.g.p, nt, cplx, dist, a, cus, s);
     case MODE_BWDQ: return launch_f2d_bwdq(pr.g.p, nt, cplx, dist, a, cus, s);

@@ -49,6 +49,22 @@ extern "C" {
 /* Library version (major*10000 + minor*100 + patch). */
 int circatt_version(void);
 
+/*
+ * Arithmetic of the fused kernels' matrix products.  The reference computes
+ * in Float32 throughout; it has no counterpart of this switch.
+ *   CIRCATT_MATH_SPLIT_F16 (default): each Float32 operand is split into two
+ *     halves and a product is taken as hi*hi + lo*hi + hi*lo on the f16
+ *     matrix cores with Float32 accumulation (relative error near 2^-21 per
+ *     operand, the order of Float32 rounding); operands must stay below
+ *     65504 in magnitude (queries after scaling by 1/sqrt(dh)*log2(e)).
+ *   CIRCATT_MATH_F32: Float32 matrix products (no range restriction).
+ * Process-wide; takes effect for launches after the call.
+ */
+#define CIRCATT_MATH_SPLIT_F16 0
+#define CIRCATT_MATH_F32 1
+int circatt_set_math(int mode);
+int circatt_get_math(void);
+
 /* Message describing the calling thread's last error ("" if none). */
 const char *circatt_last_error(void);
 
