@@ -99,8 +99,11 @@ hipError_t launch_f2d(FusedMode mode, const FusedProblem &pr, hipStream_t s) {
     const int nt = ncr / 16;
     const bool cplx = pr.ncomp == 2, dist = pr.kind == 1;
     const int cus = device_cus();
-    if (mode == MODE_FWD && nt == 1 && math_mode() == CIRCATT_MATH_SPLIT_F16) {
-        hipError_t e = launch_f2h_fwd(pr.g.p, cplx, dist, a, cus, s);
+    if (nt == 1 && math_mode() == CIRCATT_MATH_SPLIT_F16) {
+        hipError_t e = hipErrorNotSupported;
+        if (mode == MODE_FWD) e = launch_f2h_fwd(pr.g.p, cplx, dist, a, cus, s);
+        if (mode == MODE_BWDQ) e = launch_f2h_bwdq(pr.g.p, cplx, dist, a, cus, s);
+        if (mode == MODE_BWDKV) e = launch_f2h_bwdkv(pr.g.p, cplx, dist, a, cus, s);
         if (e != hipErrorNotSupported) return e;
     }
     switch (mode) {
