@@ -1,11 +1,11 @@
-// Instantiations of the split-half forward kernel (fused2h_impl.h).
+// Instantiations of the split-half kernels, forward (fused2h_impl.h).
 #include "fused2h_impl.h"
 
 namespace circatt {
 
 hipError_t launch_f2h_fwd(int p, bool cplx, bool dist, const f2d::Args &a, int cus,
                           hipStream_t s) {
-    return f2h::dispatch_fwd(p, cplx, dist, a, cus, s);
+    return f2h::dispatch<f2h::FWD>(p, cplx, dist, a, cus, s);
 }
 
 }  // namespace circatt
