@@ -35,6 +35,19 @@
 #pragma once
 #include "fused2d_impl.h"
 
+// Scheduling fences between the key blocks of the forward walk.  The
+// backward passes keep BLOCK_FENCE (without it the key-centric pass
+// interleaves blocks and runs out of registers); the forward schedules
+// better across block boundaries and runs without them by default.
+#ifndef CIRCATT_F2H_FWD_FENCE
+#define CIRCATT_F2H_FWD_FENCE 0
+#endif
+#if CIRCATT_F2H_FWD_FENCE
+#define FWD_FENCE() __builtin_amdgcn_sched_barrier(0)
+#else
+#define FWD_FENCE() ((void)0)
+#endif
+
 namespace circatt {
 namespace f2h {
 
@@ -114,7 +127,10 @@ enum { FWD = f2d::FWD, BWDQ = f2d::BWDQ, BWDKV = f2d::BWDKV };
 template <int P, int MODE, bool DIST>
 struct LGeo {
     using G = f2d::Geo<P, 1, 2, 8>;
-    static constexpr int VPS = G::HH * G::HWD;     // halves per value channel plane (forward)
+    // halves per value channel plane (forward); padded so that consecutive
+    // planes start 16 bytes apart modulo the 256-byte bank row
+    static constexpr int VPS0 = G::HH * G::HWD;
+    static constexpr int VPS = VPS0 + ((8 - VPS0 % 128) % 128 + 128) % 128;
     static constexpr int OT0 = 0;                  // tensor 0 slots (K, or Q in BWDKV)
     static constexpr int OT1 = G::LPX * KS * 2;    // tensor 1: V planes (FWD) or slots (V / dY)
     static constexpr int T1BYTES = MODE == FWD ? 2 * 16 * VPS * 2 : G::LPX * KS * 2;
@@ -382,7 +398,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 f4 S[2 * CHP];
                 static_for<cb, ce>([&](auto B) {
                     constexpr int b = decltype(B)::value;
-                    BLOCK_FENCE();
+                    FWD_FENCE();
                     f4 s0 = f4{0.f, 0.f, 0.f, 0.f};
                     if constexpr (DIST) s0 = scal(B, pS0);
                     S[b - cb] = score(B, pA0, r0h, r0l, s0);
@@ -411,7 +427,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     constexpr int b0 = 2 * pi;
                     constexpr bool has1 = b0 + 1 < NBLK;
                     constexpr int b1 = has1 ? b0 + 1 : b0;
-                    BLOCK_FENCE();
+                    FWD_FENCE();
                     float p0[4], p1[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
