@@ -165,6 +165,23 @@ __device__ __forceinline__ float mask_sel(float v, float alt) {
         return __builtin_amdgcn_inverse_ballot_w64(M) ? v : alt;
     }
 }
+// As mask_sel, with the lane mask written into SGPRs at the point of use:
+// `dep` is any wave-uniform value that changes from one loop iteration to the
+// next, so the two s_mov_b32 stay inside the loop instead of being hoisted
+// out of it, where dozens of live mask constants overflow the SGPR file.
+template <uint64_t M>
+__device__ __forceinline__ float mask_sel_d(float v, float alt, int dep) {
+    if constexpr (M == ~0ull) {
+        return v;
+    } else if constexpr (M == 0) {
+        return alt;
+    } else {
+        uint32_t lo, hi;
+        asm("s_mov_b32 %0, %2" : "=s"(lo) : "s"(dep), "i"((int)(uint32_t)M));
+        asm("s_mov_b32 %0, %2" : "=s"(hi) : "s"(dep), "i"((int)(uint32_t)(M >> 32)));
+        return __builtin_amdgcn_inverse_ballot_w64(((uint64_t)hi << 32) | lo) ? v : alt;
+    }
+}
 
 // Scheduling fence between the blocks of a walk: keeps the compiler from
 // hoisting later blocks' LDS reads (and their registers) into earlier blocks.

@@ -23,11 +23,9 @@
 //     8 g + 4 .. 8 g + 7 the same elements of block b+1, which is where the
 //     score accumulators of the two blocks already sit in the lane.
 //
-// LDS per staged pixel: [16 hi | 16 lo | pad] halves (score-type rows); the
-// forward stores values in channel planes of row-pair-major order so that
-// elements 4 g .. 4 g + 3 of a block are four consecutive halves (apply
-// rows); the backward reads its apply rows from the pixel slots, one half
-// per element.
+// LDS per staged pixel: [16 hi | 16 lo | pad] halves.  Score-type rows are
+// 16-byte reads of a slot; apply-type rows (one channel of four elements)
+// come from the same slots through the transposing read ds_read_b64_tr_b16.
 //
 // Operands must stay inside the f16 range, |x| < 65504 (queries after the
 // scale 1/sqrt(dh) * log2(e)); circatt_set_math(CIRCATT_MATH_F32) selects
@@ -59,6 +57,7 @@ using f2d::kLn2;
 using f2d::kLog2e;
 using f2d::lane_mask;
 using f2d::mask_sel;
+using f2d::mask_sel_d;
 using f2d::static_for;
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -90,6 +89,15 @@ __device__ __forceinline__ void split4(const float (&x)[4], h4 &hi, h4 &lo) {
     split2(x[2], x[3], a1, b1);
     hi = h4{a0[0], a0[1], a1[0], a1[1]};
     lo = h4{b0[0], b0[1], b1[0], b1[1]};
+}
+// transposing LDS read (ds_read_b64_tr_b16): within each group of 16 lanes,
+// lane 4 t + a supplies the address of 4 consecutive halves x[t][4a .. 4a+3]
+// and lane i receives x[0..3][i]
+typedef short s4v __attribute__((vector_size(8)));
+__device__ __forceinline__ h4 ldtr(const char *p) {
+    const s4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s4v *)(p));
+    return __builtin_bit_cast(h4, v);
 }
 __device__ __forceinline__ h8 cat(h4 a, h4 b) {
     return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
@@ -127,14 +135,9 @@ enum { FWD = f2d::FWD, BWDQ = f2d::BWDQ, BWDKV = f2d::BWDKV };
 template <int P, int MODE, bool DIST>
 struct LGeo {
     using G = f2d::Geo<P, 1, 2, 8>;
-    // halves per value channel plane (forward); padded so that consecutive
-    // planes start 16 bytes apart modulo the 256-byte bank row
-    static constexpr int VPS0 = G::HH * G::HWD;
-    static constexpr int VPS = VPS0 + ((8 - VPS0 % 128) % 128 + 128) % 128;
     static constexpr int OT0 = 0;                  // tensor 0 slots (K, or Q in BWDKV)
-    static constexpr int OT1 = G::LPX * KS * 2;    // tensor 1: V planes (FWD) or slots (V / dY)
-    static constexpr int T1BYTES = MODE == FWD ? 2 * 16 * VPS * 2 : G::LPX * KS * 2;
-    static constexpr int OS0 = OT1 + T1BYTES;      // Float32 scalars per slot
+    static constexpr int OT1 = G::LPX * KS * 2;    // tensor 1 slots (V, or dY in BWDKV)
+    static constexpr int OS0 = 2 * OT1;            // Float32 scalars per slot
     static constexpr int OS1 = OS0 + G::LPX * 4;
     static constexpr int NSCAL = MODE == BWDKV ? 2 : (DIST ? 1 : 0);
     static constexpr int bytes = OS0 + NSCAL * G::LPX * 4;
@@ -146,13 +149,16 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     using L = LGeo<P, MODE, DIST>;
     constexpr int WH = 2;
     constexpr int CR = G::CR, HH = G::HH, HWD = G::HWD, NKW = G::NKW, NBLK = G::NBLK;
-    constexpr int NPX = G::NPX, VPS = L::VPS;
+    constexpr int NPX = G::NPX;
     constexpr int NPAIR = (NBLK + 1) / 2;
     constexpr bool KV = MODE == BWDKV;
     // forward: pair chunks whose scores are held in registers at once
     constexpr int NCH = (MODE == FWD && NPAIR > 6) ? 2 : 1;
     constexpr int CHP = (NPAIR + NCH - 1) / NCH;
-    constexpr int PFP = MODE == FWD ? (NCH - 1) * CHP : NPAIR / 2;  // prefetch pair
+    // pair at which the next item's loads are issued (the forward issues them
+    // in its apply walk; with two chunks, at the last pair of the first, so
+    // that the loads are in flight over the whole second chunk)
+    constexpr int PFP = (MODE == FWD && NCH == 2) ? CHP - 1 : NPAIR / 2;
     static_assert(NPX <= 1024, "one staged pixel per thread");
     static_assert(HH % 2 == 0, "row pairs");
     char *const lds = reinterpret_cast<char *>(circatt_lds2);
@@ -170,18 +176,14 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     const int slotA = 8 * wh + (j & 1) + CR * (2 * ww + (j >> 1));
     const char *const pA0 = lds + opaque(L::OT0 + slotA * KS * 2 + 16 * g);
     const char *const pA1 = lds + opaque(L::OT1 + slotA * KS * 2 + 16 * g);
-    // apply-type rows from slots: channel j (hi; lo 16 halves further) of
-    // elements 4g + r, r = 0..3
+    // apply-type rows from slots by transposing reads: lane (j, g) receives
+    // channel j (hi; lo 16 halves further) of elements 4g + t, t = 0..3, so
+    // lane j of group g addresses channels 4 (j & 3) .. + 3 of element
+    // 4g + (j >> 2), which sits at row (j >> 2) & 1, column 2g + (j >> 3)
     const int slotE = 8 * wh + CR * (2 * ww + 2 * g);
-    const _Float16 *const pT0 =
-        reinterpret_cast<const _Float16 *>(lds + opaque(L::OT0 + (slotE * KS + j) * 2));
-    const _Float16 *const pT1 =
-        reinterpret_cast<const _Float16 *>(lds + opaque(L::OT1 + (slotE * KS + j) * 2));
-    // forward apply rows from value planes: plane j, row pair 4 wh + bi,
-    // column 2 ww + 8 bj + 2 g (elements 4g .. 4g+3 are 4 consecutive halves)
-    const int vbase = j * VPS + (4 * wh) * 2 * HWD + 2 * (2 * ww + 2 * g);
-    const char *const pVh = lds + opaque(L::OT1 + vbase * 2);
-    const char *const pVl = lds + opaque(L::OT1 + 16 * VPS * 2 + vbase * 2);
+    const int slotT = slotE + ((j >> 2) & 1) + CR * (j >> 3);
+    const char *const pR0 = lds + opaque(L::OT0 + slotT * KS * 2 + 8 * (j & 3));
+    const char *const pR1 = lds + opaque(L::OT1 + slotT * KS * 2 + 8 * (j & 3));
     // per-slot Float32 scalars of elements 4g .. 4g+3
     const float *const pS0 = reinterpret_cast<const float *>(lds + opaque(L::OS0 + slotE * 4));
     const float *const pS1 = reinterpret_cast<const float *>(lds + opaque(L::OS1 + slotE * 4));
@@ -291,23 +293,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 for (int c = 0; c < 16; ++c) n2 += h0v[c] * h0v[c];
             }
             store_slot(lds + L::OT0 + hslot * KS * 2, h0v);
-            if constexpr (MODE == FWD) {
-                // values: channel planes, (row pair, column, row & 1) order
-                const int vo = (kh >> 1) * 2 * HWD + 2 * kw + (kh & 1);
-                _Float16 *vh = reinterpret_cast<_Float16 *>(lds + L::OT1) + vo;
-                _Float16 *vl = vh + 16 * VPS;
-#pragma unroll
-                for (int c = 0; c < 16; c += 2) {
-                    h2 hi, lo;
-                    split2(h1v[c], h1v[c + 1], hi, lo);
-                    vh[c * VPS] = hi[0];
-                    vh[(c + 1) * VPS] = hi[1];
-                    vl[c * VPS] = lo[0];
-                    vl[(c + 1) * VPS] = lo[1];
-                }
-            } else {
-                store_slot(lds + L::OT1 + hslot * KS * 2, h1v);
-            }
+            store_slot(lds + L::OT1 + hslot * KS * 2, h1v);
             if constexpr (KV) {
                 // staged queries: A_q = -lse log2(e) [- c2 |q|^2 / 2], and -D
                 reinterpret_cast<float *>(lds + L::OS0)[hslot] =
@@ -350,11 +336,12 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
 
         const int nitem = f2d::item_of(a, k + 1);
         const bool has_next = nitem < a.nitems;
+        // unconditional (the last item loads itself again), so that the
+        // prefetch registers are dead between the staging and this point
         auto prefetch = [&]() {
-            if (has_next) {
-                load_stage(nitem);
-                load_regs(nitem);
-            }
+            const int li = has_next ? nitem : item;
+            load_stage(li);
+            load_regs(li);
         };
 
         // score-type product of block b (16 elements x 16 register pixels)
@@ -365,14 +352,12 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             init = mfmah(x, rh, init);
             return mfmah(x, rl, init);
         };
-        // apply-type rows of block b from slots: channel j of elements 4g + r
-        auto trows = [&](auto B, const _Float16 *pT, h4 &hi, h4 &lo) {
+        // apply-type rows of block b: channel j of elements 4g + t
+        auto trows = [&](auto B, const char *pR, h4 &hi, h4 &lo) {
             constexpr int b = decltype(B)::value;
-            constexpr int boff = 2 * (b / NKW) + CR * 8 * (b % NKW);
-            constexpr int t0 = boff * KS, t1 = (boff + 1) * KS, t2 = (boff + CR) * KS,
-                          t3 = (boff + CR + 1) * KS;
-            hi = h4{pT[t0], pT[t1], pT[t2], pT[t3]};
-            lo = h4{pT[t0 + 16], pT[t1 + 16], pT[t2 + 16], pT[t3 + 16]};
+            constexpr int boff = (2 * (b / NKW) + CR * 8 * (b % NKW)) * KS * 2;
+            hi = ldtr(pR + boff);
+            lo = ldtr(pR + boff + 32);
         };
         // per-slot scalars of elements 4g + r of block b
         auto scal = [&](auto B, const float *pS) {
@@ -394,7 +379,6 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 constexpr int pe = pb + CHP < NPAIR ? pb + CHP : NPAIR;
                 constexpr int cb = 2 * pb;
                 constexpr int ce = 2 * pe < NBLK ? 2 * pe : NBLK;
-                if constexpr (pb == PFP) prefetch();
                 f4 S[2 * CHP];
                 static_for<cb, ce>([&](auto B) {
                     constexpr int b = decltype(B)::value;
@@ -408,10 +392,10 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     constexpr int b = decltype(B)::value;
                     constexpr int bi = b / NKW, bj = b % NKW;
                     f4 &s = S[b - cb];
-                    s[0] = mask_sel<lane_mask(P, bi, bj, 0)>(s[0], -INFINITY);
-                    s[1] = mask_sel<lane_mask(P, bi, bj, 1)>(s[1], -INFINITY);
-                    s[2] = mask_sel<lane_mask(P, bi, bj, 2)>(s[2], -INFINITY);
-                    s[3] = mask_sel<lane_mask(P, bi, bj, 3)>(s[3], -INFINITY);
+                    s[0] = mask_sel_d<lane_mask(P, bi, bj, 0)>(s[0], -INFINITY, k);
+                    s[1] = mask_sel_d<lane_mask(P, bi, bj, 1)>(s[1], -INFINITY, k);
+                    s[2] = mask_sel_d<lane_mask(P, bi, bj, 2)>(s[2], -INFINITY, k);
+                    s[3] = mask_sel_d<lane_mask(P, bi, bj, 3)>(s[3], -INFINITY, k);
                     mx = fmaxf(fmaxf(mx, s[0]), s[1]);
                     mx = fmaxf(fmaxf(mx, s[2]), s[3]);
                 });
@@ -428,6 +412,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     constexpr bool has1 = b0 + 1 < NBLK;
                     constexpr int b1 = has1 ? b0 + 1 : b0;
                     FWD_FENCE();
+                    if constexpr (pi == PFP) prefetch();
                     float p0[4], p1[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -438,13 +423,10 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     h4 ph0, pl0, ph1, pl1;
                     split4(p0, ph0, pl0);
                     split4(p1, ph1, pl1);
-                    // value rows of blocks b0, b1: row pair bi, column offset 8 bj
-                    constexpr int v0 = ((b0 / NKW) * 2 * HWD + 16 * (b0 % NKW)) * 2;
-                    constexpr int v1 = ((b1 / NKW) * 2 * HWD + 16 * (b1 % NKW)) * 2;
-                    const h8 vh = cat(*reinterpret_cast<const h4 *>(pVh + v0),
-                                      *reinterpret_cast<const h4 *>(pVh + v1));
-                    const h8 vl = cat(*reinterpret_cast<const h4 *>(pVl + v0),
-                                      *reinterpret_cast<const h4 *>(pVl + v1));
+                    h4 t0h, t0l, t1h, t1l;
+                    trows(std::integral_constant<int, b0>{}, pR1, t0h, t0l);
+                    trows(std::integral_constant<int, b1>{}, pR1, t1h, t1l);
+                    const h8 vh = cat(t0h, t1h), vl = cat(t0l, t1l);
                     const h8 ph = cat(ph0, ph1), pl = cat(pl0, pl1);
                     acc = mfmah(vh, ph, acc);
                     acc = mfmah(vh, pl, acc);
@@ -493,10 +475,10 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     }
                     s = score(B, pA0, r0h, r0l, s);
                     dp = score(B, pA1, r1h, r1l, dp);
-                    p[u][0] = mask_sel<lane_mask(P, bi, bj, 0)>(__builtin_amdgcn_exp2f(s[0]), 0.f);
-                    p[u][1] = mask_sel<lane_mask(P, bi, bj, 1)>(__builtin_amdgcn_exp2f(s[1]), 0.f);
-                    p[u][2] = mask_sel<lane_mask(P, bi, bj, 2)>(__builtin_amdgcn_exp2f(s[2]), 0.f);
-                    p[u][3] = mask_sel<lane_mask(P, bi, bj, 3)>(__builtin_amdgcn_exp2f(s[3]), 0.f);
+                    p[u][0] = mask_sel_d<lane_mask(P, bi, bj, 0)>(__builtin_amdgcn_exp2f(s[0]), 0.f, k);
+                    p[u][1] = mask_sel_d<lane_mask(P, bi, bj, 1)>(__builtin_amdgcn_exp2f(s[1]), 0.f, k);
+                    p[u][2] = mask_sel_d<lane_mask(P, bi, bj, 2)>(__builtin_amdgcn_exp2f(s[2]), 0.f, k);
+                    p[u][3] = mask_sel_d<lane_mask(P, bi, bj, 3)>(__builtin_amdgcn_exp2f(s[3]), 0.f, k);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) ds[u][r] = p[u][r] * dp[r];
                     if constexpr (DIST) corr += (ds[u][0] + ds[u][1]) + (ds[u][2] + ds[u][3]);
@@ -513,8 +495,8 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 split4(ds[1], dh1, dl1);
                 const h8 dsh = cat(dh0, dh1), dsl = cat(dl0, dl1);
                 h4 t0h, t0l, t1h, t1l;
-                trows(std::integral_constant<int, b0>{}, pT0, t0h, t0l);
-                trows(std::integral_constant<int, b1>{}, pT0, t1h, t1l);
+                trows(std::integral_constant<int, b0>{}, pR0, t0h, t0l);
+                trows(std::integral_constant<int, b1>{}, pR0, t1h, t1l);
                 const h8 yh = cat(t0h, t1h), yl = cat(t0l, t1l);
                 acc0 = mfmah(yh, dsh, acc0);
                 acc0 = mfmah(yl, dsh, acc0);
@@ -524,8 +506,8 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     split4(p[0], ph0, pl0);
                     split4(p[1], ph1, pl1);
                     const h8 ph = cat(ph0, ph1), pl = cat(pl0, pl1);
-                    trows(std::integral_constant<int, b0>{}, pT1, t0h, t0l);
-                    trows(std::integral_constant<int, b1>{}, pT1, t1h, t1l);
+                    trows(std::integral_constant<int, b0>{}, pR1, t0h, t0l);
+                    trows(std::integral_constant<int, b1>{}, pR1, t1h, t1l);
                     const h8 zh = cat(t0h, t1h), zl = cat(t0l, t1l);
                     acc1 = mfmah(zh, ph, acc1);
                     acc1 = mfmah(zl, ph, acc1);
