@@ -69,18 +69,27 @@ __device__ __forceinline__ f4 mfmah(h8 a, h8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// hi = f16(x), lo = f16(x - hi); x - hi is formed by v_fma_mix from the
-// packed halves (the s_nop covers a transcendental producer of x)
+// hi = f16(x), lo = f16(x - hi): v_fma_mixlo_f16 / v_fma_mixhi_f16 form
+// x - hi exactly in Float32 from the packed halves and round it once into
+// the low / high half of lo.  The compiler inserts no wait states around
+// inline asm, so the asm keeps to registers whose hazards are settled:
+//   * x0 and x1 are read first by the conversion that forms hi, which
+//     therefore stands between their producer (an MFMA or a transcendental
+//     among them) and the asm;
+//   * lo is written into the register of x0 (tied operand), which no
+//     in-flight MFMA can be reading;
+//   * the trailing s_nop 1 gives the 2 wait states an MFMA needs before it
+//     reads a VGPR written by a vector instruction.
 __device__ __forceinline__ void split2(float x0, float x1, h2 &hi, h2 &lo) {
     hi = h2{(_Float16)x0, (_Float16)x1};
-    float r0, r1;
-    asm("s_nop 0\n\tv_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
-        : "=v"(r0)
-        : "v"(hi), "v"(x0));
-    asm("s_nop 0\n\tv_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-        : "=v"(r1)
+    float t = x0;
+    asm("v_fma_mixlo_f16 %0, %1, -1.0, %0 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
+        : "+v"(t)
+        : "v"(hi));
+    asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\ts_nop 1"
+        : "+v"(t)
         : "v"(hi), "v"(x1));
-    lo = h2{(_Float16)r0, (_Float16)r1};
+    lo = __builtin_bit_cast(h2, t);
 }
 // 4 values -> hi, lo as one half of a pair operand
 __device__ __forceinline__ void split4(const float (&x)[4], h4 &hi, h4 &lo) {
