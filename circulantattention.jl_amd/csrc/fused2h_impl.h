@@ -33,17 +33,24 @@
 #pragma once
 #include "fused2d_impl.h"
 
-// Scheduling fences between the key blocks of the forward walk.  The
-// backward passes keep BLOCK_FENCE (without it the key-centric pass
-// interleaves blocks and runs out of registers); the forward schedules
-// better across block boundaries and runs without them by default.
+// Scheduling fences of the forward walk.  The backward passes keep
+// BLOCK_FENCE between block pairs (without it the key-centric pass
+// interleaves blocks and runs out of registers); the forward fences its apply
+// pairs but lets the score products of a chunk schedule freely (measured best
+// on gfx950: fences everywhere cost 4%, none at all 7%).
 #ifndef CIRCATT_F2H_FWD_FENCE
-#define CIRCATT_F2H_FWD_FENCE 0
+#define CIRCATT_F2H_FWD_FENCE 2
 #endif
-#if CIRCATT_F2H_FWD_FENCE
-#define FWD_FENCE() __builtin_amdgcn_sched_barrier(0)
+// bit 0: between score blocks, bit 1: between apply pairs
+#if CIRCATT_F2H_FWD_FENCE & 1
+#define FWD_FENCE_S() __builtin_amdgcn_sched_barrier(0)
 #else
-#define FWD_FENCE() ((void)0)
+#define FWD_FENCE_S() ((void)0)
+#endif
+#if CIRCATT_F2H_FWD_FENCE & 2
+#define FWD_FENCE_A() __builtin_amdgcn_sched_barrier(0)
+#else
+#define FWD_FENCE_A() ((void)0)
 #endif
 
 namespace circatt {
@@ -202,7 +209,10 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     // ---- prefetch registers ----
     float h0v[16], h1v[16], hs0 = 0.f, hs1 = 0.f;
     int hslot;
-    float nr0[8], nr1[8], nry[8];
+    // register operands: lane groups g and g ^ 2 (lanes l, l ^ 32) share a
+    // pixel and its channels 8 (g & 1) .. + 7; each loads half of them,
+    // components 8 (g & 1) + 4 (g >> 1) + t, and a lane swap joins the halves
+    float nh0[4], nh1[4], nry[4];
     float nlse = 0.f;
 
     auto decode = [&](int item, int &unit, int &h0, int &w0) {
@@ -265,14 +275,14 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         const int64_t uoff = (int64_t)unit * a.unit_stride;
         const auto r0 = f2d::rsrc((KV ? a.k : a.q) + uoff, ubytes);
         const auto r1 = f2d::rsrc((KV ? a.v : a.dy) + uoff, ubytes);
-        // components 8 (g & 1) + s, s = 0..7
-        const int vo = f2d::comp_off<CPLX>(a.P, rpix, 8 * (g & 1)) * 4;
+        const int vo = f2d::comp_off<CPLX>(a.P, rpix, 8 * (g & 1) + 4 * (g >> 1)) * 4;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const int so = (CPLX ? 2 * a.P * (s >> 1) + (s & 1) : a.P * s) * 4;
-            nr0[s] = f2d::bload(r0, vo, so);
-            if constexpr (MODE != FWD) nr1[s] = f2d::bload(r1, vo, so);
-            if constexpr (MODE == BWDQ) nry[s] = f2d::bload(f2d::rsrc(a.y + uoff, ubytes), vo, so);
+        for (int t = 0; t < 4; ++t) {
+            const int so = (CPLX ? 2 * a.P * (t >> 1) + (t & 1) : a.P * t) * 4;
+            nh0[t] = f2d::bload(r0, vo, so);
+            if constexpr (MODE != FWD) nh1[t] = f2d::bload(r1, vo, so);
+            // y beside dy, for D = <dy, y>
+            if constexpr (MODE == BWDQ) nry[t] = f2d::bload(f2d::rsrc(a.y + uoff, ubytes), vo, so);
         }
         if constexpr (MODE == BWDQ)
             nlse = f2d::bload(f2d::rsrc(a.lse + (int64_t)unit * a.P, a.P * 4), rpix * 4, 0);
@@ -312,25 +322,41 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 reinterpret_cast<float *>(lds + L::OS0)[hslot] = -0.5f * c2 * n2;  // key bias
             }
         }
-        // register operands: the score product's side pre-scaled by c2
+        // register operands (the score product's side pre-scaled by c2):
+        // channels 8 (g & 1) + t from the lower half of the wave, + 4 + t
+        // from the upper half
+        float nr0[8], nr1[8];
+        auto join = [](const float (&h)[4], float (&x)[8]) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const unsigned u = __float_as_uint(h[t]);
+                const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+                x[t] = __uint_as_float(r[0]);
+                x[4 + t] = __uint_as_float(r[1]);
+            }
+        };
+        join(nh0, nr0);
         h8 r0h, r0l, r1h, r1l;
         reg_split(nr0, c2, r0h, r0l);
-        if constexpr (MODE != FWD) reg_split(nr1, 1.f, r1h, r1l);
-        // lane groups g and g ^ 2 hold the same 8 channels, so sums over the
-        // four groups count every channel twice
+        if constexpr (MODE != FWD) {
+            join(nh1, nr1);
+            reg_split(nr1, 1.f, r1h, r1l);
+        }
+        // sums of the loaded halves over the four lane groups count every
+        // channel once
         float raw2 = 0.f, rowD = 0.f, rowL = 0.f;
         if constexpr (DIST) {
 #pragma unroll
-            for (int s = 0; s < 8; ++s) raw2 += nr0[s] * nr0[s];
+            for (int t = 0; t < 4; ++t) raw2 += nh0[t] * nh0[t];
         }
         if constexpr (MODE == BWDQ) {
             float dd = 0.f;
 #pragma unroll
-            for (int s = 0; s < 8; ++s) dd += nr1[s] * nry[s];
-            rowD = 0.5f * gsum(dd);
+            for (int t = 0; t < 4; ++t) dd += nh1[t] * nry[t];
+            rowD = gsum(dd);
             rowL = nlse;
         }
-        const float sq = DIST ? 0.5f * gsum(raw2) : 0.f;
+        const float sq = DIST ? gsum(raw2) : 0.f;
         // Distance correction of the outputs needs the register pixel's
         // channels 4 g + r (the output layout): channel 4 g + r sits at
         // index 4 (g & 1) + r in lane group g' = (g >> 1) + 2 (g & 1), whose
@@ -391,7 +417,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 f4 S[2 * CHP];
                 static_for<cb, ce>([&](auto B) {
                     constexpr int b = decltype(B)::value;
-                    FWD_FENCE();
+                    FWD_FENCE_S();
                     f4 s0 = f4{0.f, 0.f, 0.f, 0.f};
                     if constexpr (DIST) s0 = scal(B, pS0);
                     S[b - cb] = score(B, pA0, r0h, r0l, s0);
@@ -420,7 +446,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     constexpr int b0 = 2 * pi;
                     constexpr bool has1 = b0 + 1 < NBLK;
                     constexpr int b1 = has1 ? b0 + 1 : b0;
-                    FWD_FENCE();
+                    FWD_FENCE_A();
                     if constexpr (pi == PFP) prefetch();
                     float p0[4], p1[4];
 #pragma unroll
