@@ -105,3 +105,19 @@ def test_python_layer_refuses_cpu_tensors():
         ca.circulant_similarity(ca.DotSimilarity(), x, x, 3)
     with pytest.raises(AssertionError, match="must be odd"):
         ca.Circulant.new(4, (8, 8, 1, 1), device="cpu")
+
+
+def test_math_mode_switch(L):
+    """circatt_set_math accepts the two documented modes, keeps the last one,
+    and rejects anything else without changing the mode."""
+    old = L.lib.circatt_get_math()
+    try:
+        assert L.lib.circatt_set_math(L.MATH_F32) == L.OK
+        assert L.lib.circatt_get_math() == L.MATH_F32
+        expect(L, L.lib.circatt_set_math(7), L.ERR_INVALID, "math")
+        assert L.lib.circatt_get_math() == L.MATH_F32
+        assert L.lib.circatt_set_math(L.MATH_SPLIT_F16) == L.OK
+        assert L.lib.circatt_get_math() == L.MATH_SPLIT_F16
+        expect(L, L.lib.circatt_set_math(-1), L.ERR_INVALID, "math")
+    finally:
+        L.lib.circatt_set_math(old)

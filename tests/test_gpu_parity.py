@@ -208,6 +208,28 @@ def test_attention_fused(ca, cuda, case, cplx, kind):
     _attention_case(ca, cuda, *case, cplx, kind, materialize=False)
 
 
+# the 2D compile-time-window cases again, with the Float32 matrix-core kernels
+# (the default above is the split-half arithmetic)
+F32_CASES = [c for c in ATT_CASES if len(c[0]) == 2 and c[1] in (3, 5, 7, 11, 15)
+             and (c[2] // c[4]) in (16, 32)]
+
+
+@pytest.fixture
+def f32_math(ca):
+    from circulant_attention import _lib as L
+    old = L.lib.circatt_get_math()
+    L.check(L.lib.circatt_set_math(L.MATH_F32))
+    yield
+    L.check(L.lib.circatt_set_math(old))
+
+
+@pytest.mark.parametrize("case", F32_CASES, ids=lambda c: f"{c[0]}-ws{c[1]}-C{c[2]}-h{c[4]}")
+@pytest.mark.parametrize("cplx", [False, True])
+@pytest.mark.parametrize("kind", [0, 1])
+def test_attention_fused_f32_math(ca, cuda, f32_math, case, cplx, kind):
+    _attention_case(ca, cuda, *case, cplx, kind, materialize=False)
+
+
 def test_fused_lse(ca, cuda):
     from circulant_attention import _lib as L
     from circulant_attention._functions import ptr, stream_ptr
