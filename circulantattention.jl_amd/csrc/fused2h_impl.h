@@ -174,7 +174,16 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     // pair at which the next item's loads are issued (the forward issues them
     // in its apply walk; with two chunks, at the last pair of the first, so
     // that the loads are in flight over the whole second chunk)
-    constexpr int PFP = (MODE == FWD && NCH == 2) ? CHP - 1 : NPAIR / 2;
+#ifndef CIRCATT_F2H_BWD_PFD
+#define CIRCATT_F2H_BWD_PFD 2
+#endif
+#ifndef CIRCATT_F2H_BWD_FSTEP
+#define CIRCATT_F2H_BWD_FSTEP 1
+#endif
+    // forward with a reference maximum from the central block row (rows 8, 9
+    // of the key region lie in every query's window when 2P >= 9)
+    constexpr bool STREAM = MODE == FWD && NKW == 2 && P >= 5;
+    constexpr int PFP = STREAM ? 1 : (MODE == FWD && NCH == 2) ? CHP - 1 : NPAIR / CIRCATT_F2H_BWD_PFD;
     static_assert(NPX <= 1024, "one staged pixel per thread");
     static_assert(HH % 2 == 0, "row pairs");
     char *const lds = reinterpret_cast<char *>(circatt_lds2);
@@ -215,6 +224,12 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     float nh0[4], nh1[4], nry[4];
     float nlse = 0.f;
 
+    // register pixel of this lane in the tile at (h0, w0)
+    auto regpix = [&](int h0, int w0, bool &rvalid, int &rpix) {
+        const int rh = h0 + 8 * wh + jh, rw = w0 + 2 * ww + jw;
+        rvalid = rh < a.n1 && rw < a.n2;
+        rpix = rvalid ? rh + a.n1 * rw : 0;
+    };
     auto decode = [&](int item, int &unit, int &h0, int &w0) {
         const int ntiles = a.tiles_h * a.tiles_w;
         unit = item / ntiles;
@@ -269,9 +284,9 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     auto load_regs = [&](int item) {
         int unit, h0, w0;
         decode(item, unit, h0, w0);
-        const int rh = h0 + 8 * wh + jh, rw = w0 + 2 * ww + jw;
-        const bool rvalid = rh < a.n1 && rw < a.n2;
-        const int rpix = rvalid ? rh + a.n1 * rw : 0;
+        bool rvalid;
+        int rpix;
+        regpix(h0, w0, rvalid, rpix);
         const int64_t uoff = (int64_t)unit * a.unit_stride;
         const auto r0 = f2d::rsrc((KV ? a.k : a.q) + uoff, ubytes);
         const auto r1 = f2d::rsrc((KV ? a.v : a.dy) + uoff, ubytes);
@@ -297,9 +312,9 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     while (true) {
         int unit, h0, w0;
         decode(item, unit, h0, w0);
-        const int rh = h0 + 8 * wh + jh, rw = w0 + 2 * ww + jw;
-        const bool rvalid = rh < a.n1 && rw < a.n2;
-        const int rpix = rvalid ? rh + a.n1 * rw : 0;
+        bool rvalid;
+        int rpix;
+        regpix(h0, w0, rvalid, rpix);
         const int64_t uoff = (int64_t)unit * a.unit_stride;
         const int64_t soff = (int64_t)unit * a.P;
         const float c2 = a.c2;
@@ -403,7 +418,106 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             return f4{lo[0], lo[1], hi[0], hi[1]};
         };
 
-        if constexpr (MODE == FWD) {
+        if constexpr (STREAM) {
+            // Scores are taken relative to a reference maximum m, set by the
+            // central pair of block row PC (inside every query's window, so
+            // m is finite), which lets the MFMA's initial accumulator carry
+            // the subtraction.  A later pair whose probabilities sum past 2^8
+            // in some lane (a score more than 8 above m, in log2 units) first
+            // raises m and rescales the accumulated terms; on typical data
+            // this never happens.
+            constexpr int PC = 4;
+            float m = 0.f, lsum = 0.f;
+            f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+            auto do_pair = [&](auto PI, auto FIRST) {
+                constexpr int pi = decltype(PI)::value;
+                constexpr bool first = decltype(FIRST)::value;
+                constexpr int b0 = 2 * pi;
+                constexpr bool has1 = b0 + 1 < NBLK;
+                constexpr int b1 = has1 ? b0 + 1 : b0;
+                FWD_FENCE_A();
+                if constexpr (pi == PFP) prefetch();
+                f4 sv[2];
+                auto sc = [&](auto B, int u) {
+                    constexpr int b = decltype(B)::value;
+                    constexpr int bi = b / NKW, bj = b % NKW;
+                    f4 init = f4{0.f, 0.f, 0.f, 0.f};
+                    if constexpr (DIST) init = scal(B, pS0);
+                    if constexpr (!first) init = init - f4{m, m, m, m};
+                    f4 x = score(B, pA0, r0h, r0l, init);
+                    x[0] = mask_sel_d<lane_mask(P, bi, bj, 0)>(x[0], -INFINITY, k);
+                    x[1] = mask_sel_d<lane_mask(P, bi, bj, 1)>(x[1], -INFINITY, k);
+                    x[2] = mask_sel_d<lane_mask(P, bi, bj, 2)>(x[2], -INFINITY, k);
+                    x[3] = mask_sel_d<lane_mask(P, bi, bj, 3)>(x[3], -INFINITY, k);
+                    sv[u] = x;
+                };
+                sc(std::integral_constant<int, b0>{}, 0);
+                if constexpr (has1) {
+                    sc(std::integral_constant<int, b1>{}, 1);
+                } else {
+                    sv[1] = f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+                }
+                auto lane_max = [&]() {
+                    const float a0 = fmaxf(fmaxf(sv[0][0], sv[0][1]), sv[0][2]);
+                    const float a1 = fmaxf(fmaxf(sv[0][3], sv[1][0]), sv[1][1]);
+                    return fmaxf(fmaxf(a0, a1), fmaxf(sv[1][2], sv[1][3]));
+                };
+                float p[2][4];
+                auto exps = [&]() {
+#pragma unroll
+                    for (int u = 0; u < 2; ++u)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) p[u][r] = __builtin_amdgcn_exp2f(sv[u][r]);
+                    return ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) +
+                           ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
+                };
+                if constexpr (first) {
+                    m = gmax(lane_max());
+                    sv[0] = sv[0] - f4{m, m, m, m};
+                    sv[1] = sv[1] - f4{m, m, m, m};
+                }
+                float ps = exps();
+                if constexpr (!first) {
+                    if (__builtin_amdgcn_ballot_w64(ps > 256.f) != 0) {
+                        const float d = fmaxf(gmax(lane_max()), 0.f);
+                        m += d;
+                        const float alpha = __builtin_amdgcn_exp2f(-d);
+                        lsum *= alpha;
+                        acc *= alpha;
+                        sv[0] = sv[0] - f4{d, d, d, d};
+                        sv[1] = sv[1] - f4{d, d, d, d};
+                        ps = exps();
+                    }
+                }
+                lsum += ps;
+                h4 ph0, pl0, ph1, pl1;
+                split4(p[0], ph0, pl0);
+                split4(p[1], ph1, pl1);
+                h4 t0h, t0l, t1h, t1l;
+                trows(std::integral_constant<int, b0>{}, pR1, t0h, t0l);
+                trows(std::integral_constant<int, b1>{}, pR1, t1h, t1l);
+                const h8 vh = cat(t0h, t1h), vl = cat(t0l, t1l);
+                const h8 ph = cat(ph0, ph1), pl = cat(pl0, pl1);
+                acc = mfmah(vh, ph, acc);
+                acc = mfmah(vh, pl, acc);
+                acc = mfmah(vl, ph, acc);
+            };
+            do_pair(std::integral_constant<int, PC>{}, std::true_type{});
+            static_for<0, NPAIR>([&](auto PI) {
+                if constexpr (decltype(PI)::value != PC) do_pair(PI, std::false_type{});
+            });
+            const float l = gsum(lsum);
+            const float inv = 1.f / l;
+            if (rvalid) {
+                float *yb = a.yout + uoff;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    yb[f2d::comp_off<CPLX>(a.P, rpix, 4 * g + r)] = acc[r] * inv;
+                if (g == 0)
+                    a.lse_out[soff + rpix] =
+                        (m + __log2f(l)) * kLn2 - (DIST ? 0.5f * sq * a.scale : 0.f);
+            }
+        } else if constexpr (MODE == FWD) {
             // running maximum starts finite: a chunk may hold no valid key of
             // a query (then its scores are all -inf and exp2 gives 0, not NaN)
             float m = -1e30f, lsum = 0.f;
@@ -492,7 +606,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 constexpr int b0 = 2 * pi;
                 constexpr bool has1 = b0 + 1 < NBLK;
                 constexpr int b1 = has1 ? b0 + 1 : b0;
-                BLOCK_FENCE();
+                if constexpr (pi % CIRCATT_F2H_BWD_FSTEP == 0) BLOCK_FENCE();
                 if constexpr (pi == PFP) prefetch();
                 float p[2][4], ds[2][4];
                 auto blk = [&](auto B, int u) {
