@@ -418,77 +418,54 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             return f4{lo[0], lo[1], hi[0], hi[1]};
         };
 
-        if constexpr (STREAM) {
-            // Scores are taken relative to a reference maximum m, set by the
-            // central pair of block row PC (inside every query's window, so
-            // m is finite), which lets the MFMA's initial accumulator carry
-            // the subtraction.  A later pair whose probabilities sum past 2^8
-            // in some lane (a score more than 8 above m, in log2 units) first
-            // raises m and rescales the accumulated terms; on typical data
-            // this never happens.
-            constexpr int PC = 4;
+        if constexpr (MODE == FWD) {
             float m = 0.f, lsum = 0.f;
             f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-            auto do_pair = [&](auto PI, auto FIRST) {
+            // scores of block b (pair slot u) relative to m, masked to -inf
+            // outside the window (dep: a per-walk value for the lane masks,
+            // so that walks do not share, and keep live, each other's masks)
+            auto scores = [&](auto PI, auto REL, f4 (&sv)[2], int dep) {
                 constexpr int pi = decltype(PI)::value;
-                constexpr bool first = decltype(FIRST)::value;
+                constexpr bool rel = decltype(REL)::value;
                 constexpr int b0 = 2 * pi;
                 constexpr bool has1 = b0 + 1 < NBLK;
-                constexpr int b1 = has1 ? b0 + 1 : b0;
-                FWD_FENCE_A();
-                if constexpr (pi == PFP) prefetch();
-                f4 sv[2];
                 auto sc = [&](auto B, int u) {
                     constexpr int b = decltype(B)::value;
                     constexpr int bi = b / NKW, bj = b % NKW;
                     f4 init = f4{0.f, 0.f, 0.f, 0.f};
                     if constexpr (DIST) init = scal(B, pS0);
-                    if constexpr (!first) init = init - f4{m, m, m, m};
+                    if constexpr (rel) init = init - f4{m, m, m, m};
                     f4 x = score(B, pA0, r0h, r0l, init);
-                    x[0] = mask_sel_d<lane_mask(P, bi, bj, 0)>(x[0], -INFINITY, k);
-                    x[1] = mask_sel_d<lane_mask(P, bi, bj, 1)>(x[1], -INFINITY, k);
-                    x[2] = mask_sel_d<lane_mask(P, bi, bj, 2)>(x[2], -INFINITY, k);
-                    x[3] = mask_sel_d<lane_mask(P, bi, bj, 3)>(x[3], -INFINITY, k);
+                    x[0] = mask_sel_d<lane_mask(P, bi, bj, 0)>(x[0], -INFINITY, dep);
+                    x[1] = mask_sel_d<lane_mask(P, bi, bj, 1)>(x[1], -INFINITY, dep);
+                    x[2] = mask_sel_d<lane_mask(P, bi, bj, 2)>(x[2], -INFINITY, dep);
+                    x[3] = mask_sel_d<lane_mask(P, bi, bj, 3)>(x[3], -INFINITY, dep);
                     sv[u] = x;
                 };
                 sc(std::integral_constant<int, b0>{}, 0);
                 if constexpr (has1) {
-                    sc(std::integral_constant<int, b1>{}, 1);
+                    sc(std::integral_constant<int, b0 + 1>{}, 1);
                 } else {
                     sv[1] = f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
                 }
-                auto lane_max = [&]() {
-                    const float a0 = fmaxf(fmaxf(sv[0][0], sv[0][1]), sv[0][2]);
-                    const float a1 = fmaxf(fmaxf(sv[0][3], sv[1][0]), sv[1][1]);
-                    return fmaxf(fmaxf(a0, a1), fmaxf(sv[1][2], sv[1][3]));
-                };
+            };
+            auto pair_max = [](const f4 (&sv)[2]) {
+                const float a0 = fmaxf(fmaxf(sv[0][0], sv[0][1]), sv[0][2]);
+                const float a1 = fmaxf(fmaxf(sv[0][3], sv[1][0]), sv[1][1]);
+                return fmaxf(fmaxf(a0, a1), fmaxf(sv[1][2], sv[1][3]));
+            };
+            // probabilities exp2(sv) of a pair into the sums and the output
+            auto apply = [&](auto PI, const f4 (&sv)[2]) {
+                constexpr int pi = decltype(PI)::value;
+                constexpr int b0 = 2 * pi;
+                constexpr int b1 = b0 + 1 < NBLK ? b0 + 1 : b0;
                 float p[2][4];
-                auto exps = [&]() {
 #pragma unroll
-                    for (int u = 0; u < 2; ++u)
+                for (int u = 0; u < 2; ++u)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) p[u][r] = __builtin_amdgcn_exp2f(sv[u][r]);
-                    return ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) +
-                           ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
-                };
-                if constexpr (first) {
-                    m = gmax(lane_max());
-                    sv[0] = sv[0] - f4{m, m, m, m};
-                    sv[1] = sv[1] - f4{m, m, m, m};
-                }
-                float ps = exps();
-                if constexpr (!first) {
-                    if (__builtin_amdgcn_ballot_w64(ps > 256.f) != 0) {
-                        const float d = fmaxf(gmax(lane_max()), 0.f);
-                        m += d;
-                        const float alpha = __builtin_amdgcn_exp2f(-d);
-                        lsum *= alpha;
-                        acc *= alpha;
-                        sv[0] = sv[0] - f4{d, d, d, d};
-                        sv[1] = sv[1] - f4{d, d, d, d};
-                        ps = exps();
-                    }
-                }
+                    for (int r = 0; r < 4; ++r) p[u][r] = __builtin_amdgcn_exp2f(sv[u][r]);
+                const float ps = ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) +
+                                 ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
                 lsum += ps;
                 h4 ph0, pl0, ph1, pl1;
                 split4(p[0], ph0, pl0);
@@ -501,88 +478,60 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 acc = mfmah(vh, ph, acc);
                 acc = mfmah(vh, pl, acc);
                 acc = mfmah(vl, ph, acc);
+                return ps;
             };
-            do_pair(std::integral_constant<int, PC>{}, std::true_type{});
-            static_for<0, NPAIR>([&](auto PI) {
-                if constexpr (decltype(PI)::value != PC) do_pair(PI, std::false_type{});
-            });
-            const float l = gsum(lsum);
-            const float inv = 1.f / l;
-            if (rvalid) {
-                float *yb = a.yout + uoff;
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    yb[f2d::comp_off<CPLX>(a.P, rpix, 4 * g + r)] = acc[r] * inv;
-                if (g == 0)
-                    a.lse_out[soff + rpix] =
-                        (m + __log2f(l)) * kLn2 - (DIST ? 0.5f * sq * a.scale : 0.f);
-            }
-        } else if constexpr (MODE == FWD) {
-            // running maximum starts finite: a chunk may hold no valid key of
-            // a query (then its scores are all -inf and exp2 gives 0, not NaN)
-            float m = -1e30f, lsum = 0.f;
-            f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-            auto chunk = [&](auto CH) {
-                constexpr int ci = decltype(CH)::value;
-                constexpr int pb = ci * CHP;
-                constexpr int pe = pb + CHP < NPAIR ? pb + CHP : NPAIR;
-                constexpr int cb = 2 * pb;
-                constexpr int ce = 2 * pe < NBLK ? 2 * pe : NBLK;
-                f4 S[2 * CHP];
-                static_for<cb, ce>([&](auto B) {
-                    constexpr int b = decltype(B)::value;
-                    FWD_FENCE_S();
-                    f4 s0 = f4{0.f, 0.f, 0.f, 0.f};
-                    if constexpr (DIST) s0 = scal(B, pS0);
-                    S[b - cb] = score(B, pA0, r0h, r0l, s0);
-                });
-                float mx = m;
-                static_for<cb, ce>([&](auto B) {
-                    constexpr int b = decltype(B)::value;
-                    constexpr int bi = b / NKW, bj = b % NKW;
-                    f4 &s = S[b - cb];
-                    s[0] = mask_sel_d<lane_mask(P, bi, bj, 0)>(s[0], -INFINITY, k);
-                    s[1] = mask_sel_d<lane_mask(P, bi, bj, 1)>(s[1], -INFINITY, k);
-                    s[2] = mask_sel_d<lane_mask(P, bi, bj, 2)>(s[2], -INFINITY, k);
-                    s[3] = mask_sel_d<lane_mask(P, bi, bj, 3)>(s[3], -INFINITY, k);
-                    mx = fmaxf(fmaxf(mx, s[0]), s[1]);
-                    mx = fmaxf(fmaxf(mx, s[2]), s[3]);
-                });
-                const float mn = gmax(mx);
-                if constexpr (ci > 0) {
-                    const float alpha = __builtin_amdgcn_exp2f(m - mn);
-                    lsum *= alpha;
-                    acc *= alpha;
+            // Scores relative to a reference maximum m, folded into the MFMA's
+            // initial accumulator.  The first walk takes m from the central
+            // pair PC (block row 4: rows 8, 9 of the key region lie in every
+            // query's window when 2P >= 9, so m is finite) and has no branch;
+            // if a pair's probabilities sum past 2^8 in some lane (a score
+            // more than 8 above m, in log2 units, where the halves could
+            // overflow), the item is redone with m the exact row maximum from
+            // a scores-only pass.  On typical data the redo never runs.
+            constexpr int PC = STREAM ? 4 : 0;
+            uint64_t over = 1;
+            if constexpr (STREAM) {
+                {
+                    f4 sv[2];
+                    scores(std::integral_constant<int, PC>{}, std::false_type{}, sv, k);
+                    m = gmax(pair_max(sv));
+                    sv[0] = sv[0] - f4{m, m, m, m};
+                    sv[1] = sv[1] - f4{m, m, m, m};
+                    apply(std::integral_constant<int, PC>{}, sv);
                 }
-                m = mn;
-                static_for<pb, pe>([&](auto PI) {
+                over = 0;
+                static_for<0, NPAIR>([&](auto PI) {
                     constexpr int pi = decltype(PI)::value;
-                    constexpr int b0 = 2 * pi;
-                    constexpr bool has1 = b0 + 1 < NBLK;
-                    constexpr int b1 = has1 ? b0 + 1 : b0;
-                    FWD_FENCE_A();
-                    if constexpr (pi == PFP) prefetch();
-                    float p0[4], p1[4];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        p0[r] = __builtin_amdgcn_exp2f(S[b0 - cb][r] - m);
-                        p1[r] = has1 ? __builtin_amdgcn_exp2f(S[b1 - cb][r] - m) : 0.f;
-                        lsum += p0[r] + p1[r];
+                    if constexpr (pi != PC) {
+                        FWD_FENCE_A();
+                        if constexpr (pi == PFP) prefetch();
+                        f4 sv[2];
+                        scores(PI, std::true_type{}, sv, k);
+                        const float ps = apply(PI, sv);
+                        over |= __builtin_amdgcn_ballot_w64(!(ps <= 256.f));
                     }
-                    h4 ph0, pl0, ph1, pl1;
-                    split4(p0, ph0, pl0);
-                    split4(p1, ph1, pl1);
-                    h4 t0h, t0l, t1h, t1l;
-                    trows(std::integral_constant<int, b0>{}, pR1, t0h, t0l);
-                    trows(std::integral_constant<int, b1>{}, pR1, t1h, t1l);
-                    const h8 vh = cat(t0h, t1h), vl = cat(t0l, t1l);
-                    const h8 ph = cat(ph0, ph1), pl = cat(pl0, pl1);
-                    acc = mfmah(vh, ph, acc);
-                    acc = mfmah(vh, pl, acc);
-                    acc = mfmah(vl, ph, acc);
                 });
-            };
-            static_for<0, NCH>(chunk);
+            }
+            if (over != 0) {
+                // exact row maximum, then one walk with every score <= m
+                float mx = -INFINITY;
+                static_for<0, NPAIR>([&](auto PI) {
+                    FWD_FENCE_A();
+                    if constexpr (!STREAM && decltype(PI)::value == PFP) prefetch();
+                    f4 sv[2];
+                    scores(PI, std::false_type{}, sv, k + 1);
+                    mx = fmaxf(mx, pair_max(sv));
+                });
+                m = gmax(mx);
+                lsum = 0.f;
+                acc = f4{0.f, 0.f, 0.f, 0.f};
+                static_for<0, NPAIR>([&](auto PI) {
+                    FWD_FENCE_A();
+                    f4 sv[2];
+                    scores(PI, std::true_type{}, sv, k + 2);
+                    apply(PI, sv);
+                });
+            }
             const float l = gsum(lsum);
             const float inv = 1.f / l;
             if (rvalid) {
