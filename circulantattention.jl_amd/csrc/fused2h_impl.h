@@ -38,6 +38,9 @@
 // interleaves blocks and runs out of registers); the forward fences its apply
 // pairs but lets the score products of a chunk schedule freely (measured best
 // on gfx950: fences everywhere cost 4%, none at all 7%).
+#ifndef CIRCATT_F2H_SGB
+#define CIRCATT_F2H_SGB 0
+#endif
 #ifndef CIRCATT_F2H_FWD_FENCE
 #define CIRCATT_F2H_FWD_FENCE 2
 #endif
@@ -421,10 +424,43 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         if constexpr (MODE == FWD) {
             float m = 0.f, lsum = 0.f;
             f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-            // scores of block b (pair slot u) relative to m, masked to -inf
-            // outside the window (dep: a per-walk value for the lane masks,
-            // so that walks do not share, and keep live, each other's masks)
-            auto scores = [&](auto PI, auto REL, f4 (&sv)[2], int dep) {
+            // LDS operands of a pair: score rows of its two blocks, apply rows
+            // (values), and the Distance key biases
+            struct POps {
+                h8 a[2];
+                h4 vh[2], vl[2];
+                f4 kb[2];
+            };
+            auto load_a = [&](auto PI, POps &o) {
+                constexpr int pi = decltype(PI)::value;
+                constexpr int b0 = 2 * pi;
+                constexpr int b1 = b0 + 1 < NBLK ? b0 + 1 : b0;
+                constexpr int a0 = (2 * (b0 / NKW) + CR * 8 * (b0 % NKW)) * KS * 2;
+                constexpr int a1 = (2 * (b1 / NKW) + CR * 8 * (b1 % NKW)) * KS * 2;
+                o.a[0] = *reinterpret_cast<const h8 *>(pA0 + a0);
+                o.a[1] = *reinterpret_cast<const h8 *>(pA0 + a1);
+                if constexpr (DIST) {
+                    o.kb[0] = scal(std::integral_constant<int, b0>{}, pS0);
+                    o.kb[1] = scal(std::integral_constant<int, b1>{}, pS0);
+                }
+            };
+            auto load_v = [&](auto PI, POps &o) {
+                constexpr int pi = decltype(PI)::value;
+                constexpr int b0 = 2 * pi;
+                constexpr int b1 = b0 + 1 < NBLK ? b0 + 1 : b0;
+                trows(std::integral_constant<int, b0>{}, pR1, o.vh[0], o.vl[0]);
+                trows(std::integral_constant<int, b1>{}, pR1, o.vh[1], o.vl[1]);
+            };
+            auto load_ops = [&](auto PI) {
+                POps o;
+                load_a(PI, o);
+                load_v(PI, o);
+                return o;
+            };
+            // scores of the pair's blocks relative to m, masked to -inf outside
+            // the window (dep: a per-walk value for the lane masks, so that
+            // walks do not share, and keep live, each other's masks)
+            auto scores_ops = [&](auto PI, auto REL, const POps &o, f4 (&sv)[2], int dep) {
                 constexpr int pi = decltype(PI)::value;
                 constexpr bool rel = decltype(REL)::value;
                 constexpr int b0 = 2 * pi;
@@ -433,9 +469,10 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     constexpr int b = decltype(B)::value;
                     constexpr int bi = b / NKW, bj = b % NKW;
                     f4 init = f4{0.f, 0.f, 0.f, 0.f};
-                    if constexpr (DIST) init = scal(B, pS0);
+                    if constexpr (DIST) init = o.kb[u];
                     if constexpr (rel) init = init - f4{m, m, m, m};
-                    f4 x = score(B, pA0, r0h, r0l, init);
+                    init = mfmah(o.a[u], r0h, init);
+                    f4 x = mfmah(o.a[u], r0l, init);
                     x[0] = mask_sel_d<lane_mask(P, bi, bj, 0)>(x[0], -INFINITY, dep);
                     x[1] = mask_sel_d<lane_mask(P, bi, bj, 1)>(x[1], -INFINITY, dep);
                     x[2] = mask_sel_d<lane_mask(P, bi, bj, 2)>(x[2], -INFINITY, dep);
@@ -455,10 +492,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 return fmaxf(fmaxf(a0, a1), fmaxf(sv[1][2], sv[1][3]));
             };
             // probabilities exp2(sv) of a pair into the sums and the output
-            auto apply = [&](auto PI, const f4 (&sv)[2]) {
-                constexpr int pi = decltype(PI)::value;
-                constexpr int b0 = 2 * pi;
-                constexpr int b1 = b0 + 1 < NBLK ? b0 + 1 : b0;
+            auto apply_ops = [&](const POps &o, const f4 (&sv)[2]) {
                 float p[2][4];
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
@@ -470,16 +504,17 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 h4 ph0, pl0, ph1, pl1;
                 split4(p[0], ph0, pl0);
                 split4(p[1], ph1, pl1);
-                h4 t0h, t0l, t1h, t1l;
-                trows(std::integral_constant<int, b0>{}, pR1, t0h, t0l);
-                trows(std::integral_constant<int, b1>{}, pR1, t1h, t1l);
-                const h8 vh = cat(t0h, t1h), vl = cat(t0l, t1l);
+                const h8 vh = cat(o.vh[0], o.vh[1]), vl = cat(o.vl[0], o.vl[1]);
                 const h8 ph = cat(ph0, ph1), pl = cat(pl0, pl1);
                 acc = mfmah(vh, ph, acc);
                 acc = mfmah(vh, pl, acc);
                 acc = mfmah(vl, ph, acc);
                 return ps;
             };
+            auto scores = [&](auto PI, auto REL, f4 (&sv)[2], int dep) {
+                scores_ops(PI, REL, load_ops(PI), sv, dep);
+            };
+            auto apply = [&](auto PI, const f4 (&sv)[2]) { return apply_ops(load_ops(PI), sv); };
             // Scores relative to a reference maximum m, folded into the MFMA's
             // initial accumulator.  The first walk takes m from the central
             // pair PC (block row 4: rows 8, 9 of the key region lie in every
@@ -491,25 +526,51 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             constexpr int PC = STREAM ? 4 : 0;
             uint64_t over = 1;
             if constexpr (STREAM) {
-                {
-                    f4 sv[2];
-                    scores(std::integral_constant<int, PC>{}, std::false_type{}, sv, k);
-                    m = gmax(pair_max(sv));
-                    sv[0] = sv[0] - f4{m, m, m, m};
-                    sv[1] = sv[1] - f4{m, m, m, m};
-                    apply(std::integral_constant<int, PC>{}, sv);
-                }
+                // Walk order: PC, then the other pairs.  Skewed by one pair:
+                // an iteration takes the scores of the next pair (MFMA) beside
+                // the softmax of the current one (vector ALU), so that the two
+                // units have independent work; the score rows of the pair
+                // after next and the value rows of the next pair are read from
+                // LDS one iteration ahead.
+                constexpr auto ord = [](int i) { return i == 0 ? PC : (i - 1 < PC ? i - 1 : i); };
+                f4 sv[2];
+                POps ca, cv;  // score rows of the next pair, value rows of the current
+                load_a(std::integral_constant<int, PC>{}, ca);
+                load_v(std::integral_constant<int, PC>{}, cv);
+                scores_ops(std::integral_constant<int, PC>{}, std::false_type{}, ca, sv, k);
+                m = gmax(pair_max(sv));
+                sv[0] = sv[0] - f4{m, m, m, m};
+                sv[1] = sv[1] - f4{m, m, m, m};
+                load_a(std::integral_constant<int, ord(1)>{}, ca);
                 over = 0;
-                static_for<0, NPAIR>([&](auto PI) {
-                    constexpr int pi = decltype(PI)::value;
-                    if constexpr (pi != PC) {
-                        FWD_FENCE_A();
-                        if constexpr (pi == PFP) prefetch();
-                        f4 sv[2];
-                        scores(PI, std::true_type{}, sv, k);
-                        const float ps = apply(PI, sv);
-                        over |= __builtin_amdgcn_ballot_w64(!(ps <= 256.f));
+                static_for<0, NPAIR>([&](auto I) {
+                    constexpr int i = decltype(I)::value;
+                    constexpr int pi = ord(i);
+                    FWD_FENCE_A();
+                    if constexpr (pi == PFP) prefetch();
+                    POps na, nv;
+                    if constexpr (i + 2 < NPAIR) load_a(std::integral_constant<int, ord(i + 2)>{}, na);
+                    if constexpr (i + 1 < NPAIR) load_v(std::integral_constant<int, ord(i + 1)>{}, nv);
+                    f4 svn[2];
+                    if constexpr (i + 1 < NPAIR)
+                        scores_ops(std::integral_constant<int, ord(i + 1)>{}, std::true_type{}, ca, svn, k);
+                    const float ps = apply_ops(cv, sv);
+                    if constexpr (i > 0) over |= __builtin_amdgcn_ballot_w64(!(ps <= 256.f));
+                    if constexpr (i + 1 < NPAIR) {
+                        sv[0] = svn[0];
+                        sv[1] = svn[1];
+                        cv = nv;
                     }
+                    if constexpr (i + 2 < NPAIR) ca = na;
+#if CIRCATT_F2H_SGB
+                    // issue order: LDS reads, then MFMAs one at a time with
+                    // vector instructions between them
+                    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+                    static_for<0, 7>([&](auto) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, CIRCATT_F2H_SGB, 0);
+                    });
+#endif
                 });
             }
             if (over != 0) {
