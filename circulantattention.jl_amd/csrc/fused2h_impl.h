@@ -79,27 +79,32 @@ __device__ __forceinline__ f4 mfmah(h8 a, h8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// hi = f16(x), lo = f16(x - hi): v_fma_mixlo_f16 / v_fma_mixhi_f16 form
-// x - hi exactly in Float32 from the packed halves and round it once into
-// the low / high half of lo.  The compiler inserts no wait states around
-// inline asm, so the asm keeps to registers whose hazards are settled:
-//   * x0 and x1 are read first by the conversion that forms hi, which
-//     therefore stands between their producer (an MFMA or a transcendental
-//     among them) and the asm;
-//   * lo is written into the register of x0 (tied operand), which no
-//     in-flight MFMA can be reading;
-//   * the trailing s_nop 1 gives the 2 wait states an MFMA needs before it
-//     reads a VGPR written by a vector instruction.
+// -1.0f the compiler cannot see: fma(h, -1, x) with a literal -1 folds to
+// x - h, which loses the mixed-precision form below (the SALU move is hoisted
+// to one SGPR).
+__device__ __forceinline__ float opaque_neg_one() {
+    float c;
+    asm("s_mov_b32 %0, -1.0" : "=s"(c));
+    return c;
+}
+// hi = f16(x), lo = f16(x - hi): one packed conversion for hi, then
+// v_fma_mixlo_f16 / v_fma_mixhi_f16 take x - hi exactly in Float32 from the
+// packed halves and round it once into each half of lo.  Only empty asm
+// statements steer the instruction selection (the first keeps hi one packed
+// value for both mixes, the second keeps the two halves of lo from being
+// combined into two mix_f32 and a packed conversion), so the mixes are
+// ordinary compiler instructions and the compiler inserts the wait states
+// they need next to matrix-core operations.
 __device__ __forceinline__ void split2(float x0, float x1, h2 &hi, h2 &lo) {
-    hi = h2{(_Float16)x0, (_Float16)x1};
-    float t = x0;
-    asm("v_fma_mixlo_f16 %0, %1, -1.0, %0 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
-        : "+v"(t)
-        : "v"(hi));
-    asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\ts_nop 1"
-        : "+v"(t)
-        : "v"(hi), "v"(x1));
-    lo = __builtin_bit_cast(h2, t);
+    const float m1 = opaque_neg_one();
+    h2 h = h2{(_Float16)x0, (_Float16)x1};
+    asm("" : "+v"(h));
+    h2 l;
+    l[0] = (_Float16)__builtin_fmaf((float)h[0], m1, x0);
+    asm("" : "+v"(l));
+    l[1] = (_Float16)__builtin_fmaf((float)h[1], m1, x1);
+    hi = h;
+    lo = l;
 }
 // 4 values -> hi, lo as one half of a pair operand
 __device__ __forceinline__ void split4(const float (&x)[4], h4 &hi, h4 &lo) {
