@@ -92,6 +92,103 @@ def cpu_baseline(name, budget_s=12.0):
     }
 
 
+# Unfused entry points (the Circulant-materialising path), HBM-bound: name ->
+# (spatial, C per unit, nb units, ws, complex).  cfg2 is the reference README's
+# 128x96x64x2 ws=15 similarity; cfg5's units are its 2 heads x 2 batches of
+# ComplexF32 with 16 channels per head (A + m*B and C ⨷ v of README.md:130).
+OPS_CONFIGS = {
+    "cfg2": ((128, 96), 64, 2, 15, False),
+    "cfg5": ((320, 320), 16, 4, 11, True),
+}
+
+
+def bench_ops(args):
+    """Time every unfused entry point at the OPS_CONFIGS shapes with HIP events
+    on the launch stream; one JSON line per (config, entry point) with the
+    algorithmic HBM bytes (each input read once, each output written once) over
+    the average launch time against MI355X's 8 TB/s."""
+    import torch
+
+    from circulant_attention import _lib as L
+    from circulant_attention._functions import ptr
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    g = torch.Generator(device=dev)
+    g.manual_seed(2000)
+    for name, (dims, C, nb, ws, cplx) in OPS_CONFIGS.items():
+        nsp = len(dims)
+        n1, n2 = dims[0], (dims[1] if nsp == 2 else 1)
+        P = int(math.prod(dims))
+        K = ws ** nsp
+        nnz = P * K * nb
+        dt = L.C32 if cplx else L.F32
+        dtype = torch.complex64 if cplx else torch.float32
+        shape = (nb, C, *reversed(dims))
+        x, y, z, dx, dy = (torch.randn(shape, device=dev, dtype=dtype, generator=g)
+                           for _ in range(5))
+        T = x.numel() * x.element_size()
+        A, B, Z = (torch.rand((nb, P, K), device=dev, generator=g) for _ in range(3))
+        rowptr = torch.empty((nb, P + 1), device=dev, dtype=torch.int32)
+        colval = torch.empty((nb, P * K), device=dev, dtype=torch.int32)
+        sums = torch.empty((nb, P), device=dev)
+        m = torch.randn(nb, device=dev, generator=g)
+        s = 1.0 / math.sqrt(C)
+        ops = [
+            ("pattern", 4 * (P + 1) * nb + 4 * nnz,
+             lambda: L.lib.circatt_pattern(nsp, n1, n2, ws, nb, ptr(rowptr), ptr(colval), sp)),
+            ("similarity_dot", 2 * T + 4 * nnz,
+             lambda: L.lib.circatt_similarity(L.DOT, dt, nsp, n1, n2, ws, C, nb, s, ptr(x),
+                                              ptr(y), ptr(A), sp)),
+            ("softmax", 8 * nnz,
+             lambda: L.lib.circatt_softmax(K, P * nb, ptr(A), ptr(Z), sp)),
+            ("softmax_bwd", 12 * nnz,
+             lambda: L.lib.circatt_softmax_bwd(K, P * nb, ptr(A), ptr(B), ptr(Z), sp)),
+            ("apply", 4 * nnz + 2 * T,
+             lambda: L.lib.circatt_apply(0, dt, nsp, n1, n2, ws, C, nb, ptr(A), ptr(x), ptr(z),
+                                         sp)),
+            ("apply_transposed", 4 * nnz + 2 * T,
+             lambda: L.lib.circatt_apply(1, dt, nsp, n1, n2, ws, C, nb, ptr(A), ptr(x), ptr(z),
+                                         sp)),
+            ("similarity_bwd_dot", 4 * nnz + 4 * T,
+             lambda: L.lib.circatt_similarity_bwd(L.DOT, dt, nsp, n1, n2, ws, C, nb, s, ptr(B),
+                                                  ptr(x), ptr(y), ptr(dx), ptr(dy), sp)),
+            ("similarity_bwd_distance", 4 * nnz + 4 * T,
+             lambda: L.lib.circatt_similarity_bwd(L.DISTANCE, dt, nsp, n1, n2, ws, C, nb, s,
+                                                  ptr(B), ptr(x), ptr(y), ptr(dx), ptr(dy), sp)),
+            ("rowsum", 4 * nnz + 4 * P * nb,
+             lambda: L.lib.circatt_rowsum(nsp, n1, n2, ws, nb, ptr(A), ptr(sums), sp)),
+            ("colsum", 4 * nnz + 4 * P * nb,
+             lambda: L.lib.circatt_colsum(nsp, n1, n2, ws, nb, ptr(A), ptr(sums), sp)),
+            ("axpby_scaled", 12 * nnz,  # C = A + m*B, m per (head, batch)
+             lambda: L.lib.circatt_axpby(P * K, nb, None, 1.0, ptr(A), ptr(m), 0.0, ptr(B),
+                                         ptr(Z), sp)),
+        ]
+        for op, nbytes, f in ops:
+            for _ in range(args.warmup):
+                L.check(f())
+            torch.cuda.synchronize()
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(args.steps)]
+            for e0, e1 in evs:
+                e0.record(stream)
+                L.check(f())
+                e1.record(stream)
+            torch.cuda.synchronize()
+            ts = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
+            avg = sum(ts) / len(ts)
+            gbs = nbytes / (avg / 1e3) / 1e9
+            print(json.dumps({
+                "op": op, "config": name, "spatial": list(dims), "C": C, "nb": nb, "ws": ws,
+                "dtype": "c32" if cplx else "f32", "nnz": nnz, "avg_us": round(avg * 1e3, 2),
+                "min_us": round(ts[0] * 1e3, 2), "alg_bytes": nbytes,
+                "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                             "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}}), flush=True)
+        del x, y, z, dx, dy, A, B, Z, rowptr, colval
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,11 +199,18 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed region, run 3 device copies of this many MiB "
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--ops", action="store_true",
+                    help="instead of the fused step, time each unfused entry point (similarity, "
+                         "softmax, apply, sums, axpby, pattern) at the cfg2 / cfg5 shapes and "
+                         "print one JSON line per entry point (GB/s against HBM peak)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the (head, batch) units "
                                    "shard across GPUs without communication, see DESIGN.md"}))
         sys.exit(2)
+    if args.ops:
+        bench_ops(args)
+        return
 
     import torch
 

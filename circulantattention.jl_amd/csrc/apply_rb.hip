@@ -1,0 +1,698 @@
+// Sparse apply for windows of width 3 .. 15:
+//   TRANS = false: y[c] = sum_d A[c, slot(c, d)] x[c + d]            (A ⊗ x)
+//   TRANS = true : y[c] = sum_d A[c - d, slot(c - d, d)] x[c - d]    (Aᵀ ⊗ x)
+// optionally minus (sum of the A entries used) .* z (Distance rrule), times
+// scale; and sum(A; dims=1).  Replaces the CUSPARSE.bmm! products of
+// src/batchedmul.jl:82-110 and the column sum of src/array.jl:119-130.
+//
+// nzVal (K floats per pixel) dominates the bytes, so it is read with
+// coalesced loads and everything else is arranged around that:
+//   * a wavefront owns 4 lane rows of 64 pixels (a 64 x 4 tile in 2D, 256
+//     pixels of the line in 1D); each lane owns 4 consecutive pixels of its
+//     lane row, so for one window row d2 it applies 4 x ws products per
+//     component to one run of 4 + 2p values of x;
+//   * per window row, the lane row's 64 pixels' slot chunks (ws contiguous
+//     floats each; 64 + 2p source pixels for the transposed product) are
+//     loaded 16 lanes per chunk, written to a wave-private LDS buffer and read
+//     back by the lanes that own the pixels.  The read offsets carry the
+//     reference's circular shift of the slot order near borders
+//     (src/circulant.jl:6-44);
+//   * x runs are 16-byte buffer loads from L1 (4 + 2p values, wrapped near the
+//     borders of dim 1 through a per-lane column table).
+#include <algorithm>
+
+#include "circatt_common.h"
+#include "circatt_kernels.h"
+
+extern __shared__ __attribute__((aligned(16))) float circatt_lds_apply[];
+
+namespace circatt {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kR = 4;     // pixels per lane along dim 1
+constexpr int kCC = 8;    // real components per chunk of the whole-row kernel
+constexpr int kCP = 8;    // real components per staging pass of the chunked kernel
+constexpr unsigned kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data
+
+struct ApplyArgs {
+    Geom g;
+    int C;           // channels per unit
+    int corr;        // subtract sums(A) .* z
+    int tiles1, tiles2;
+    int fa, fb;      // tile columns [fa, fb) are interior
+    int gchunk;      // chunk groups on the grid
+    int ichunk;      // chunks per wavefront
+    float scale;
+    const float *nz, *x, *z;
+    float *y;
+};
+
+__host__ __device__ constexpr int tile_w(int nsp) { return nsp == 2 ? 64 : 256; }
+__host__ __device__ constexpr int tile_h(int nsp) { return nsp == 2 ? 4 : 1; }
+// staged source pixels per lane row and LDS floats per wavefront
+__host__ __device__ constexpr int nsrc(int ws, bool trans) { return trans ? 64 + ws - 1 : 64; }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const float *p, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), (short)0, (int)bytes,
+                                             kRsrcWord3);
+}
+__device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ f4 bload4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// Per-lane geometry shared by the apply and the column sum.
+template <int WS>
+struct Lane {
+    static constexpr int P = (WS - 1) / 2;
+    int l16, rho;   // lane within its lane row, lane row
+    int f1;         // first column of the lane row
+    int c2;         // image row of the lane row (wrapped into range)
+    bool row_ok;
+    __device__ Lane(const Geom &g, int t1, int t2) {
+        const int lane = threadIdx.x & 63;
+        l16 = lane & 15;
+        rho = lane >> 4;
+        const bool two = g.nsp == 2;
+        f1 = two ? t1 * 64 : t1 * 256 + 64 * rho;
+        const int c2u = two ? t2 * 4 + rho : 0;
+        row_ok = c2u < g.n2;
+        c2 = row_ok ? c2u : c2u % g.n2;
+    }
+    __device__ int col(int i) const { return f1 + 4 * l16 + i; }
+};
+
+// Stages the slot chunks of one window row into the wavefront's LDS buffer
+// with LDS-DMA buffer loads (no registers): chunk u (0 <= u < NS) of source
+// column f1 - off + u (wrapped) of each lane row.  A load instruction covers
+// chunk u of all 4 lane rows; lane 4 e + r loads element e of lane row r, and
+// the instruction's 64 dwords land at u * kPU, so element e of chunk u of lane
+// row r sits at u * kPU + 4 e + r.  With kPU = 65 the owners' reads
+// (u = 4 l16 + i, lane row r) fall in 64 different banks.
+constexpr int kPU = 65;
+__host__ __device__ constexpr int lds_floats(int ws, bool trans) { return nsrc(ws, trans) * kPU; }
+
+template <int WS, int NS, bool FAST>
+__device__ __forceinline__ void stage_dma(float *lw, const Geom &g, __amdgpu_buffer_rsrc_t rs,
+                                          int f1r, int r2r, int mmr, int off, int k4) {
+    const int e = min((int)(threadIdx.x & 63) >> 2, WS - 1);
+    typedef __attribute__((address_space(3))) void *lptr;
+    // each load's offset is formed right before it (fences keep the
+    // scheduler from computing all of them up front into registers)
+    if (FAST) {
+        const int vo = (f1r - off + g.n1 * r2r) * k4 + (mmr * WS + e) * 4;
+        int so = 0;
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(lw + u * kPU), 4, vo,
+                                                    __builtin_amdgcn_readfirstlane(so), 0, 0);
+            so += k4;
+        }
+    } else {
+        const int vo = g.n1 * r2r * k4 + (mmr * WS + e) * 4;
+        int c = pmod(f1r - off, g.n1);
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(lw + u * kPU), 4, vo + c * k4, 0,
+                                                    0, 0);
+            c = c + 1 == g.n1 ? 0 : c + 1;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// s_waitcnt encodings (gfx9): all counters, LDS/scalar counter only
+constexpr int kWaitAll = 0;
+constexpr int kWaitLgkm = 0x0070 | 0xC000 | 0x000F;  // lgkmcnt(0), vmcnt and expcnt at max
+
+// Geometry of the lane row whose chunks this lane stages (lane & 3) and the
+// window row's chunk row / chunk index for it.
+template <int WS>
+__device__ __forceinline__ void staging_row(const Geom &g, int t1, int t2, int dd, bool trans,
+                                            int &f1r, int &r2r, int &mmr) {
+    constexpr int P = (WS - 1) / 2;
+    const int r = threadIdx.x & 3;
+    const bool two = g.nsp == 2;
+    f1r = two ? t1 * 64 : t1 * 256 + 64 * r;
+    if (two) {
+        const int c2u = t2 * 4 + r;
+        const int c2 = c2u < g.n2 ? c2u : c2u % g.n2;
+        r2r = trans ? pmod(c2 - (dd - P), g.n2) : c2;
+        mmr = pmod(dd + slot_shift(r2r + 1, g.n2, P), WS);
+    } else {
+        r2r = 0;
+        mmr = 0;
+    }
+}
+
+// slot_shift of 0-based column c (same case order as slot_shift)
+__device__ __forceinline__ int shift0(int c, int n, int p) {
+    return c + 1 <= p ? c - p : (c + 1 > n - p ? p - n + c + 1 : 0);
+}
+// j + s folded into [0, ws) for |s| <= p < ws
+__device__ __forceinline__ int fold(int v, int ws) {
+    return v < 0 ? v + ws : (v >= ws ? v - ws : v);
+}
+
+template <int WS, int NCOMP, bool TRANS, bool FAST>
+__device__ __forceinline__ void apply_body(const ApplyArgs &a, int gc, int t1, int t2, int b) {
+    using L_ = Lane<WS>;
+    constexpr int P = L_::P;
+    constexpr int XW = kR + 2 * P;                 // x run per lane
+    constexpr int XN = NCOMP * XW;                 // floats of one run
+    constexpr int XN4 = (XN + 3) / 4;
+    constexpr int NS = nsrc(WS, TRANS);
+    constexpr int CCH = kCP / NCOMP;               // channels per staging pass
+    const Geom &g = a.g;
+    const bool two = g.nsp == 2;
+    const int n1 = g.n1, n2 = g.n2, K = g.K;
+    const int64_t Pp = g.P;
+    const L_ L(g, t1, t2);
+    float *lw = circatt_lds_apply;
+    const auto rs = rsrc(a.nz + (int64_t)b * Pp * K, Pp * K * 4);
+    const auto rx = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, Pp * NCOMP * a.C * 4);
+    const int nd2 = two ? WS : 1;
+
+    // x run of channel c for window row dd
+    auto load_x = [&](float (&xw)[4 * XN4], int c, int dd, int f1) {
+        const int d2 = dd - P;
+        const int xr2 = two ? pmod(TRANS ? L.c2 - d2 : L.c2 + d2, n2) : 0;
+        const int cw = c < a.C ? c : a.C - 1;
+        const int rowoff = (int)(NCOMP * ((int64_t)n1 * xr2 + Pp * cw)) * 4;
+        if (FAST) {
+            const int vo = rowoff + NCOMP * (f1 + 4 * L.l16 - P) * 4;
+#pragma unroll
+            for (int q = 0; q < XN4; ++q) {
+                const f4 v = bload4(rx, vo, 16 * q);
+                xw[4 * q] = v[0];
+                xw[4 * q + 1] = v[1];
+                xw[4 * q + 2] = v[2];
+                xw[4 * q + 3] = v[3];
+            }
+        } else {
+            int xc = pmod(f1 + 4 * L.l16 - P, n1);
+#pragma unroll
+            for (int w = 0; w < XW; ++w) {
+#pragma unroll
+                for (int e = 0; e < NCOMP; ++e)
+                    xw[NCOMP * w + e] = bload(rx, rowoff + (NCOMP * xc + e) * 4, 0);
+                xc = xc + 1 == n1 ? 0 : xc + 1;
+            }
+        }
+    };
+    auto stage = [&](int dd, int k4) {
+        int f1r, r2r, mmr;
+        staging_row<WS>(g, t1, t2, dd, TRANS, f1r, r2r, mmr);
+        stage_dma<WS, NS, FAST>(lw, g, rs, f1r, r2r, mmr, TRANS ? P : 0, k4);
+    };
+
+    for (int ci = 0; ci < a.ichunk; ++ci) {
+        const int k0 = (gc * a.ichunk + ci) * kCP;
+        if (k0 >= NCOMP * a.C) break;
+        float acc[kR][kCP];
+        float asum[kR];
+#pragma unroll
+        for (int i = 0; i < kR; ++i) {
+            asum[i] = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < kCP; ++kk) acc[i][kk] = 0.f;
+        }
+        // the buffer is free: the previous chunk's reads completed before
+        // its last products
+        stage(0, 4 * K);
+        for (int dd = 0; dd < nd2; ++dd) {
+            // f1 and k4 are redefined in every iteration so that per-chunk
+            // and per-column offsets are recomputed here instead of being
+            // hoisted out of the loop as tables of registers
+            int f1 = L.f1, k4 = 4 * K;
+            asm volatile("" : "+v"(f1), "+s"(k4));
+            __builtin_amdgcn_s_waitcnt(kWaitAll);  // this window row's chunks are in LDS
+            float av[kR][WS];
+#pragma unroll
+            for (int i = 0; i < kR; ++i) {
+                // border body: wrapped source column of offset j, stepped
+                // from one modulo per pixel
+                int c1 = 0, s1 = 0;
+                if (!FAST) {
+                    c1 = pmod(f1 + 4 * L.l16 + i + (TRANS ? P : 0), n1);
+                    if (!TRANS) s1 = shift0(c1, n1, P);
+                }
+#pragma unroll
+                for (int j = 0; j < WS; ++j) {
+                    const int u = TRANS ? 4 * L.l16 + i - j + 2 * P : 4 * L.l16 + i;
+                    int pos = j;
+                    if (!FAST) {
+                        if (TRANS) {
+                            pos = fold(j + shift0(c1, n1, P), WS);
+                            c1 = c1 == 0 ? n1 - 1 : c1 - 1;
+                        } else {
+                            pos = fold(j + s1, WS);
+                        }
+                    }
+                    av[i][j] = lw[u * kPU + 4 * pos + L.rho];
+                }
+            }
+            // every read of the buffer has returned before the next window
+            // row's chunks are loaded into it
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+            if (dd + 1 < nd2) stage(dd + 1, k4);
+            if (a.corr) {
+#pragma unroll
+                for (int i = 0; i < kR; ++i)
+#pragma unroll
+                    for (int j = 0; j < WS; ++j) asum[i] += av[i][j];
+            }
+            // products, one channel (NCOMP components) at a time; channels
+            // past C are computed on a clamped channel and not stored
+#pragma unroll
+            for (int cl = 0; cl < CCH; ++cl) {
+                float xc[4 * XN4];
+                // nothing crosses these fences, so the loads of later channels
+                // are not hoisted over the products into registers
+                __builtin_amdgcn_sched_barrier(0);
+                load_x(xc, k0 / NCOMP + cl, dd, f1);
+#pragma unroll
+                for (int i = 0; i < kR; ++i)
+#pragma unroll
+                    for (int j = 0; j < WS; ++j)
+#pragma unroll
+                        for (int e = 0; e < NCOMP; ++e)
+                            acc[i][NCOMP * cl + e] = __builtin_fmaf(
+                                av[i][j], xc[NCOMP * (TRANS ? i - j + 2 * P : i + j) + e],
+                                acc[i][NCOMP * cl + e]);
+            }
+        }
+        // store the chunk
+        float *yb = a.y + (int64_t)b * Pp * NCOMP * a.C;
+        const float *zb = a.z ? a.z + (int64_t)b * Pp * NCOMP * a.C : nullptr;
+#pragma unroll
+        for (int i = 0; i < kR; ++i) {
+            if (!L.row_ok || L.col(i) >= n1) continue;
+            const int64_t pix = L.col(i) + (int64_t)n1 * L.c2;
+#pragma unroll
+            for (int kk = 0; kk < kCP; ++kk) {
+                const int k = k0 + kk;
+                if (k >= NCOMP * a.C) break;
+                const int c = k / NCOMP, e = k - c * NCOMP;
+                const int64_t idx = NCOMP * (pix + Pp * c) + e;
+                float v = acc[i][kk];
+                if (a.corr) v -= asum[i] * zb[idx];
+                yb[idx] = v * a.scale;
+            }
+        }
+    }
+}
+
+// One wavefront per (chunk group, 64 x 4 tile, unit).  Tile columns [fa, fb)
+// lie 2p or more inside dim 1 (no wrap of x or of source rows, no slot shift)
+// and take the interior body, whose offsets are immediates; the others take
+// the border body, which computes wrapped columns and shifted slots per value.
+template <int WS, int NCOMP, bool TRANS>
+__global__ __launch_bounds__(64, 2) void apply_rb_kernel(ApplyArgs a) {
+    // item indices (integer division runs on the vector unit: bring the
+    // results back to scalar registers, or every buffer load whose descriptor
+    // derives from them is wrapped in a readfirstlane loop)
+    int it = blockIdx.x;
+    const int gc = __builtin_amdgcn_readfirstlane(it % a.gchunk);
+    it /= a.gchunk;
+    const int t1 = __builtin_amdgcn_readfirstlane(it % a.tiles1);
+    it /= a.tiles1;
+    const int t2 = __builtin_amdgcn_readfirstlane(it % a.tiles2);
+    const int b = __builtin_amdgcn_readfirstlane(it / a.tiles2);
+    if (t1 >= a.fa && t1 < a.fb)
+        apply_body<WS, NCOMP, TRANS, true>(a, gc, t1, t2, b);
+    else
+        apply_body<WS, NCOMP, TRANS, false>(a, gc, t1, t2, b);
+}
+
+// sum(A; dims=1): out[c] = sum over window offsets d of A[c - d, slot(c - d, d)]
+template <int WS, bool FAST>
+__device__ __forceinline__ void colsum_body(const Geom &g, int t1, int t2, int b, const float *nz,
+                                            float *out) {
+    using L_ = Lane<WS>;
+    constexpr int P = L_::P;
+    constexpr int NS = nsrc(WS, true);
+    const bool two = g.nsp == 2;
+    const int n1 = g.n1, K = g.K;
+    const L_ L(g, t1, t2);
+    float *lw = circatt_lds_apply;
+    const auto rs = rsrc(nz + (int64_t)b * g.P * K, g.P * K * 4);
+    float s[kR] = {0.f, 0.f, 0.f, 0.f};
+    const int nd2 = two ? WS : 1;
+    auto stage = [&](int dd, int k4) {
+        int f1r, r2r, mmr;
+        staging_row<WS>(g, t1, t2, dd, true, f1r, r2r, mmr);
+        stage_dma<WS, NS, FAST>(lw, g, rs, f1r, r2r, mmr, P, k4);
+    };
+    stage(0, 4 * K);
+    for (int dd = 0; dd < nd2; ++dd) {
+        int f1 = L.f1, k4 = 4 * K;
+        asm volatile("" : "+v"(f1), "+s"(k4));
+        __builtin_amdgcn_s_waitcnt(kWaitAll);
+        float v[kR][WS];
+#pragma unroll
+        for (int i = 0; i < kR; ++i)
+#pragma unroll
+            for (int j = 0; j < WS; ++j) {
+                const int u = 4 * L.l16 + i - j + 2 * P;
+                int pos = j;
+                if (!FAST) pos = fold(j + shift0(pmod(f1 - P + u, n1), n1, P), WS);
+                v[i][j] = lw[u * kPU + 4 * pos + L.rho];
+            }
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+        if (dd + 1 < nd2) stage(dd + 1, k4);
+#pragma unroll
+        for (int i = 0; i < kR; ++i)
+#pragma unroll
+            for (int j = 0; j < WS; ++j) s[i] += v[i][j];
+    }
+#pragma unroll
+    for (int i = 0; i < kR; ++i)
+        if (L.row_ok && L.col(i) < n1) out[(int64_t)b * g.P + L.col(i) + (int64_t)n1 * L.c2] = s[i];
+}
+
+template <int WS>
+__global__ __launch_bounds__(64, 2) void colsum_rb_kernel(Geom g, int tiles1, int tiles2, int fa,
+                                                          int fb, const float *nz, float *out) {
+    int it = blockIdx.x;
+    const int t1 = __builtin_amdgcn_readfirstlane(it % tiles1);
+    it /= tiles1;
+    const int t2 = __builtin_amdgcn_readfirstlane(it % tiles2);
+    const int b = __builtin_amdgcn_readfirstlane(it / tiles2);
+    if (t1 >= fa && t1 < fb)
+        colsum_body<WS, true>(g, t1, t2, b, nz, out);
+    else
+        colsum_body<WS, false>(g, t1, t2, b, nz, out);
+}
+
+// ---------------------------------------------------------------------------
+// A ⊗ x in 2D with whole rows of nzVal: a wavefront owns 64 consecutive pixels
+// of one image row, whose nzVal rows are 64 K contiguous floats; they are
+// staged into LDS once (LDS-DMA, fully coalesced) and serve every component
+// chunk.  The four lane groups take every fourth window row (lane 16 r + l
+// owns pixels 4 l .. 4 l + 3 for window rows r, r + 4, ...) and their partial
+// sums are added across the groups at the end of a chunk.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float group4_sum(float v) {
+    unsigned u = __float_as_uint(v);
+    auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    u = __float_as_uint(v);
+    auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+template <int WS>
+__host__ __device__ constexpr int rows_lds_floats() { return 64 * WS * WS; }
+
+template <int WS, int NCOMP, bool FAST>
+__device__ __forceinline__ void rows_body(const ApplyArgs &a, int gc, int t1, int c2, int b) {
+    constexpr int P = (WS - 1) / 2;
+    constexpr int K = WS * WS;
+    constexpr int XW = kR + 2 * P;
+    constexpr int XN = NCOMP * XW;
+    constexpr int XN4 = (XN + 3) / 4;
+    constexpr int CCH = kCC / NCOMP;
+    constexpr int NIT = (WS + 3) / 4;  // window rows per lane group
+    typedef __attribute__((address_space(3))) void *lptr;
+    const Geom &g = a.g;
+    const int n1 = g.n1, n2 = g.n2;
+    const int64_t Pp = g.P;
+    const int lane = threadIdx.x & 63;
+    const int l16 = lane & 15, rho = lane >> 4;
+    const int f1 = t1 * 64;
+    float *lw = circatt_lds_apply;
+    const auto rs = rsrc(a.nz + (int64_t)b * Pp * K, Pp * K * 4);
+    const auto rx = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, Pp * NCOMP * a.C * 4);
+
+    // stage the 64 rows (pixels f1 .. f1 + 63 of image row c2; rows past the
+    // image row or the unit are never stored, the buffer bound zeroes reads
+    // past the unit)
+    {
+        const int vo = (int)((f1 + (int64_t)n1 * c2) * K * 4) + lane * 4;
+        int so = 0;
+#pragma unroll
+        for (int q = 0; q < K; ++q) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(lw + 64 * q), 4, vo,
+                                                    __builtin_amdgcn_readfirstlane(so), 0, 0);
+            so += 256;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // slot shift of the lane's pixels (border body)
+    int s1[kR];
+#pragma unroll
+    for (int i = 0; i < kR; ++i) s1[i] = FAST ? 0 : shift0(pmod(f1 + 4 * l16 + i, n1), n1, P);
+    const int s2 = slot_shift(c2 + 1, n2, P);
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+
+    auto load_x = [&](float (&xw)[4 * XN4], int c, int xr2) {
+        const int cw = c < a.C ? c : a.C - 1;
+        const int rowoff = (int)(NCOMP * ((int64_t)n1 * xr2 + Pp * cw)) * 4;
+        if (FAST) {
+            const int vo = rowoff + NCOMP * (f1 + 4 * l16 - P) * 4;
+#pragma unroll
+            for (int q = 0; q < XN4; ++q) {
+                const f4 v = bload4(rx, vo, 16 * q);
+                xw[4 * q] = v[0];
+                xw[4 * q + 1] = v[1];
+                xw[4 * q + 2] = v[2];
+                xw[4 * q + 3] = v[3];
+            }
+        } else {
+            int xc = pmod(f1 + 4 * l16 - P, n1);
+#pragma unroll
+            for (int w = 0; w < XW; ++w) {
+#pragma unroll
+                for (int e = 0; e < NCOMP; ++e)
+                    xw[NCOMP * w + e] = bload(rx, rowoff + (NCOMP * xc + e) * 4, 0);
+                xc = xc + 1 == n1 ? 0 : xc + 1;
+            }
+        }
+    };
+
+    const int nchunk = (NCOMP * a.C + kCC - 1) / kCC;
+    float *yb = a.y + (int64_t)b * Pp * NCOMP * a.C;
+    const float *zb = a.z ? a.z + (int64_t)b * Pp * NCOMP * a.C : nullptr;
+    const int ch1 = min(nchunk, (gc + 1) * a.ichunk);
+    for (int ch = gc * a.ichunk; ch < ch1; ++ch) {
+        const int k0 = ch * kCC;
+        float acc[kR][kCC];
+        float asum[kR];
+#pragma unroll
+        for (int i = 0; i < kR; ++i) {
+            asum[i] = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < kCC; ++kk) acc[i][kk] = 0.f;
+        }
+        for (int itr = 0; itr < NIT; ++itr) {
+            const int dd = 4 * itr + rho;
+            const bool live = dd < WS;
+            const int ddc = live ? dd : WS - 1;
+            const int xr2 = pmod(c2 + ddc - P, n2);
+            const int mm = pmod(ddc + s2, WS);
+            float av[kR][WS];
+#pragma unroll
+            for (int i = 0; i < kR; ++i)
+#pragma unroll
+                for (int j = 0; j < WS; ++j) {
+                    const int pos = FAST ? j : fold(j + s1[i], WS);
+                    const float v = lw[(4 * l16 + i) * K + mm * WS + pos];
+                    av[i][j] = live ? v : 0.f;
+                }
+            if (a.corr) {
+#pragma unroll
+                for (int i = 0; i < kR; ++i)
+#pragma unroll
+                    for (int j = 0; j < WS; ++j) asum[i] += av[i][j];
+            }
+            float xa[4 * XN4], xb[4 * XN4];
+            load_x(xa, k0 / NCOMP, xr2);
+#pragma unroll
+            for (int cl = 0; cl < CCH; ++cl) {
+                float(&xc)[4 * XN4] = (cl & 1) ? xb : xa;
+                float(&xn)[4 * XN4] = (cl & 1) ? xa : xb;
+                __builtin_amdgcn_sched_barrier(0);
+                if (cl + 1 < CCH) load_x(xn, k0 / NCOMP + cl + 1, xr2);
+#pragma unroll
+                for (int i = 0; i < kR; ++i)
+#pragma unroll
+                    for (int j = 0; j < WS; ++j)
+#pragma unroll
+                        for (int e = 0; e < NCOMP; ++e)
+                            acc[i][NCOMP * cl + e] = __builtin_fmaf(
+                                av[i][j], xc[NCOMP * (i + j) + e], acc[i][NCOMP * cl + e]);
+            }
+        }
+        // add the four lane groups' window rows; group r stores components
+        // 2 r, 2 r + 1 of the chunk
+#pragma unroll
+        for (int i = 0; i < kR; ++i) {
+            if (a.corr) asum[i] = group4_sum(asum[i]);
+#pragma unroll
+            for (int kk = 0; kk < kCC; ++kk) acc[i][kk] = group4_sum(acc[i][kk]);
+        }
+#pragma unroll
+        for (int i = 0; i < kR; ++i) {
+            const int col = f1 + 4 * l16 + i;
+            if (col >= n1) continue;
+            const int64_t pix = col + (int64_t)n1 * c2;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int kk = 2 * rho + h;
+                const int k = k0 + kk;
+                if (k >= NCOMP * a.C) break;
+                const int c = k / NCOMP, e = k - c * NCOMP;
+                const int64_t idx = NCOMP * (pix + Pp * c) + e;
+                float v = acc[i][0];
+#pragma unroll
+                for (int q = 1; q < kCC; ++q) v = kk == q ? acc[i][q] : v;
+                if (a.corr) v -= asum[i] * zb[idx];
+                yb[idx] = v * a.scale;
+            }
+        }
+    }
+}
+
+// One wavefront per (64 pixels of an image row, unit).
+template <int WS, int NCOMP>
+__global__ __launch_bounds__(64, 2) void apply_rows_kernel(ApplyArgs a) {
+    int it = blockIdx.x;
+    const int gc = __builtin_amdgcn_readfirstlane(it % a.gchunk);
+    it /= a.gchunk;
+    const int t1 = __builtin_amdgcn_readfirstlane(it % a.tiles1);
+    it /= a.tiles1;
+    const int c2 = __builtin_amdgcn_readfirstlane(it % a.g.n2);
+    const int b = __builtin_amdgcn_readfirstlane(it / a.g.n2);
+    if (t1 >= a.fa && t1 < a.fb)
+        rows_body<WS, NCOMP, true>(a, gc, t1, c2, b);
+    else
+        rows_body<WS, NCOMP, false>(a, gc, t1, c2, b);
+}
+
+// Interior tile columns [fa, fb): every lane row 2p or more inside dim 1.
+inline void interior_cols(const Geom &g, int &fa, int &fb) {
+    const int tw = tile_w(g.nsp), tiles1 = (g.n1 + tw - 1) / tw;
+    const int two_p = g.ws - 1;
+    fa = (two_p + tw - 1) / tw;                 // first t1 with t1 * tw >= 2p
+    fb = (g.n1 - two_p - tw) >= 0 ? (g.n1 - two_p - tw) / tw + 1 : 0;  // t1 * tw + tw - 1 + 2p < n1
+    if (fb > tiles1) fb = tiles1;
+    if (fb < fa) fb = fa;
+}
+
+template <int WS, int NCOMP, bool TRANS>
+hipError_t launch_rb(ApplyArgs a, int64_t nb, hipStream_t s) {
+    if (!TRANS && a.g.nsp == 2) {
+        // whole-row kernel: interior when no x wrap and no slot shift
+        const int tiles1 = (a.g.n1 + 63) / 64;
+        a.tiles1 = tiles1;
+        a.fa = (a.g.p + 63) / 64;
+        a.fb = a.g.n1 - 64 - a.g.p >= 0 ? (a.g.n1 - 64 - a.g.p) / 64 + 1 : 0;
+        if (a.fb > tiles1) a.fb = tiles1;
+        if (a.fb < a.fa) a.fb = a.fa;
+        // component chunks of a row segment in one wavefront (its nzVal rows
+        // staged once) unless that leaves the GPU underfilled
+        const int nchunk = (NCOMP * a.C + kCC - 1) / kCC;
+        const int64_t waves = (int64_t)tiles1 * a.g.n2 * nb;
+        a.ichunk = waves >= 2048 ? nchunk : std::max(1, (int)((int64_t)nchunk * waves / 2048));
+        a.gchunk = (nchunk + a.ichunk - 1) / a.ichunk;
+        const int64_t grid = waves * a.gchunk;
+        hipLaunchKernelGGL((apply_rows_kernel<WS, NCOMP>), dim3((unsigned)grid), dim3(64),
+                           (size_t)rows_lds_floats<WS>() * sizeof(float), s, a);
+        return hipGetLastError();
+    }
+    const size_t lds = (size_t)lds_floats(WS, TRANS) * sizeof(float);
+    interior_cols(a.g, a.fa, a.fb);
+    const int64_t grid = (int64_t)a.gchunk * a.tiles1 * a.tiles2 * nb;
+    hipLaunchKernelGGL((apply_rb_kernel<WS, NCOMP, TRANS>), dim3((unsigned)grid), dim3(64), lds, s,
+                       a);
+    return hipGetLastError();
+}
+
+template <int NCOMP, bool TRANS>
+hipError_t dispatch_ws(const ApplyArgs &a, int64_t nb, hipStream_t s) {
+    switch (a.g.ws) {
+        case 3: return launch_rb<3, NCOMP, TRANS>(a, nb, s);
+        case 5: return launch_rb<5, NCOMP, TRANS>(a, nb, s);
+        case 7: return launch_rb<7, NCOMP, TRANS>(a, nb, s);
+        case 9: return launch_rb<9, NCOMP, TRANS>(a, nb, s);
+        case 11: return launch_rb<11, NCOMP, TRANS>(a, nb, s);
+        case 13: return launch_rb<13, NCOMP, TRANS>(a, nb, s);
+        case 15: return launch_rb<15, NCOMP, TRANS>(a, nb, s);
+        default: return hipErrorNotSupported;
+    }
+}
+
+template <int WS>
+hipError_t launch_colsum_t(const Geom &g, int64_t nb, const float *nz, float *out, hipStream_t s) {
+    const int tiles1 = (g.n1 + tile_w(g.nsp) - 1) / tile_w(g.nsp);
+    const int tiles2 = (g.n2 + tile_h(g.nsp) - 1) / tile_h(g.nsp);
+    int fa, fb;
+    interior_cols(g, fa, fb);
+    hipLaunchKernelGGL(colsum_rb_kernel<WS>, dim3((unsigned)((int64_t)tiles1 * tiles2 * nb)),
+                       dim3(64), (size_t)lds_floats(WS, true) * sizeof(float), s, g, tiles1,
+                       tiles2, fa, fb, nz, out);
+    return hipGetLastError();
+}
+
+int64_t tiles_of(const Geom &g) {
+    return (int64_t)((g.n1 + tile_w(g.nsp) - 1) / tile_w(g.nsp)) *
+           ((g.n2 + tile_h(g.nsp) - 1) / tile_h(g.nsp));
+}
+
+}  // namespace
+
+bool apply_rb_supported(const Geom &g, int C, int ncomp, int64_t nb) {
+    if (g.ws < 3 || g.ws > 15 || (g.ws & 1) == 0) return false;
+    // 32-bit byte offsets into one unit's nzVal and x, grid in one dimension
+    if (g.P * g.K * 4 >= (int64_t)1 << 31) return false;
+    if (g.P * ncomp * C * 4 >= (int64_t)1 << 31) return false;
+    const int64_t grid = tiles_of(g) * ((ncomp * C + kCC - 1) / kCC) * nb;  // upper bound
+    return grid > 0 && grid < ((int64_t)1 << 31);
+}
+
+hipError_t launch_apply_rb(bool trans, bool corr, int ncomp, const Geom &g, int C, int64_t nb,
+                           float scale, const float *nz, const float *x, const float *z, float *y,
+                           hipStream_t s) {
+    ApplyArgs a;
+    a.g = g;
+    a.C = C;
+    a.corr = corr ? 1 : 0;
+    a.tiles1 = (g.n1 + tile_w(g.nsp) - 1) / tile_w(g.nsp);
+    a.tiles2 = (g.n2 + tile_h(g.nsp) - 1) / tile_h(g.nsp);
+    // staging passes of one tile run in one wavefront (nzVal re-read from L2)
+    // unless the grid would be too small to fill the GPU
+    const int npass = (ncomp * C + kCP - 1) / kCP;
+    const int64_t waves = tiles_of(g) * nb;
+    a.ichunk = waves >= 1024 ? npass : 1;
+    a.gchunk = (npass + a.ichunk - 1) / a.ichunk;
+    a.scale = scale;
+    a.nz = nz;
+    a.x = x;
+    a.z = z;
+    a.y = y;
+    if (ncomp == 1) return trans ? dispatch_ws<1, true>(a, nb, s) : dispatch_ws<1, false>(a, nb, s);
+    return trans ? dispatch_ws<2, true>(a, nb, s) : dispatch_ws<2, false>(a, nb, s);
+}
+
+hipError_t launch_colsum_rb(const Geom &g, int64_t nb, const float *nz, float *out, hipStream_t s) {
+    switch (g.ws) {
+        case 3: return launch_colsum_t<3>(g, nb, nz, out, s);
+        case 5: return launch_colsum_t<5>(g, nb, nz, out, s);
+        case 7: return launch_colsum_t<7>(g, nb, nz, out, s);
+        case 9: return launch_colsum_t<9>(g, nb, nz, out, s);
+        case 11: return launch_colsum_t<11>(g, nb, nz, out, s);
+        case 13: return launch_colsum_t<13>(g, nb, nz, out, s);
+        case 15: return launch_colsum_t<15>(g, nb, nz, out, s);
+        default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace circatt

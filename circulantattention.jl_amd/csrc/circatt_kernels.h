@@ -15,6 +15,14 @@ hipError_t launch_softmax_bwd(int K, int64_t rows, const float *A, const float *
 hipError_t launch_apply(bool trans, bool corr, int ncomp, const Geom &g, int C, int64_t nb,
                         float scale, const float *nz, const float *x, const float *z, float *y,
                         hipStream_t s);
+// Register-blocked form of launch_apply for windows 3 .. 15 (apply_rb.hip);
+// launch_apply routes there when apply_rb_supported holds.
+bool apply_rb_supported(const Geom &g, int C, int ncomp, int64_t nb);
+hipError_t launch_apply_rb(bool trans, bool corr, int ncomp, const Geom &g, int C, int64_t nb,
+                           float scale, const float *nz, const float *x, const float *z, float *y,
+                           hipStream_t s);
+// colsum (sum(A; dims=1)) through the transposed product's offset tables
+hipError_t launch_colsum_rb(const Geom &g, int64_t nb, const float *nz, float *out, hipStream_t s);
 hipError_t launch_similarity(bool dist, int ncomp, const Geom &g, int C, int64_t nb, float scale,
                              const float *x, const float *y, float *nz, hipStream_t s);
 hipError_t launch_sum(bool col, const Geom &g, int64_t nb, const float *nz, float *out,

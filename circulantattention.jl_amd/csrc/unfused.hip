@@ -5,6 +5,8 @@
 // offset bijection of circatt_common.h, so the transposed products gather
 // without atomics.  These kernels are memory/latency bound; the fused
 // MFMA kernels (fused.hip) carry the north-star path.
+#include <algorithm>
+
 #include "circatt_common.h"
 #include "circatt_kernels.h"
 
@@ -29,6 +31,30 @@ __global__ void pattern_kernel(Geom g, int64_t nb, int32_t *__restrict__ rowptr,
         const int32_t v = (int32_t)(1 + (int64_t)g.K * r);
         for (int64_t b = 0; b < nb; ++b) rowptr[r + b * (g.P + 1)] = v;
     }
+}
+
+// Same pattern with 32-bit index arithmetic (P * K < 2^31), one thread per
+// slot computing its column once for all batch copies.
+__global__ void pattern32_kernel(int nsp, int n1, int n2, int ws, int nb,
+                                 int32_t *__restrict__ rowptr, int32_t *__restrict__ colval) {
+    const int p = (ws - 1) / 2;
+    const int K = nsp == 1 ? ws : ws * ws;
+    const int P = n1 * n2;
+    const int PK = P * K;
+    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < PK; n += gridDim.x * blockDim.x) {
+        const int r = n / K, t = n - r * K;
+        const int i1 = r % n1, i2 = r / n1;
+        const int m0 = nsp == 1 ? t : t % ws;
+        const int d1 = slot_to_offset(m0, slot_shift(i1 + 1, n1, p), ws, p);
+        int col = pmod(i1 + d1, n1);
+        if (nsp == 2) {
+            const int d2 = slot_to_offset(t / ws, slot_shift(i2 + 1, n2, p), ws, p);
+            col += n1 * pmod(i2 + d2, n2);
+        }
+        for (int b = 0; b < nb; ++b) colval[n + (int64_t)b * PK] = col + 1;
+    }
+    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r <= P; r += gridDim.x * blockDim.x)
+        for (int b = 0; b < nb; ++b) rowptr[r + (int64_t)b * (P + 1)] = 1 + K * r;
 }
 
 // ---------------------------------------------------------------------------
@@ -75,6 +101,101 @@ __global__ __launch_bounds__(256) void softmax_bwd_kernel(int K, int64_t rows,
     for (int t = lane; t < K; t += 64) s += a[t] * da[t];
     s = wave_sum(s);
     for (int t = lane; t < K; t += 64) dS[row * K + t] = a[t] * (da[t] - s);
+}
+
+// Rows held in registers: a group of L lanes owns one row of K <= L * V
+// slots, reads it once, reduces with cross-lane shuffles inside the group and
+// writes it once.
+template <int L>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int o = L / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = L / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+template <int L, int V>
+__global__ __launch_bounds__(256) void softmax_rows_kernel(int K, int64_t rows,
+                                                           const float *__restrict__ in,
+                                                           float *__restrict__ out) {
+    const int gl = threadIdx.x % L;
+    const int64_t row = (int64_t)blockIdx.x * (256 / L) + threadIdx.x / L;
+    const bool live = row < rows;
+    const float *a = in + (live ? row : 0) * K;
+    float v[V];
+    float m = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+        const int t = gl + L * u;
+        v[u] = live && t < K ? a[t] : -INFINITY;
+        m = fmaxf(m, v[u]);
+    }
+    m = group_max<L>(m);
+    float s = 0.f;
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+        const int t = gl + L * u;
+        v[u] = live && t < K ? __expf(v[u] - m) : 0.f;
+        s += v[u];
+    }
+    s = group_sum<L>(s);
+    const float inv = 1.f / s;
+    if (!live) return;
+    float *o = out + row * K;
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+        const int t = gl + L * u;
+        if (t < K) o[t] = v[u] * inv;
+    }
+}
+
+template <int L, int V>
+__global__ __launch_bounds__(256) void softmax_bwd_rows_kernel(int K, int64_t rows,
+                                                               const float *__restrict__ A,
+                                                               const float *dA, float *dS) {
+    const int gl = threadIdx.x % L;
+    const int64_t row = (int64_t)blockIdx.x * (256 / L) + threadIdx.x / L;
+    const bool live = row < rows;
+    const int64_t base = (live ? row : 0) * K;
+    float av[V], dv[V];
+    float s = 0.f;
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+        const int t = gl + L * u;
+        const bool in = live && t < K;
+        av[u] = in ? A[base + t] : 0.f;
+        dv[u] = in ? dA[base + t] : 0.f;
+        s += av[u] * dv[u];
+    }
+    s = group_sum<L>(s);  // every read of the row precedes this, so dS may alias dA
+    if (!live) return;
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+        const int t = gl + L * u;
+        if (t < K) dS[base + t] = av[u] * (dv[u] - s);
+    }
+}
+
+// sum over a row's K contiguous slots, 16 lanes per row
+__global__ __launch_bounds__(256) void rowsum_kernel(int K, int64_t rows,
+                                                     const float *__restrict__ nz,
+                                                     float *__restrict__ out) {
+    const int gl = threadIdx.x & 15;
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const bool live = row < rows;
+    const float *a = nz + (live ? row : 0) * K;
+    float s = 0.f;
+    if (live) {
+#pragma unroll 4
+        for (int t = gl; t < K; t += 16) s += a[t];
+    }
+    s = group_sum<16>(s);
+    if (live && gl == 0) out[row] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -216,6 +337,38 @@ __global__ void axpby_kernel(int64_t nnz, int64_t nb, const float *__restrict__ 
     }
 }
 
+// Z[:, b] = alpha_b X[:, b] + beta_b Y[:, b]: batch b = blockIdx.y, float4
+// accesses when every slice is 16-byte aligned (VEC), no per-element division.
+template <bool VEC>
+__global__ __launch_bounds__(256) void axpby2_kernel(int64_t nnz, const float *__restrict__ alpha,
+                                                     float alpha0, const float *X,
+                                                     const float *__restrict__ beta, float beta0,
+                                                     const float *Y, float *Z) {
+    const int64_t b = blockIdx.y;
+    const float al = alpha ? alpha[b] : alpha0;
+    const float be = Y ? (beta ? beta[b] : beta0) : 0.f;
+    const int64_t off = b * nnz;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t i0 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (VEC) {
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        const f4 *x4 = (const f4 *)(X + off);
+        const f4 *y4 = (const f4 *)(Y ? Y + off : nullptr);
+        f4 *z4 = (f4 *)(Z + off);
+        for (int64_t i = i0; i < nnz / 4; i += stride) {
+            f4 v = al * x4[i];
+            if (Y) v += be * y4[i];
+            z4[i] = v;
+        }
+    } else {
+        for (int64_t i = i0; i < nnz; i += stride) {
+            float v = al * X[off + i];
+            if (Y) v += be * Y[off + i];
+            Z[off + i] = v;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
@@ -228,12 +381,43 @@ static inline unsigned grid_for(int64_t n, int threads, int64_t cap = 1 << 20) {
 
 hipError_t launch_pattern(const Geom &g, int64_t nb, int32_t *rowptr, int32_t *colval,
                           hipStream_t s) {
+    if (g.P * g.K < ((int64_t)1 << 31) - 1 && nb <= INT32_MAX) {
+        hipLaunchKernelGGL(pattern32_kernel, dim3(grid_for(g.P * g.K, 256, 1 << 16)), dim3(256), 0,
+                           s, g.nsp, g.n1, g.n2, g.ws, (int)nb, rowptr, colval);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(pattern_kernel, dim3(grid_for(g.P * g.K, 256)), dim3(256), 0, s, g, nb,
                        rowptr, colval);
     return hipGetLastError();
 }
 
+#define CIRCATT_ROWS_DISPATCH(KERNEL, ...)                                                   \
+    do {                                                                                     \
+        const int64_t rows16 = (rows + 15) / 16, rows4 = (rows + 3) / 4;                     \
+        if (K <= 16 && rows16 < (1LL << 31)) {                                               \
+            hipLaunchKernelGGL((KERNEL<16, 1>), dim3((unsigned)rows16), dim3(256), 0, s, __VA_ARGS__); \
+            return hipGetLastError();                                                        \
+        }                                                                                    \
+        if (K <= 64 && rows16 < (1LL << 31)) {                                               \
+            hipLaunchKernelGGL((KERNEL<16, 4>), dim3((unsigned)rows16), dim3(256), 0, s, __VA_ARGS__); \
+            return hipGetLastError();                                                        \
+        }                                                                                    \
+        if (K <= 128 && rows16 < (1LL << 31)) {                                              \
+            hipLaunchKernelGGL((KERNEL<16, 8>), dim3((unsigned)rows16), dim3(256), 0, s, __VA_ARGS__); \
+            return hipGetLastError();                                                        \
+        }                                                                                    \
+        if (K <= 256 && rows16 < (1LL << 31)) {                                              \
+            hipLaunchKernelGGL((KERNEL<16, 16>), dim3((unsigned)rows16), dim3(256), 0, s, __VA_ARGS__); \
+            return hipGetLastError();                                                        \
+        }                                                                                    \
+        if (K <= 1024 && rows4 < (1LL << 31)) {                                              \
+            hipLaunchKernelGGL((KERNEL<64, 16>), dim3((unsigned)rows4), dim3(256), 0, s, __VA_ARGS__); \
+            return hipGetLastError();                                                        \
+        }                                                                                    \
+    } while (0)
+
 hipError_t launch_softmax(int K, int64_t rows, const float *in, float *out, hipStream_t s) {
+    CIRCATT_ROWS_DISPATCH(softmax_rows_kernel, K, rows, in, out);
     hipLaunchKernelGGL(softmax_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, K,
                        rows, in, out);
     return hipGetLastError();
@@ -241,6 +425,7 @@ hipError_t launch_softmax(int K, int64_t rows, const float *in, float *out, hipS
 
 hipError_t launch_softmax_bwd(int K, int64_t rows, const float *A, const float *dA, float *dS,
                               hipStream_t s) {
+    CIRCATT_ROWS_DISPATCH(softmax_bwd_rows_kernel, K, rows, A, dA, dS);
     hipLaunchKernelGGL(softmax_bwd_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s,
                        K, rows, A, dA, dS);
     return hipGetLastError();
@@ -259,6 +444,8 @@ static hipError_t launch_apply_t(const Geom &g, int C, int64_t nb, float scale, 
 hipError_t launch_apply(bool trans, bool corr, int ncomp, const Geom &g, int C, int64_t nb,
                         float scale, const float *nz, const float *x, const float *z, float *y,
                         hipStream_t s) {
+    if (apply_rb_supported(g, C, ncomp, nb))
+        return launch_apply_rb(trans, corr, ncomp, g, C, nb, scale, nz, x, z, y, s);
 #define CIRCATT_APPLY_CASE(NC, T, CR)                                       \
     if (ncomp == NC && trans == T && corr == CR)                            \
         return launch_apply_t<NC, T, CR>(g, C, nb, scale, nz, x, z, y, s);
@@ -290,6 +477,12 @@ hipError_t launch_similarity(bool dist, int ncomp, const Geom &g, int C, int64_t
 
 hipError_t launch_sum(bool col, const Geom &g, int64_t nb, const float *nz, float *out,
                       hipStream_t s) {
+    if (!col && (g.P * nb + 15) / 16 < (1LL << 31)) {
+        hipLaunchKernelGGL(rowsum_kernel, dim3((unsigned)((g.P * nb + 15) / 16)), dim3(256), 0, s,
+                           g.K, g.P * nb, nz, out);
+        return hipGetLastError();
+    }
+    if (col && apply_rb_supported(g, 1, 1, nb)) return launch_colsum_rb(g, nb, nz, out, s);
     const unsigned grid = grid_for(g.P * nb, 256, 1LL << 31);
     if (col)
         hipLaunchKernelGGL(sum_kernel<true>, dim3(grid), dim3(256), 0, s, g, nb, nz, out);
@@ -301,6 +494,18 @@ hipError_t launch_sum(bool col, const Geom &g, int64_t nb, const float *nz, floa
 hipError_t launch_axpby(int64_t nnz, int64_t nb, const float *alpha, float alpha0,
                         const float *X, const float *beta, float beta0, const float *Y, float *Z,
                         hipStream_t s) {
+    if (nb <= 65535) {
+        const bool vec = nnz % 4 == 0 && ((uintptr_t)X | (uintptr_t)Z | (uintptr_t)Y) % 16 == 0;
+        const int64_t n = vec ? nnz / 4 : nnz;
+        const unsigned gx = grid_for(n, 256, std::max<int64_t>(1, 4096 / nb));
+        if (vec)
+            hipLaunchKernelGGL(axpby2_kernel<true>, dim3(gx, (unsigned)nb), dim3(256), 0, s, nnz,
+                               alpha, alpha0, X, beta, beta0, Y, Z);
+        else
+            hipLaunchKernelGGL(axpby2_kernel<false>, dim3(gx, (unsigned)nb), dim3(256), 0, s, nnz,
+                               alpha, alpha0, X, beta, beta0, Y, Z);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(axpby_kernel, dim3(grid_for(nnz * nb, 256, 1 << 16)), dim3(256), 0, s,
                        nnz, nb, alpha, alpha0, X, beta, beta0, Y, Z);
     return hipGetLastError();
