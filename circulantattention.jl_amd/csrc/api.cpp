@@ -140,7 +140,13 @@ int circatt_similarity(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int
     pr.q = static_cast<const float *>(x);
     pr.k = static_cast<const float *>(y);
     pr.nz = nzval;
-    if (fused_supported(MODE_SIM, pr))
+    const bool rows_ok = sim_rows_supported(g, (int)C, ncomp, nb);
+    const bool mfma_ok = fused_supported(MODE_SIM, pr);
+    if (rows_ok && (!mfma_ok || sim_rows_preferred(g, nb)))
+        return hip_result(launch_sim_rows(kind == CIRCATT_DISTANCE, ncomp, g, (int)C, nb, scale,
+                                          pr.q, pr.k, nzval, as_stream(stream)),
+                          "circatt_similarity");
+    if (mfma_ok)
         return hip_result(launch_fused(MODE_SIM, pr, as_stream(stream)), "circatt_similarity");
     return hip_result(launch_similarity(kind == CIRCATT_DISTANCE, ncomp, g, (int)C, nb, scale,
                                         pr.q, pr.k, nzval, as_stream(stream)),

@@ -577,6 +577,141 @@ __global__ __launch_bounds__(64, 2) void apply_rows_kernel(ApplyArgs a) {
         rows_body<WS, NCOMP, false>(a, gc, t1, c2, b);
 }
 
+// ---------------------------------------------------------------------------
+// nzVal = scale * similarity(x, y) in 2D (src/similarity.jl:31-103): a
+// wavefront owns 64 consecutive pixels of one image row; lane group r takes
+// window rows r, r + 4, ...; for one window row a lane accumulates the ws
+// slots of its 4 pixels over the channels (sequentially, as the reference
+// does) from one run of 4 + 2p key pixels per channel, then stores each
+// pixel's chunk of ws slots (contiguous in the row, rotated near borders).
+// ---------------------------------------------------------------------------
+template <int WS, int NCOMP, bool DIST, bool FAST>
+__device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int c2, int b) {
+    constexpr int P = (WS - 1) / 2;
+    constexpr int K = WS * WS;
+    constexpr int XW = kR + 2 * P;
+    constexpr int XN = NCOMP * XW;
+    constexpr int XN4 = (XN + 3) / 4;
+    constexpr int QN = NCOMP * kR;  // query floats of a lane per channel
+    constexpr int NIT = (WS + 3) / 4;
+    const Geom &g = a.g;
+    const int n1 = g.n1, n2 = g.n2;
+    const int64_t Pp = g.P;
+    const int lane = threadIdx.x & 63;
+    const int l16 = lane & 15, rho = lane >> 4;
+    const int f1 = t1 * 64;
+    const int ubytes = (int)(Pp * NCOMP * a.C * 4);
+    const auto rq = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, ubytes);  // rows (queries)
+    const auto rk = rsrc(a.z + (int64_t)b * Pp * NCOMP * a.C, ubytes);  // columns (keys)
+    float *nzb = a.y + (int64_t)b * Pp * K;
+    int s1[kR];
+#pragma unroll
+    for (int i = 0; i < kR; ++i) s1[i] = FAST ? 0 : shift0(pmod(f1 + 4 * l16 + i, n1), n1, P);
+    const int s2 = slot_shift(c2 + 1, n2, P);
+    // query pixels of the lane (wrapped columns keep reads in range)
+    int qcol[kR];
+#pragma unroll
+    for (int i = 0; i < kR; ++i) qcol[i] = FAST ? f1 + 4 * l16 + i : pmod(f1 + 4 * l16 + i, n1);
+    const int plane = (int)(NCOMP * Pp * 4);  // bytes per channel
+
+    // window-row iterations [gc * ichunk, ...) of this wavefront
+    const int it1 = min(NIT, (gc + 1) * a.ichunk);
+    for (int itr = gc * a.ichunk; itr < it1; ++itr) {
+        const int dd = 4 * itr + rho;
+        const bool live = dd < WS;
+        const int ddc = live ? dd : WS - 1;
+        const int kr2 = pmod(c2 + ddc - P, n2);
+        const int mm = pmod(ddc + s2, WS);
+        const int qoff = NCOMP * (qcol[0] + n1 * c2) * 4;
+        const int koff = NCOMP * (n1 * kr2) * 4;
+        float acc[kR][WS];
+#pragma unroll
+        for (int i = 0; i < kR; ++i)
+#pragma unroll
+            for (int j = 0; j < WS; ++j) acc[i][j] = 0.f;
+#pragma unroll 1
+        for (int c = 0; c < a.C; ++c) {
+            float q[QN], kw[4 * XN4];
+            const int cb = c * plane;
+            if (FAST) {
+#pragma unroll
+                for (int h = 0; h < QN / 4; ++h) {
+                    const f4 v = bload4(rq, qoff + cb, 16 * h);
+                    q[4 * h] = v[0];
+                    q[4 * h + 1] = v[1];
+                    q[4 * h + 2] = v[2];
+                    q[4 * h + 3] = v[3];
+                }
+                const int vo = koff + cb + NCOMP * (f1 + 4 * l16 - P) * 4;
+#pragma unroll
+                for (int h = 0; h < XN4; ++h) {
+                    const f4 v = bload4(rk, vo, 16 * h);
+                    kw[4 * h] = v[0];
+                    kw[4 * h + 1] = v[1];
+                    kw[4 * h + 2] = v[2];
+                    kw[4 * h + 3] = v[3];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < kR; ++i)
+#pragma unroll
+                    for (int e = 0; e < NCOMP; ++e)
+                        q[NCOMP * i + e] =
+                            bload(rq, cb + (NCOMP * (qcol[i] + n1 * c2) + e) * 4, 0);
+                int xc = pmod(f1 + 4 * l16 - P, n1);
+#pragma unroll
+                for (int w = 0; w < XW; ++w) {
+#pragma unroll
+                    for (int e = 0; e < NCOMP; ++e)
+                        kw[NCOMP * w + e] = bload(rk, koff + cb + (NCOMP * xc + e) * 4, 0);
+                    xc = xc + 1 == n1 ? 0 : xc + 1;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < kR; ++i)
+#pragma unroll
+                for (int j = 0; j < WS; ++j)
+#pragma unroll
+                    for (int e = 0; e < NCOMP; ++e) {
+                        const float xv = q[NCOMP * i + e], yv = kw[NCOMP * (i + j) + e];
+                        if (DIST) {
+                            const float d = xv - yv;
+                            acc[i][j] = __builtin_fmaf(d, d, acc[i][j]);
+                        } else {
+                            acc[i][j] = __builtin_fmaf(xv, yv, acc[i][j]);
+                        }
+                    }
+        }
+        if (!live) continue;
+        const float sc = DIST ? -0.5f * a.scale : a.scale;
+#pragma unroll
+        for (int i = 0; i < kR; ++i) {
+            const int col = f1 + 4 * l16 + i;
+            if (col >= n1) continue;
+            float *row = nzb + (col + (int64_t)n1 * c2) * K + mm * WS;
+#pragma unroll
+            for (int j = 0; j < WS; ++j) row[FAST ? j : fold(j + s1[i], WS)] = acc[i][j] * sc;
+        }
+    }
+}
+
+// One wavefront per (64 pixels of an image row, unit).  Fields of ApplyArgs:
+// x = rows (queries), z = columns (keys), y = nzVal.
+template <int WS, int NCOMP, bool DIST>
+__global__ __launch_bounds__(64, 2) void sim_rows_kernel(ApplyArgs a) {
+    int it = blockIdx.x;
+    const int gc = __builtin_amdgcn_readfirstlane(it % a.gchunk);
+    it /= a.gchunk;
+    const int t1 = __builtin_amdgcn_readfirstlane(it % a.tiles1);
+    it /= a.tiles1;
+    const int c2 = __builtin_amdgcn_readfirstlane(it % a.g.n2);
+    const int b = __builtin_amdgcn_readfirstlane(it / a.g.n2);
+    if (t1 >= a.fa && t1 < a.fb)
+        sim_body<WS, NCOMP, DIST, true>(a, gc, t1, c2, b);
+    else
+        sim_body<WS, NCOMP, DIST, false>(a, gc, t1, c2, b);
+}
+
 // Interior tile columns [fa, fb): every lane row 2p or more inside dim 1.
 inline void interior_cols(const Geom &g, int &fa, int &fb) {
     const int tw = tile_w(g.nsp), tiles1 = (g.n1 + tw - 1) / tw;
@@ -647,7 +782,65 @@ int64_t tiles_of(const Geom &g) {
            ((g.n2 + tile_h(g.nsp) - 1) / tile_h(g.nsp));
 }
 
+template <int WS, int NCOMP, bool DIST>
+hipError_t launch_sim_t(ApplyArgs a, int64_t nb, hipStream_t s) {
+    const int tiles1 = (a.g.n1 + 63) / 64;
+    a.tiles1 = tiles1;
+    a.fa = (a.g.p + 63) / 64;
+    a.fb = a.g.n1 - 64 - a.g.p >= 0 ? (a.g.n1 - 64 - a.g.p) / 64 + 1 : 0;
+    if (a.fb > tiles1) a.fb = tiles1;
+    if (a.fb < a.fa) a.fb = a.fa;
+    // window-row iterations split over wavefronts when the grid is small
+    constexpr int NIT = (WS + 3) / 4;
+    const int64_t waves = (int64_t)tiles1 * a.g.n2 * nb;
+    a.ichunk = waves >= 2048 ? NIT : std::max(1, (int)((int64_t)NIT * waves / 2048));
+    a.gchunk = (NIT + a.ichunk - 1) / a.ichunk;
+    const int64_t grid = waves * a.gchunk;
+    hipLaunchKernelGGL((sim_rows_kernel<WS, NCOMP, DIST>), dim3((unsigned)grid), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int NCOMP, bool DIST>
+hipError_t sim_ws(const ApplyArgs &a, int64_t nb, hipStream_t s) {
+    switch (a.g.ws) {
+        case 3: return launch_sim_t<3, NCOMP, DIST>(a, nb, s);
+        case 5: return launch_sim_t<5, NCOMP, DIST>(a, nb, s);
+        case 7: return launch_sim_t<7, NCOMP, DIST>(a, nb, s);
+        case 9: return launch_sim_t<9, NCOMP, DIST>(a, nb, s);
+        case 11: return launch_sim_t<11, NCOMP, DIST>(a, nb, s);
+        case 13: return launch_sim_t<13, NCOMP, DIST>(a, nb, s);
+        case 15: return launch_sim_t<15, NCOMP, DIST>(a, nb, s);
+        default: return hipErrorNotSupported;
+    }
+}
+
 }  // namespace
+
+bool sim_rows_supported(const Geom &g, int C, int ncomp, int64_t nb) {
+    if (g.nsp != 2 || g.ws < 3 || g.ws > 15 || (g.ws & 1) == 0) return false;
+    if (g.P * g.K * 4 >= (int64_t)1 << 31) return false;
+    if (g.P * ncomp * C * 4 >= (int64_t)1 << 31) return false;
+    const int64_t grid = (int64_t)((g.n1 + 63) / 64) * g.n2 * nb;
+    return grid > 0 && grid < ((int64_t)1 << 31);
+}
+bool sim_rows_preferred(const Geom &g, int64_t nb) {
+    // the vector kernel needs many row segments to hide its load latency;
+    // small grids go to the matrix-core kernel when it supports the shape
+    return (int64_t)((g.n1 + 63) / 64) * g.n2 * nb >= 1024;
+}
+
+hipError_t launch_sim_rows(bool dist, int ncomp, const Geom &g, int C, int64_t nb, float scale,
+                           const float *x, const float *y, float *nz, hipStream_t s) {
+    ApplyArgs a{};
+    a.g = g;
+    a.C = C;
+    a.scale = scale;
+    a.x = x;
+    a.z = y;
+    a.y = nz;
+    if (ncomp == 1) return dist ? sim_ws<1, true>(a, nb, s) : sim_ws<1, false>(a, nb, s);
+    return dist ? sim_ws<2, true>(a, nb, s) : sim_ws<2, false>(a, nb, s);
+}
 
 bool apply_rb_supported(const Geom &g, int C, int ncomp, int64_t nb) {
     if (g.ws < 3 || g.ws > 15 || (g.ws & 1) == 0) return false;

@@ -105,6 +105,24 @@ def test_similarity(ca, cuda, dims, ws, C, cplx, kind):
     assert rel_err(host(S.nzval).reshape(B, -1), ref) < TOL_FWD
 
 
+@pytest.mark.parametrize("ws", [7, 11])
+@pytest.mark.parametrize("cplx", [False, True])
+@pytest.mark.parametrize("kind", [0, 1])
+def test_similarity_many_rows(ca, cuda, ws, cplx, kind):
+    """Grids of 2048 or more 64-pixel row segments take the row-blocked
+    similarity kernel (smaller grids take the matrix-core kernel): 96 x 256,
+    4 units, against the oracle; 96 is not a multiple of 64, so partial
+    segments and both border paths run."""
+    dims, C, B = (96, 256), 6, 4
+    x = seeded(13, shape_of(dims, C, B), cplx)
+    y = seeded(14, shape_of(dims, C, B), cplx)
+    simfun = ca.DotSimilarity() if kind == 0 else ca.DistanceSimilarity()
+    S = ca.circulant_similarity(simfun, dev(x, cuda), dev(y, cuda), ws)
+    P = int(np.prod(dims))
+    ref = O.similarity(kind, x.reshape(B, C, P), y.reshape(B, C, P), dims, ws)
+    assert rel_err(host(S.nzval).reshape(B, -1), ref) < TOL_FWD
+
+
 @pytest.mark.parametrize("K,rows", [(1, 10), (9, 1000), (225, 3000), (961, 70), (3969, 5)])
 def test_softmax_and_pullback(ca, cuda, K, rows):
     from circulant_attention._functions import SoftmaxFn
