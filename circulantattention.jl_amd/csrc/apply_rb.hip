@@ -131,8 +131,20 @@ __device__ __forceinline__ void stage_dma(float *lw, const Geom &g, __amdgpu_buf
 constexpr int kWaitAll = 0;
 constexpr int kWaitLgkm = 0x0070 | 0xC000 | 0x000F;  // lgkmcnt(0), vmcnt and expcnt at max
 
-// Geometry of the lane row whose chunks this lane stages (lane & 3) and the
-// window row's chunk row / chunk index for it.
+// Geometry of the lane row whose chunks this lane stages (lane & 3): first
+// source column, source image row and chunk index at iteration dd.
+//   forward (A ⊗ x): iteration dd is window row d2 = dd - p of the lane
+//     row's own pixels;
+//   transposed, 2D: iteration dd is source image row t2 * 4 - p + dd, shared
+//     by the 4 lane rows (output rows t2 * 4 + r), which need its chunks of
+//     window rows d2 = r + p - dd: 4 adjacent chunks of every source pixel,
+//     one contiguous run per load instruction.  Lane rows whose d2 falls
+//     outside the window stage a clamped chunk they do not use.
+template <int WS>
+__device__ __forceinline__ int trans_d2(int r, int dd) {
+    constexpr int P = (WS - 1) / 2;
+    return r + P - dd;
+}
 template <int WS>
 __device__ __forceinline__ void staging_row(const Geom &g, int t1, int t2, int dd, bool trans,
                                             int &f1r, int &r2r, int &mmr) {
@@ -140,15 +152,23 @@ __device__ __forceinline__ void staging_row(const Geom &g, int t1, int t2, int d
     const int r = threadIdx.x & 3;
     const bool two = g.nsp == 2;
     f1r = two ? t1 * 64 : t1 * 256 + 64 * r;
-    if (two) {
+    if (two && trans) {
+        r2r = pmod(t2 * 4 - P + dd, g.n2);
+        const int d2 = min(P, max(-P, trans_d2<WS>(r, dd)));
+        mmr = pmod(d2 + P + slot_shift(r2r + 1, g.n2, P), WS);
+    } else if (two) {
         const int c2u = t2 * 4 + r;
-        const int c2 = c2u < g.n2 ? c2u : c2u % g.n2;
-        r2r = trans ? pmod(c2 - (dd - P), g.n2) : c2;
+        r2r = c2u < g.n2 ? c2u : c2u % g.n2;
         mmr = pmod(dd + slot_shift(r2r + 1, g.n2, P), WS);
     } else {
         r2r = 0;
         mmr = 0;
     }
+}
+// iterations of the staging loop
+template <int WS>
+__host__ __device__ constexpr int n_iter(bool two, bool trans) {
+    return two ? (trans ? WS + 3 : WS) : 1;
 }
 
 // slot_shift of 0-based column c (same case order as slot_shift)
@@ -177,12 +197,12 @@ __device__ __forceinline__ void apply_body(const ApplyArgs &a, int gc, int t1, i
     float *lw = circatt_lds_apply;
     const auto rs = rsrc(a.nz + (int64_t)b * Pp * K, Pp * K * 4);
     const auto rx = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, Pp * NCOMP * a.C * 4);
-    const int nd2 = two ? WS : 1;
+    const int nd2 = n_iter<WS>(two, TRANS);
 
-    // x run of channel c for window row dd
+    // x run of channel c at iteration dd (window row dd - p of the own image
+    // row, or the source image row of the transposed product)
     auto load_x = [&](float (&xw)[4 * XN4], int c, int dd, int f1) {
-        const int d2 = dd - P;
-        const int xr2 = two ? pmod(TRANS ? L.c2 - d2 : L.c2 + d2, n2) : 0;
+        const int xr2 = two ? pmod(TRANS ? t2 * 4 - P + dd : L.c2 + dd - P, n2) : 0;
         const int cw = c < a.C ? c : a.C - 1;
         const int rowoff = (int)(NCOMP * ((int64_t)n1 * xr2 + Pp * cw)) * 4;
         if (FAST) {
@@ -232,7 +252,10 @@ __device__ __forceinline__ void apply_body(const ApplyArgs &a, int gc, int t1, i
             // hoisted out of the loop as tables of registers
             int f1 = L.f1, k4 = 4 * K;
             asm volatile("" : "+v"(f1), "+s"(k4));
-            __builtin_amdgcn_s_waitcnt(kWaitAll);  // this window row's chunks are in LDS
+            __builtin_amdgcn_s_waitcnt(kWaitAll);  // this iteration's chunks are in LDS
+            // transposed, 2D: this lane row's window row at this source row
+            const int d2t = trans_d2<WS>(L.rho, dd);
+            const bool live = !(TRANS && two) || (d2t >= -P && d2t <= P);
             float av[kR][WS];
 #pragma unroll
             for (int i = 0; i < kR; ++i) {
@@ -255,11 +278,12 @@ __device__ __forceinline__ void apply_body(const ApplyArgs &a, int gc, int t1, i
                             pos = fold(j + s1, WS);
                         }
                     }
-                    av[i][j] = lw[u * kPU + 4 * pos + L.rho];
+                    const float v = lw[u * kPU + 4 * pos + L.rho];
+                    av[i][j] = live ? v : 0.f;
                 }
             }
-            // every read of the buffer has returned before the next window
-            // row's chunks are loaded into it
+            // every read of the buffer has returned before the next
+            // iteration's chunks are loaded into it
             __builtin_amdgcn_s_waitcnt(kWaitLgkm);
             if (dd + 1 < nd2) stage(dd + 1, k4);
             if (a.corr) {
@@ -344,7 +368,7 @@ __device__ __forceinline__ void colsum_body(const Geom &g, int t1, int t2, int b
     float *lw = circatt_lds_apply;
     const auto rs = rsrc(nz + (int64_t)b * g.P * K, g.P * K * 4);
     float s[kR] = {0.f, 0.f, 0.f, 0.f};
-    const int nd2 = two ? WS : 1;
+    const int nd2 = n_iter<WS>(two, true);
     auto stage = [&](int dd, int k4) {
         int f1r, r2r, mmr;
         staging_row<WS>(g, t1, t2, dd, true, f1r, r2r, mmr);
@@ -355,6 +379,8 @@ __device__ __forceinline__ void colsum_body(const Geom &g, int t1, int t2, int b
         int f1 = L.f1, k4 = 4 * K;
         asm volatile("" : "+v"(f1), "+s"(k4));
         __builtin_amdgcn_s_waitcnt(kWaitAll);
+        const int d2t = trans_d2<WS>(L.rho, dd);
+        const bool live = !two || (d2t >= -P && d2t <= P);
         float v[kR][WS];
 #pragma unroll
         for (int i = 0; i < kR; ++i)
@@ -363,7 +389,8 @@ __device__ __forceinline__ void colsum_body(const Geom &g, int t1, int t2, int b
                 const int u = 4 * L.l16 + i - j + 2 * P;
                 int pos = j;
                 if (!FAST) pos = fold(j + shift0(pmod(f1 - P + u, n1), n1, P), WS);
-                v[i][j] = lw[u * kPU + 4 * pos + L.rho];
+                const float x = lw[u * kPU + 4 * pos + L.rho];
+                v[i][j] = live ? x : 0.f;
             }
         __builtin_amdgcn_s_waitcnt(kWaitLgkm);
         if (dd + 1 < nd2) stage(dd + 1, k4);
