@@ -1,24 +1,34 @@
-// Sparse apply for windows of width 3 .. 15:
-//   TRANS = false: y[c] = sum_d A[c, slot(c, d)] x[c + d]            (A ⊗ x)
-//   TRANS = true : y[c] = sum_d A[c - d, slot(c - d, d)] x[c - d]    (Aᵀ ⊗ x)
-// optionally minus (sum of the A entries used) .* z (Distance rrule), times
-// scale; and sum(A; dims=1).  Replaces the CUSPARSE.bmm! products of
-// src/batchedmul.jl:82-110 and the column sum of src/array.jl:119-130.
+// Row-blocked kernels of the unfused (Circulant-materialising) path for
+// windows of width 3 .. 15:
+//   apply  y[c] = sum_d A[c, slot(c, d)] x[c + d]             (A ⊗ x)
+//   trans  y[c] = sum_d A[c - d, slot(c - d, d)] x[c - d]     (Aᵀ ⊗ x)
+//          optionally minus (sum of the A entries used) .* z (Distance
+//          rrule), times scale; replaces the CUSPARSE.bmm! products of
+//          src/batchedmul.jl:82-110;
+//   colsum sum(A; dims=1) (src/array.jl:119-130);
+//   sim    nzVal = scale * similarity(x, y) (src/similarity.jl:31-103).
 //
-// nzVal (K floats per pixel) dominates the bytes, so it is read with
-// coalesced loads and everything else is arranged around that:
-//   * a wavefront owns 4 lane rows of 64 pixels (a 64 x 4 tile in 2D, 256
-//     pixels of the line in 1D); each lane owns 4 consecutive pixels of its
-//     lane row, so for one window row d2 it applies 4 x ws products per
-//     component to one run of 4 + 2p values of x;
-//   * per window row, the lane row's 64 pixels' slot chunks (ws contiguous
-//     floats each; 64 + 2p source pixels for the transposed product) are
-//     loaded 16 lanes per chunk, written to a wave-private LDS buffer and read
-//     back by the lanes that own the pixels.  The read offsets carry the
-//     reference's circular shift of the slot order near borders
-//     (src/circulant.jl:6-44);
-//   * x runs are 16-byte buffer loads from L1 (4 + 2p values, wrapped near the
-//     borders of dim 1 through a per-lane column table).
+// nzVal (K floats per pixel) dominates the bytes, so it is read or written
+// in contiguous runs and everything else is arranged around that.  Every
+// lane owns 4 consecutive pixels along dim 1, so one run of 4 + 2p values
+// of x per component serves 4 x ws products.
+//   * 2D apply (apply_rows_kernel): a wavefront owns 64 pixels of one image
+//     row; their 64 K contiguous nzVal floats are loaded into LDS once by
+//     LDS-DMA buffer loads and serve every component chunk; the four lane
+//     groups split the window rows and add their partial sums at the end.
+//   * transposed apply, column sum, 1D apply (apply_rb_kernel,
+//     colsum_rb_kernel): a wavefront owns 4 lane rows of 64 pixels (a 64 x 4
+//     tile in 2D, 256 pixels of the line in 1D); per iteration the slot
+//     chunks it needs (64 + 2p source pixels for the transposed product) are
+//     DMA-loaded, 16 lanes per chunk, into a wave-private LDS buffer and read
+//     back by the owning lanes.  In 2D the transposed product walks source
+//     image rows, whose 4 chunks for the 4 lane rows are adjacent.
+//   * similarity (sim_rows_kernel): row ownership as in the 2D apply; each
+//     pixel's chunk of ws slots is accumulated over the channels in registers
+//     and stored as one run.
+// Read offsets carry the reference's circular shift of the slot order near
+// borders (src/circulant.jl:6-44); wavefronts within 2p of a border of dim 1
+// run a border body that steps wrapped columns, the others use immediates.
 #include <algorithm>
 
 #include "circatt_common.h"
