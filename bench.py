@@ -7,6 +7,11 @@ batch of synthetic N(0,1) float32 inputs already resident in HBM, at the
 configuration BASELINE.json's metric is quoted on (cfg3: DotSimilarity,
 256x256x64x4, 4 heads, ws = 15).  Prints one JSON line.
 
+Timing: after W warm-up steps, K steps of eager launches with HIP events
+around every entry point (per-kernel times, `ms_per_step_eager`), then the
+step captured once as a HIP graph and replayed W + K times, K of them timed
+(`ms_per_step` and `value`; `--no-graph` times the eager launches only).
+
 Roofline: every kernel of the step is priced at its algorithmic FLOPs
 (U = 2*P*K*dh*nheads*B per window contraction; forward 2U, dq pass 2U for
 dP and dQ, dk/dv pass 2U for dV and dK; recomputation and softmax work not
@@ -202,6 +207,9 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed region, run 3 device copies of this many MiB "
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time eager launches only (default: the step is also captured as a HIP "
+                         "graph, and `value` comes from its replays)")
     ap.add_argument("--ops", action="store_true",
                     help="instead of the fused step, time each unfused entry point (similarity, "
                          "softmax, apply, sums, axpby, pattern) at the cfg2 / cfg5 shapes and "
@@ -242,27 +250,28 @@ def main():
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
 
-    def fwd():
+    def fwd(s):
         L.check(L.lib.circatt_fused_fwd(kind, dt, nsp, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
-                                        ptr(v), ptr(y), ptr(lse), sp))
+                                        ptr(v), ptr(y), ptr(lse), s))
 
-    def bwd_dq():
+    def bwd_dq(s):
         L.check(L.lib.circatt_fused_bwd_dq(kind, dt, nsp, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
                                            ptr(v), ptr(y), ptr(dy), ptr(lse), ptr(dq),
-                                           ptr(work), wbytes, sp))
+                                           ptr(work), wbytes, s))
 
-    def bwd_dkdv():
+    def bwd_dkdv(s):
         L.check(L.lib.circatt_fused_bwd_dkdv(kind, dt, nsp, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
                                              ptr(v), ptr(dy), ptr(lse), ptr(dk), ptr(dv),
-                                             ptr(work), wbytes, sp))
+                                             ptr(work), wbytes, s))
 
     kernels = [("fwd", fwd), ("bwd_dq", bwd_dq), ("bwd_dkdv", bwd_dkdv)]
     for _ in range(args.warmup):
         for _, f in kernels:
-            f()
+            f(sp)
     torch.cuda.synchronize()
 
-    # timed region: K steps, HIP events around every launch on `stream`
+    # eager timed region: K steps of the three entry points, HIP events around
+    # every launch on `stream` (per-kernel times for the roofline)
     evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             for _ in kernels] for _ in range(args.steps)]
     torch.cuda.synchronize()
@@ -270,13 +279,36 @@ def main():
     for s in range(args.steps):
         for (_, f), (e0, e1) in zip(kernels, evs[s]):
             e0.record(stream)
-            f()
+            f(sp)
             e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_step = wall * 1e3 / args.steps
+    ms_step_eager = wall * 1e3 / args.steps
     kern_ms = {name: sum(evs[s][i][0].elapsed_time(evs[s][i][1]) for s in range(args.steps)) /
                args.steps for i, (name, _) in enumerate(kernels)}
+
+    # graph timed region: the step (the same three entry points) captured once
+    # as a HIP graph and replayed K times, as a training loop would launch it;
+    # the entry points allocate nothing and record no memset, so they capture
+    ms_step_graph = None
+    if not args.no_graph:
+        cs = torch.cuda.Stream(dev)
+        csp = ctypes.c_void_p(cs.cuda_stream)
+        graph = torch.cuda.CUDAGraph()
+        cs.wait_stream(stream)
+        with torch.cuda.graph(graph, stream=cs):
+            for _, f in kernels:
+                f(csp)
+        torch.cuda.synchronize()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        ms_step_graph = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms_step = ms_step_graph if ms_step_graph is not None else ms_step_eager
 
     mpix = B * P / (ms_step / 1e3) / 1e6
     cfac = 2 if cplx else 1
@@ -298,6 +330,9 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
+        "timing": ("HIP graph of the step's three entry points, replayed" if ms_step_graph
+                   is not None else "eager launches"),
+        "ms_per_step_eager": round(ms_step_eager, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -263,6 +263,57 @@ def test_fused_lse(ca, cuda):
         assert np.max(np.abs(host(lse) - ref)) < 1e-5 * np.max(np.abs(ref)) + 1e-5
 
 
+def test_fused_step_graph_replay(ca, cuda):
+    """The fused step's three entry points captured as one HIP graph (the way
+    bench.py times the step): every replay, with eager work and a
+    synchronisation between replays, reproduces the eager outputs bit for bit."""
+    import ctypes
+
+    from circulant_attention import _lib as L
+    from circulant_attention._functions import ptr
+    dims, ws, C, B, nh = (40, 24), 15, 64, 1, 4  # split-half kernels
+    n1, n2 = dims
+    g = torch.Generator(device=cuda)
+    g.manual_seed(7)
+    q, k, v, dy = (torch.randn(shape_of(dims, C, B), device=cuda, generator=g) for _ in range(4))
+    wbytes = L.lib.circatt_fused_bwd_workspace_bytes(2, n1, n2, nh, B)
+    work = torch.empty((wbytes // 4,), device=cuda)
+
+    def buffers():
+        return [torch.empty_like(q) for _ in range(4)] + [
+            torch.empty((B * nh, n1 * n2), device=cuda)]
+
+    def step(bufs, s):
+        y, dq, dk, dv, lse = bufs
+        L.check(L.lib.circatt_fused_fwd(0, L.F32, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k), ptr(v),
+                                        ptr(y), ptr(lse), s))
+        L.check(L.lib.circatt_fused_bwd_dq(0, L.F32, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
+                                           ptr(v), ptr(y), ptr(dy), ptr(lse), ptr(dq), ptr(work),
+                                           wbytes, s))
+        L.check(L.lib.circatt_fused_bwd_dkdv(0, L.F32, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
+                                             ptr(v), ptr(dy), ptr(lse), ptr(dk), ptr(dv),
+                                             ptr(work), wbytes, s))
+
+    ref = buffers()
+    step(ref, ctypes.c_void_p(torch.cuda.current_stream(cuda).cuda_stream))
+    torch.cuda.synchronize()
+    out = buffers()
+    cs = torch.cuda.Stream(cuda)
+    graph = torch.cuda.CUDAGraph()
+    cs.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.graph(graph, stream=cs):
+        step(out, ctypes.c_void_p(cs.cuda_stream))
+    torch.cuda.synchronize()
+    for r in range(3):
+        for t in out:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("y", "dq", "dk", "dv", "lse"), out, ref):
+            assert torch.equal(a, b), (r, name)
+
+
 def test_mh_attention_ignores_simfun(ca, cuda):
     """src/attention.jl:40 drops simfun: multi-head attention is always Dot."""
     dims, ws, C, B, nh = (10, 10), 3, 8, 2, 2
