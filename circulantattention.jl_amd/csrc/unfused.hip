@@ -119,6 +119,65 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Lane gl of a row's group holds slots 4 gl + 4 L v + e (v < V / 4, e < 4):
+// one 16-byte access per v (rows start at any 4-byte boundary: K is odd for
+// the circulant patterns), single floats only where a vector crosses the
+// row's end.  V = 1 (K <= 16) uses single floats.
+typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
+
+template <int L, int V>
+__device__ __forceinline__ void load_row(const float *a, int K, int gl, bool live, float fill,
+                                         float (&v)[V]) {
+    if constexpr (V < 4) {
+#pragma unroll
+        for (int u = 0; u < V; ++u) {
+            const int t = gl + L * u;
+            v[u] = live && t < K ? a[t] : fill;
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < V / 4; ++u) {
+            const int t0 = 4 * gl + 4 * L * u;
+            if (live && t0 + 3 < K) {
+                const f4u x = *(const f4u *)(a + t0);
+                v[4 * u] = x[0];
+                v[4 * u + 1] = x[1];
+                v[4 * u + 2] = x[2];
+                v[4 * u + 3] = x[3];
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[4 * u + q] = live && t0 + q < K ? a[t0 + q] : fill;
+            }
+        }
+    }
+}
+template <int L, int V>
+__device__ __forceinline__ int slot_of(int gl, int u) {
+    return V < 4 ? gl + L * u : 4 * gl + 4 * L * (u / 4) + (u & 3);
+}
+template <int L, int V>
+__device__ __forceinline__ void store_row(float *o, int K, int gl, const float (&v)[V]) {
+    if constexpr (V < 4) {
+#pragma unroll
+        for (int u = 0; u < V; ++u) {
+            const int t = gl + L * u;
+            if (t < K) o[t] = v[u];
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < V / 4; ++u) {
+            const int t0 = 4 * gl + 4 * L * u;
+            if (t0 + 3 < K) {
+                *(f4u *)(o + t0) = f4u{v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]};
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (t0 + q < K) o[t0 + q] = v[4 * u + q];
+            }
+        }
+    }
+}
+
 template <int L, int V>
 __global__ __launch_bounds__(256) void softmax_rows_kernel(int K, int64_t rows,
                                                            const float *__restrict__ in,
@@ -126,32 +185,24 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(int K, int64_t rows,
     const int gl = threadIdx.x % L;
     const int64_t row = (int64_t)blockIdx.x * (256 / L) + threadIdx.x / L;
     const bool live = row < rows;
-    const float *a = in + (live ? row : 0) * K;
     float v[V];
+    load_row<L, V>(in + (live ? row : 0) * K, K, gl, live, -INFINITY, v);
     float m = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < V; ++u) {
-        const int t = gl + L * u;
-        v[u] = live && t < K ? a[t] : -INFINITY;
-        m = fmaxf(m, v[u]);
-    }
+    for (int u = 0; u < V; ++u) m = fmaxf(m, v[u]);
     m = group_max<L>(m);
     float s = 0.f;
 #pragma unroll
     for (int u = 0; u < V; ++u) {
-        const int t = gl + L * u;
-        v[u] = live && t < K ? __expf(v[u] - m) : 0.f;
+        v[u] = live && slot_of<L, V>(gl, u) < K ? __expf(v[u] - m) : 0.f;
         s += v[u];
     }
     s = group_sum<L>(s);
     const float inv = 1.f / s;
     if (!live) return;
-    float *o = out + row * K;
 #pragma unroll
-    for (int u = 0; u < V; ++u) {
-        const int t = gl + L * u;
-        if (t < K) o[t] = v[u] * inv;
-    }
+    for (int u = 0; u < V; ++u) v[u] *= inv;
+    store_row<L, V>(out + row * K, K, gl, v);
 }
 
 template <int L, int V>
@@ -163,22 +214,16 @@ __global__ __launch_bounds__(256) void softmax_bwd_rows_kernel(int K, int64_t ro
     const bool live = row < rows;
     const int64_t base = (live ? row : 0) * K;
     float av[V], dv[V];
+    load_row<L, V>(A + base, K, gl, live, 0.f, av);
+    load_row<L, V>(dA + base, K, gl, live, 0.f, dv);
     float s = 0.f;
 #pragma unroll
-    for (int u = 0; u < V; ++u) {
-        const int t = gl + L * u;
-        const bool in = live && t < K;
-        av[u] = in ? A[base + t] : 0.f;
-        dv[u] = in ? dA[base + t] : 0.f;
-        s += av[u] * dv[u];
-    }
+    for (int u = 0; u < V; ++u) s += av[u] * dv[u];
     s = group_sum<L>(s);  // every read of the row precedes this, so dS may alias dA
     if (!live) return;
 #pragma unroll
-    for (int u = 0; u < V; ++u) {
-        const int t = gl + L * u;
-        if (t < K) dS[base + t] = av[u] * (dv[u] - s);
-    }
+    for (int u = 0; u < V; ++u) av[u] *= dv[u] - s;
+    store_row<L, V>(dS + base, K, gl, av);
 }
 
 // sum over a row's K contiguous slots, 16 lanes per row
