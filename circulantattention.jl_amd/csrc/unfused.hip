@@ -33,25 +33,35 @@ __global__ void pattern_kernel(Geom g, int64_t nb, int32_t *__restrict__ rowptr,
     }
 }
 
-// Same pattern with 32-bit index arithmetic (P * K < 2^31), one thread per
-// slot computing its column once for all batch copies.
-__global__ void pattern32_kernel(int nsp, int n1, int n2, int ws, int nb,
-                                 int32_t *__restrict__ rowptr, int32_t *__restrict__ colval) {
+// Same pattern with 32-bit index arithmetic (P * K < 2^31): 16 lanes per CSR
+// row, the row's border shifts computed once per lane, each slot's window
+// offsets from t = mm * ws + m0 (quotient by a float reciprocal, exact for
+// t < 2^22), all batch copies written from the same column.
+__global__ __launch_bounds__(256) void pattern32_kernel(int nsp, int n1, int n2, int ws, int nb,
+                                                        int32_t *__restrict__ rowptr,
+                                                        int32_t *__restrict__ colval) {
     const int p = (ws - 1) / 2;
     const int K = nsp == 1 ? ws : ws * ws;
     const int P = n1 * n2;
     const int PK = P * K;
-    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < PK; n += gridDim.x * blockDim.x) {
-        const int r = n / K, t = n - r * K;
+    const float inv_ws = 1.f / (float)ws;
+    const int gl = threadIdx.x & 15;
+    for (int r = blockIdx.x * 16 + (threadIdx.x >> 4); r < P; r += gridDim.x * 16) {
         const int i1 = r % n1, i2 = r / n1;
-        const int m0 = nsp == 1 ? t : t % ws;
-        const int d1 = slot_to_offset(m0, slot_shift(i1 + 1, n1, p), ws, p);
-        int col = pmod(i1 + d1, n1);
-        if (nsp == 2) {
-            const int d2 = slot_to_offset(t / ws, slot_shift(i2 + 1, n2, p), ws, p);
-            col += n1 * pmod(i2 + d2, n2);
+        const int s1 = slot_shift(i1 + 1, n1, p);
+        const int s2 = nsp == 2 ? slot_shift(i2 + 1, n2, p) : 0;
+        for (int t = gl; t < K; t += 16) {
+            int mm = nsp == 2 ? (int)(((float)t + 0.5f) * inv_ws) : 0;
+            const int m0 = t - mm * ws;
+            const int d1 = slot_to_offset(m0, s1, ws, p);
+            int col = pmod(i1 + d1, n1);
+            if (nsp == 2) {
+                const int d2 = slot_to_offset(mm, s2, ws, p);
+                col += n1 * pmod(i2 + d2, n2);
+            }
+            const int n = r * K + t;
+            for (int b = 0; b < nb; ++b) colval[n + (int64_t)b * PK] = col + 1;
         }
-        for (int b = 0; b < nb; ++b) colval[n + (int64_t)b * PK] = col + 1;
     }
     for (int r = blockIdx.x * blockDim.x + threadIdx.x; r <= P; r += gridDim.x * blockDim.x)
         for (int b = 0; b < nb; ++b) rowptr[r + (int64_t)b * (P + 1)] = 1 + K * r;
@@ -426,8 +436,9 @@ static inline unsigned grid_for(int64_t n, int threads, int64_t cap = 1 << 20) {
 
 hipError_t launch_pattern(const Geom &g, int64_t nb, int32_t *rowptr, int32_t *colval,
                           hipStream_t s) {
-    if (g.P * g.K < ((int64_t)1 << 31) - 1 && nb <= INT32_MAX) {
-        hipLaunchKernelGGL(pattern32_kernel, dim3(grid_for(g.P * g.K, 256, 1 << 16)), dim3(256), 0,
+    // the float quotient t / ws of pattern32_kernel is exact for ws < 1024
+    if (g.P * g.K < ((int64_t)1 << 31) - 1 && nb <= INT32_MAX && g.ws < 1024) {
+        hipLaunchKernelGGL(pattern32_kernel, dim3(grid_for(g.P * 16, 256, 1 << 16)), dim3(256), 0,
                            s, g.nsp, g.n1, g.n2, g.ws, (int)nb, rowptr, colval);
         return hipGetLastError();
     }
