@@ -122,7 +122,11 @@ def bench_ops(args):
     sp = ctypes.c_void_p(stream.cuda_stream)
     g = torch.Generator(device=dev)
     g.manual_seed(2000)
+    only_ops = set(filter(None, args.op.split(",")))
+    only_cfg = set(filter(None, args.ops_config.split(",")))
     for name, (dims, C, nb, ws, cplx) in OPS_CONFIGS.items():
+        if only_cfg and name not in only_cfg:
+            continue
         nsp = len(dims)
         n1, n2 = dims[0], (dims[1] if nsp == 2 else 1)
         P = int(math.prod(dims))
@@ -171,6 +175,8 @@ def bench_ops(args):
                                          ptr(Z), sp)),
         ]
         for op, nbytes, f in ops:
+            if only_ops and op not in only_ops:
+                continue
             for _ in range(args.warmup):
                 L.check(f())
             torch.cuda.synchronize()
@@ -214,6 +220,10 @@ def main():
                     help="instead of the fused step, time each unfused entry point (similarity, "
                          "softmax, apply, sums, axpby, pattern) at the cfg2 / cfg5 shapes and "
                          "print one JSON line per entry point (GB/s against HBM peak)")
+    ap.add_argument("--op", default="",
+                    help="with --ops: comma-separated entry points to time (default: all)")
+    ap.add_argument("--ops-config", default="",
+                    help="with --ops: comma-separated shapes to time (cfg2, cfg5; default: both)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the (head, batch) units "

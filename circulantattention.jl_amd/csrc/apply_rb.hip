@@ -40,6 +40,7 @@ namespace circatt {
 namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));  // 4-byte aligned
 
 constexpr int kR = 4;     // pixels per lane along dim 1
 constexpr int kCC = 8;    // real components per chunk of the whole-row kernel
@@ -619,18 +620,39 @@ __global__ __launch_bounds__(64, 2) void apply_rows_kernel(ApplyArgs a) {
 // wavefront owns 64 consecutive pixels of one image row; lane group r takes
 // window rows r, r + 4, ...; for one window row a lane accumulates the ws
 // slots of its 4 pixels over the channels (sequentially, as the reference
-// does) from one run of 4 + 2p key pixels per channel, then stores each
-// pixel's chunk of ws slots (contiguous in the row, rotated near borders).
+// does), then stores each pixel's chunk of ws slots (contiguous in the row,
+// rotated near borders).
+//
+// Per channel the wavefront stages, with 16-byte loads, the 4 key rows'
+// columns f1 - kHalo .. f1 + 63 + kHalo and its 64 query pixels into LDS
+// (3 load instructions for complex data instead of one overlapping run of
+// 4 + 2p pixels per lane); the lanes read their runs back from LDS.  The
+// loads of channel c + 1 are in flight while channel c is multiplied.
 // ---------------------------------------------------------------------------
+constexpr int kHalo = 8;  // staged key columns beyond each side (>= p)
+template <int NCOMP>
+struct SimStage {
+    static constexpr int RW = 64 + 2 * kHalo;  // staged key columns per row
+    static constexpr int RF = NCOMP * RW;      // floats per key row
+    static constexpr int KF = 4 * RF;          // key floats
+    static constexpr int SF = KF + NCOMP * 64; // floats per channel
+    static constexpr int SF4 = SF / 4;
+    static constexpr int NLD = (SF4 + 63) / 64;  // 16-byte loads per lane
+};
+
 template <int WS, int NCOMP, bool DIST, bool FAST>
 __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int c2, int b) {
+    using S = SimStage<NCOMP>;
     constexpr int P = (WS - 1) / 2;
     constexpr int K = WS * WS;
     constexpr int XW = kR + 2 * P;
-    constexpr int XN = NCOMP * XW;
-    constexpr int XN4 = (XN + 3) / 4;
-    constexpr int QN = NCOMP * kR;  // query floats of a lane per channel
     constexpr int NIT = (WS + 3) / 4;
+    // a lane's key run starts at staged column 4 l16 + kHalo - P; it is read
+    // from the 16-byte boundary AL floats before
+    constexpr int AL = (NCOMP * (kHalo - P)) % 4;
+    constexpr int KW4 = (NCOMP * XW + AL + 3) / 4;
+    constexpr int NB = FAST ? S::NLD : 4 * S::NLD;  // loads per lane per channel
+    static_assert(P <= kHalo, "window wider than the staged halo");
     const Geom &g = a.g;
     const int n1 = g.n1, n2 = g.n2;
     const int64_t Pp = g.P;
@@ -641,14 +663,11 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
     const auto rq = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, ubytes);  // rows (queries)
     const auto rk = rsrc(a.z + (int64_t)b * Pp * NCOMP * a.C, ubytes);  // columns (keys)
     float *nzb = a.y + (int64_t)b * Pp * K;
+    float *lw = circatt_lds_apply;
     int s1[kR];
 #pragma unroll
     for (int i = 0; i < kR; ++i) s1[i] = FAST ? 0 : shift0(pmod(f1 + 4 * l16 + i, n1), n1, P);
     const int s2 = slot_shift(c2 + 1, n2, P);
-    // query pixels of the lane (wrapped columns keep reads in range)
-    int qcol[kR];
-#pragma unroll
-    for (int i = 0; i < kR; ++i) qcol[i] = FAST ? f1 + 4 * l16 + i : pmod(f1 + 4 * l16 + i, n1);
     const int plane = (int)(NCOMP * Pp * 4);  // bytes per channel
 
     // window-row iterations [gc * ichunk, ...) of this wavefront
@@ -656,53 +675,100 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
     for (int itr = gc * a.ichunk; itr < it1; ++itr) {
         const int dd = 4 * itr + rho;
         const bool live = dd < WS;
-        const int ddc = live ? dd : WS - 1;
-        const int kr2 = pmod(c2 + ddc - P, n2);
-        const int mm = pmod(ddc + s2, WS);
-        const int qoff = NCOMP * (qcol[0] + n1 * c2) * 4;
-        const int koff = NCOMP * (n1 * kr2) * 4;
+        const int mm = pmod(min(dd, WS - 1) + s2, WS);
+        // byte offsets (within a channel) of this lane's staged values; a
+        // value of the staging area is a key (f < KF) or a query
+        int off[NB];
+#pragma unroll
+        for (int m = 0; m < NB; ++m) {
+            const int f = FAST ? 4 * (lane + 64 * m) : lane + 64 * m;  // first float
+            const int fr = f < S::SF ? f : 0;
+            if (fr < S::KF) {
+                const int rr = fr / S::RF, w = fr - rr * S::RF;
+                const int kr2 = pmod(c2 + min(4 * itr + rr, WS - 1) - P, n2);
+                if (FAST) {
+                    off[m] = (NCOMP * (n1 * kr2 + f1 - kHalo) + w) * 4;
+                } else {
+                    const int u = w / NCOMP, e = w - u * NCOMP;
+                    off[m] = (NCOMP * (n1 * kr2 + pmod(f1 - kHalo + u, n1)) + e) * 4;
+                }
+            } else {
+                const int w = fr - S::KF;
+                if (FAST) {
+                    off[m] = (NCOMP * (n1 * c2 + f1) + w) * 4;
+                } else {
+                    const int u = w / NCOMP, e = w - u * NCOMP;
+                    off[m] = (NCOMP * (n1 * c2 + pmod(f1 + u, n1)) + e) * 4;
+                }
+            }
+        }
+        // staged values of one channel, in registers
+        auto load_stage = [&](float (&st)[4 * S::NLD], int c) {
+            const int cb = __builtin_amdgcn_readfirstlane(c * plane);
+#pragma unroll
+            for (int m = 0; m < NB; ++m) {
+                const int s = FAST ? lane + 64 * m : (lane + 64 * m) / 4;
+                // the first key / query boundary and the end are multiples of 16
+                // values, so a 16-byte slot is all key or all query
+                const int f0 = FAST ? 4 * s : lane + 64 * m;
+                if (f0 >= S::SF) continue;
+                if (FAST) {
+                    const f4 v = f0 < S::KF ? bload4(rk, off[m], cb) : bload4(rq, off[m], cb);
+                    st[4 * m] = v[0];
+                    st[4 * m + 1] = v[1];
+                    st[4 * m + 2] = v[2];
+                    st[4 * m + 3] = v[3];
+                } else {
+                    st[m] = f0 < S::KF ? bload(rk, off[m], cb) : bload(rq, off[m], cb);
+                }
+            }
+        };
+        auto store_stage = [&](const float (&st)[4 * S::NLD]) {
+            if (FAST) {
+#pragma unroll
+                for (int m = 0; m < S::NLD; ++m) {
+                    const int s = lane + 64 * m;
+                    if (4 * s < S::SF) *(f4 *)(lw + 4 * s) = f4{st[4 * m], st[4 * m + 1], st[4 * m + 2], st[4 * m + 3]};
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < NB; ++m) {
+                    const int f = lane + 64 * m;
+                    if (f < S::SF) lw[f] = st[m];
+                }
+            }
+        };
+
         float acc[kR][WS];
 #pragma unroll
         for (int i = 0; i < kR; ++i)
 #pragma unroll
             for (int j = 0; j < WS; ++j) acc[i][j] = 0.f;
+        float st[4 * S::NLD];
+        load_stage(st, 0);
 #pragma unroll 1
         for (int c = 0; c < a.C; ++c) {
-            float q[QN], kw[4 * XN4];
-            const int cb = c * plane;
-            if (FAST) {
+            // the previous channel's LDS reads were consumed by its products,
+            // and LDS operations of a wavefront complete in order
+            store_stage(st);
+            if (c + 1 < a.C) load_stage(st, c + 1);
+            float q[4 * NCOMP], kw[4 * KW4];
 #pragma unroll
-                for (int h = 0; h < QN / 4; ++h) {
-                    const f4 v = bload4(rq, qoff + cb, 16 * h);
-                    q[4 * h] = v[0];
-                    q[4 * h + 1] = v[1];
-                    q[4 * h + 2] = v[2];
-                    q[4 * h + 3] = v[3];
-                }
-                const int vo = koff + cb + NCOMP * (f1 + 4 * l16 - P) * 4;
+            for (int h = 0; h < NCOMP; ++h) {
+                const f4 v = *(const f4 *)(lw + S::KF + NCOMP * 4 * l16 + 4 * h);
+                q[4 * h] = v[0];
+                q[4 * h + 1] = v[1];
+                q[4 * h + 2] = v[2];
+                q[4 * h + 3] = v[3];
+            }
+            const float *kr = lw + rho * S::RF + NCOMP * (4 * l16 + kHalo - P) - AL;
 #pragma unroll
-                for (int h = 0; h < XN4; ++h) {
-                    const f4 v = bload4(rk, vo, 16 * h);
-                    kw[4 * h] = v[0];
-                    kw[4 * h + 1] = v[1];
-                    kw[4 * h + 2] = v[2];
-                    kw[4 * h + 3] = v[3];
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < kR; ++i)
-#pragma unroll
-                    for (int e = 0; e < NCOMP; ++e)
-                        q[NCOMP * i + e] =
-                            bload(rq, cb + (NCOMP * (qcol[i] + n1 * c2) + e) * 4, 0);
-                int xc = pmod(f1 + 4 * l16 - P, n1);
-#pragma unroll
-                for (int w = 0; w < XW; ++w) {
-#pragma unroll
-                    for (int e = 0; e < NCOMP; ++e)
-                        kw[NCOMP * w + e] = bload(rk, koff + cb + (NCOMP * xc + e) * 4, 0);
-                    xc = xc + 1 == n1 ? 0 : xc + 1;
-                }
+            for (int h = 0; h < KW4; ++h) {
+                const f4 v = *(const f4 *)(kr + 4 * h);
+                kw[4 * h] = v[0];
+                kw[4 * h + 1] = v[1];
+                kw[4 * h + 2] = v[2];
+                kw[4 * h + 3] = v[3];
             }
 #pragma unroll
             for (int i = 0; i < kR; ++i)
@@ -710,7 +776,7 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
                 for (int j = 0; j < WS; ++j)
 #pragma unroll
                     for (int e = 0; e < NCOMP; ++e) {
-                        const float xv = q[NCOMP * i + e], yv = kw[NCOMP * (i + j) + e];
+                        const float xv = q[NCOMP * i + e], yv = kw[AL + NCOMP * (i + j) + e];
                         if (DIST) {
                             const float d = xv - yv;
                             acc[i][j] = __builtin_fmaf(d, d, acc[i][j]);
@@ -719,24 +785,66 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
                         }
                     }
         }
-        if (!live) continue;
+        // the slot shifts are redefined here, so that the store addresses
+        // are not computed before the channel loop and held through it
+#pragma unroll
+        for (int i = 0; i < kR; ++i) asm volatile("" : "+v"(s1[i]));
         const float sc = DIST ? -0.5f * a.scale : a.scale;
+        // the live window rows of this iteration, mm0 .. mm0 + nlive - 1,
+        // are one run of each pixel's nzVal row unless the slot order wraps
+        const int nlive = min(4, WS - 4 * itr);
+        const int mm0 = pmod(4 * itr + s2, WS);
+        if (mm0 + nlive <= WS) {
+            // through LDS (the staging area is free: LDS operations complete
+            // in order), then 16 lanes per pixel store its run of nlive * ws
+            // floats with 16-byte stores, 4 pixels per instruction
+            constexpr int PS = 4 * WS;  // LDS floats per pixel
+            if (live) {
 #pragma unroll
-        for (int i = 0; i < kR; ++i) {
-            const int col = f1 + 4 * l16 + i;
-            if (col >= n1) continue;
-            float *row = nzb + (col + (int64_t)n1 * c2) * K + mm * WS;
+                for (int i = 0; i < kR; ++i)
 #pragma unroll
-            for (int j = 0; j < WS; ++j) row[FAST ? j : fold(j + s1[i], WS)] = acc[i][j] * sc;
+                    for (int j = 0; j < WS; ++j)
+                        lw[(4 * l16 + i) * PS + rho * WS + (FAST ? j : fold(j + s1[i], WS))] =
+                            acc[i][j] * sc;
+            }
+            const int run = nlive * WS, tq = lane & 15, g4 = lane >> 4;
+#pragma unroll 4
+            for (int m = 0; m < 16; ++m) {
+                const int px = 4 * m + g4, col = f1 + px;
+                const f4 v = *(const f4 *)(lw + px * PS + 4 * tq);
+                float *dst = nzb + (col + (int64_t)n1 * c2) * K + mm0 * WS + 4 * tq;
+                if (col >= n1 || 4 * tq >= run) continue;
+                if (4 * tq + 4 <= run) {
+                    *(f4u *)dst = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 3; ++e)
+                        if (4 * tq + e < run) dst[e] = v[e];
+                }
+            }
+        } else if (live) {
+#pragma unroll
+            for (int i = 0; i < kR; ++i) {
+                const int col = f1 + 4 * l16 + i;
+                if (col >= n1) continue;
+                float *row = nzb + (col + (int64_t)n1 * c2) * K + mm * WS;
+#pragma unroll
+                for (int j = 0; j < WS; ++j) row[FAST ? j : fold(j + s1[i], WS)] = acc[i][j] * sc;
+            }
         }
     }
 }
 
 // One wavefront per (64 pixels of an image row, unit).  Fields of ApplyArgs:
-// x = rows (queries), z = columns (keys), y = nzVal.
+// x = rows (queries), z = columns (keys), y = nzVal.  The dispatcher deals
+// workgroups round robin over the 8 XCDs; work item (bid % 8) * nper + bid / 8
+// gives each XCD a contiguous band of image rows, whose key rows stay in its
+// L2 for the wavefronts of the neighbouring rows.
 template <int WS, int NCOMP, bool DIST>
-__global__ __launch_bounds__(64, 2) void sim_rows_kernel(ApplyArgs a) {
-    int it = blockIdx.x;
+__global__ __launch_bounds__(64, 2) void sim_rows_kernel(ApplyArgs a, int nwork) {
+    const int nper = (nwork + 7) >> 3;
+    int it = (int)(blockIdx.x & 7) * nper + (int)(blockIdx.x >> 3);
+    if (it >= nwork) return;
     const int gc = __builtin_amdgcn_readfirstlane(it % a.gchunk);
     it /= a.gchunk;
     const int t1 = __builtin_amdgcn_readfirstlane(it % a.tiles1);
@@ -823,8 +931,9 @@ template <int WS, int NCOMP, bool DIST>
 hipError_t launch_sim_t(ApplyArgs a, int64_t nb, hipStream_t s) {
     const int tiles1 = (a.g.n1 + 63) / 64;
     a.tiles1 = tiles1;
-    a.fa = (a.g.p + 63) / 64;
-    a.fb = a.g.n1 - 64 - a.g.p >= 0 ? (a.g.n1 - 64 - a.g.p) / 64 + 1 : 0;
+    // interior tiles: staged key columns f1 - kHalo .. f1 + 63 + kHalo in range
+    a.fa = (kHalo + 63) / 64;
+    a.fb = a.g.n1 - 64 - kHalo >= 0 ? (a.g.n1 - 64 - kHalo) / 64 + 1 : 0;
     if (a.fb > tiles1) a.fb = tiles1;
     if (a.fb < a.fa) a.fb = a.fa;
     // window-row iterations split over wavefronts when the grid is small
@@ -832,8 +941,14 @@ hipError_t launch_sim_t(ApplyArgs a, int64_t nb, hipStream_t s) {
     const int64_t waves = (int64_t)tiles1 * a.g.n2 * nb;
     a.ichunk = waves >= 2048 ? NIT : std::max(1, (int)((int64_t)NIT * waves / 2048));
     a.gchunk = (NIT + a.ichunk - 1) / a.ichunk;
-    const int64_t grid = waves * a.gchunk;
-    hipLaunchKernelGGL((sim_rows_kernel<WS, NCOMP, DIST>), dim3((unsigned)grid), dim3(64), 0, s, a);
+    const int64_t nwork = waves * a.gchunk;
+    const int64_t grid = 8 * ((nwork + 7) / 8);
+    // LDS: the staging area, which also holds 64 pixels x 4 window rows of
+    // results before they are stored (plus the 16 floats that the last
+    // pixel's 16 lanes read past its 4 ws)
+    const size_t lds = (size_t)std::max(SimStage<NCOMP>::SF, 64 * 4 * WS + 64) * sizeof(float);
+    hipLaunchKernelGGL((sim_rows_kernel<WS, NCOMP, DIST>), dim3((unsigned)grid), dim3(64), lds, s,
+                       a, (int)nwork);
     return hipGetLastError();
 }
 
@@ -857,7 +972,7 @@ bool sim_rows_supported(const Geom &g, int C, int ncomp, int64_t nb) {
     if (g.nsp != 2 || g.ws < 3 || g.ws > 15 || (g.ws & 1) == 0) return false;
     if (g.P * g.K * 4 >= (int64_t)1 << 31) return false;
     if (g.P * ncomp * C * 4 >= (int64_t)1 << 31) return false;
-    const int64_t grid = (int64_t)((g.n1 + 63) / 64) * g.n2 * nb;
+    const int64_t grid = (int64_t)((g.n1 + 63) / 64) * g.n2 * nb * ((g.ws + 3) / 4) + 8;
     return grid > 0 && grid < ((int64_t)1 << 31);
 }
 bool sim_rows_preferred(const Geom &g, int64_t nb) {
