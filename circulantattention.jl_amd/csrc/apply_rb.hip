@@ -857,6 +857,304 @@ __global__ __launch_bounds__(64, 2) void sim_rows_kernel(ApplyArgs a, int nwork)
         sim_body<WS, NCOMP, DIST, false>(a, gc, t1, c2, b);
 }
 
+// ---------------------------------------------------------------------------
+// 2D apply, both directions (apply2_kernel): a wavefront owns 64 output
+// pixels of one image row and a pass of 4 x kCG components; lane group g
+// (lane >> 4) owns components g kCG .. g kCG + kCG - 1 of the pass, so no
+// partial sums are exchanged.  Per window row dd it stages, by LDS-DMA, the
+// slot chunk that row needs of every pixel involved (the 64 own pixels for
+// A ⊗ x, the 64 + 2p source pixels for Aᵀ ⊗ x) and reads the lane's 4 x ws
+// coefficients back into registers; the DMA of the next row's chunks is then
+// in flight during the products.  x is staged one channel per lane group and
+// step (the rows' columns f1 - kHalo .. f1 + 63 + kHalo, 16-byte loads), and
+// the loads of the next step are in flight during the products.
+//   forward:    y[o] += A[o, slot(o, (j - p, dd - p))] x[o + (j - p, dd - p)]
+//   transposed: y[o] += A[s, slot(s, (p - j, dd - p))] x[s], s = o - (p - j, dd - p)
+// ---------------------------------------------------------------------------
+constexpr int kCG = 8;          // components per lane group and pass
+constexpr int kCPass = 4 * kCG; // components per pass
+
+template <int WS, int NCOMP, bool TRANS>
+struct A2 {
+    static constexpr int P = (WS - 1) / 2;
+    static constexpr int NSRC = TRANS ? 64 + 2 * P : 64;  // staged chunks per row
+    static constexpr int NZF = NSRC * WS;
+    static constexpr int NZL = (NZF + 63) / 64;           // DMA loads per lane
+    static constexpr int NZB = NZL * 64;                  // nzVal buffer floats
+    static constexpr int RF = NCOMP * (64 + 2 * kHalo);   // x floats per group
+    static constexpr int XF = 4 * RF;
+    static constexpr int XL = (XF / 4 + 63) / 64;         // 16-byte loads per lane
+    static constexpr int CHS = kCG / NCOMP;               // channels per group and pass
+    static constexpr int LDS = NZB + XF + 4;  // a lane's last x read may pass its row by 3
+    static constexpr int EDGE = kHalo > 2 * P ? kHalo : 2 * P;  // interior margin
+};
+
+template <int WS, int NCOMP, bool TRANS, bool FAST>
+__device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1, int c2, int b) {
+    using S = A2<WS, NCOMP, TRANS>;
+    constexpr int P = S::P;
+    constexpr int K = WS * WS;
+    constexpr int XW = kR + 2 * P;
+    constexpr int AL = (NCOMP * (kHalo - P)) % 4;
+    constexpr int KW4 = (NCOMP * XW + AL + 3) / 4;
+    constexpr int NB = FAST ? S::XL : 4 * S::XL;  // x loads per lane per step
+    typedef __attribute__((address_space(3))) void *lptr;
+    const Geom &g = a.g;
+    const int n1 = g.n1, n2 = g.n2;
+    const int64_t Pp = g.P;
+    const int lane = threadIdx.x & 63;
+    const int l16 = lane & 15, grp = lane >> 4;
+    const int f1 = t1 * 64;
+    float *lz = circatt_lds_apply;   // staged chunks
+    float *lx = lz + S::NZB;         // staged x
+    const auto rs = rsrc(a.nz + (int64_t)b * Pp * K, Pp * K * 4);
+    const int ubytes = (int)(Pp * NCOMP * a.C * 4);
+    const auto rx = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, ubytes);
+    const int plane = (int)(NCOMP * Pp * 4);  // bytes per channel
+    const int s2own = slot_shift(c2 + 1, n2, P);
+
+    // chunk DMA: lane float f = lane + 64 m of a staged row is element e of
+    // chunk w (source column f1 - off + w, wrapped); its byte offset within
+    // an image row of nzVal does not depend on the window row
+    int zo[S::NZL];
+#pragma unroll
+    for (int m = 0; m < S::NZL; ++m) {
+        const int f = min(lane + 64 * m, S::NZF - 1);
+        const int w = f / WS, e = f - w * WS;
+        const int col = FAST ? f1 - (TRANS ? P : 0) + w : pmod(f1 - (TRANS ? P : 0) + w, n1);
+        zo[m] = (col * K + e) * 4;
+    }
+    // image row and chunk index of window row dd
+    auto zrow = [&](int dd, int &r2, int &mm) {
+        if (TRANS) {
+            const int d2 = dd - P;  // output row - source row
+            r2 = pmod(c2 - d2, n2);
+            mm = pmod(dd + slot_shift(r2 + 1, n2, P), WS);
+        } else {
+            r2 = c2;
+            mm = pmod(dd + s2own, WS);
+        }
+    };
+    auto stage_z = [&](int dd) {
+        int r2, mm;
+        zrow(dd, r2, mm);
+        const int so = __builtin_amdgcn_readfirstlane((n1 * r2 * K + mm * WS) * 4);
+#pragma unroll
+        for (int m = 0; m < S::NZL; ++m) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(lz + 64 * m), 4, zo[m], so, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // x staging: lane value (16-byte slot, or float in the border body) of
+    // group gs = f / RF, column w, at step 0 and image row 0.  A group's
+    // channels past C lie past the unit's bytes: the buffer range check makes
+    // their reads zero (they are never stored)
+    const int ch0 = pass * (kCPass / NCOMP);  // first channel of the pass
+    int xo[NB];
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+        const int f = FAST ? 4 * (lane + 64 * m) : lane + 64 * m;
+        const int fr = f < S::XF ? f : 0;
+        const int gs = fr / S::RF, w = fr - gs * S::RF;
+        const int chan = (ch0 + gs * S::CHS) * plane;
+        if (FAST) {
+            xo[m] = chan + (NCOMP * (f1 - kHalo) + w) * 4;
+        } else {
+            const int u = w / NCOMP, e = w - u * NCOMP;
+            xo[m] = chan + (NCOMP * pmod(f1 - kHalo + u, n1) + e) * 4;
+        }
+    }
+    auto x_row = [&](int dd) {
+        int r2, mm;
+        if (TRANS) {
+            zrow(dd, r2, mm);
+        } else {
+            r2 = pmod(c2 + dd - P, n2);
+        }
+        return r2;
+    };
+    auto load_x = [&](float (&st)[4 * S::XL], int dd, int cl) {
+        // one scalar per step (opaque, so that no per-step offsets are
+        // computed ahead of the loop); the whole offset is in the vector
+        // operand, which the range check sees
+        const int so = __builtin_amdgcn_readfirstlane(NCOMP * n1 * x_row(dd) * 4 + cl * plane);
+#pragma unroll
+        for (int m = 0; m < NB; ++m) {
+            const int f0 = FAST ? 4 * (lane + 64 * m) : lane + 64 * m;
+            if (f0 >= S::XF) continue;
+            const int vo = xo[m] + so;
+            if (FAST) {
+                const f4 v = bload4(rx, vo, 0);
+                st[4 * m] = v[0];
+                st[4 * m + 1] = v[1];
+                st[4 * m + 2] = v[2];
+                st[4 * m + 3] = v[3];
+            } else {
+                st[m] = bload(rx, vo, 0);
+            }
+        }
+    };
+    auto store_x = [&](const float (&st)[4 * S::XL]) {
+        if (FAST) {
+#pragma unroll
+            for (int m = 0; m < S::XL; ++m) {
+                const int s = lane + 64 * m;
+                if (4 * s < S::XF)
+                    *(f4 *)(lx + 4 * s) = f4{st[4 * m], st[4 * m + 1], st[4 * m + 2], st[4 * m + 3]};
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < NB; ++m) {
+                const int f = lane + 64 * m;
+                if (f < S::XF) lx[f] = st[m];
+            }
+        }
+    };
+
+    float acc[kR][kCG];
+    float asum[kR];
+#pragma unroll
+    for (int i = 0; i < kR; ++i) {
+        asum[i] = 0.f;
+#pragma unroll
+        for (int k = 0; k < kCG; ++k) acc[i][k] = 0.f;
+    }
+    float st[4 * S::XL];
+    stage_z(0);
+    load_x(st, 0, 0);
+#pragma unroll 1
+    for (int dd = 0; dd < WS; ++dd) {
+        int f1v = f1;
+        asm volatile("" : "+v"(f1v));
+        __builtin_amdgcn_s_waitcnt(kWaitAll);  // this row's chunks are in LDS
+        float av[kR][WS];
+#pragma unroll
+        for (int i = 0; i < kR; ++i) {
+            int c1 = 0, s1 = 0;
+            if (!FAST) {
+                c1 = pmod(f1v + 4 * l16 + i + (TRANS ? P : 0), n1);
+                if (!TRANS) s1 = shift0(c1, n1, P);
+            }
+#pragma unroll
+            for (int j = 0; j < WS; ++j) {
+                const int u = TRANS ? 4 * l16 + i - j + 2 * P : 4 * l16 + i;
+                int pos = j;
+                if (!FAST) {
+                    if (TRANS) {
+                        pos = fold(j + shift0(c1, n1, P), WS);
+                        c1 = c1 == 0 ? n1 - 1 : c1 - 1;
+                    } else {
+                        pos = fold(j + s1, WS);
+                    }
+                }
+                av[i][j] = lz[u * WS + pos];
+            }
+        }
+        // the coefficients are in registers before the buffer is refilled
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+        if (dd + 1 < WS) stage_z(dd + 1);
+        if (a.corr) {
+#pragma unroll
+            for (int i = 0; i < kR; ++i)
+#pragma unroll
+                for (int j = 0; j < WS; ++j) asum[i] += av[i][j];
+        }
+#pragma unroll
+        for (int cl = 0; cl < S::CHS; ++cl) {
+            // nothing is scheduled across steps (the loads of later steps
+            // would be issued early into registers of their own)
+            __builtin_amdgcn_sched_barrier(0);
+            // LDS operations of a wavefront complete in order: the previous
+            // step's reads of lx are done before these writes
+            store_x(st);
+            if (cl + 1 < S::CHS)
+                load_x(st, dd, cl + 1);
+            else if (dd + 1 < WS)
+                load_x(st, dd + 1, 0);
+            float xw[4 * KW4];
+            const float *xr = lx + grp * S::RF + NCOMP * (4 * l16 + kHalo - P) - AL;
+#pragma unroll
+            for (int h = 0; h < KW4; ++h) {
+                const f4 v = *(const f4 *)(xr + 4 * h);
+                xw[4 * h] = v[0];
+                xw[4 * h + 1] = v[1];
+                xw[4 * h + 2] = v[2];
+                xw[4 * h + 3] = v[3];
+            }
+#pragma unroll
+            for (int i = 0; i < kR; ++i)
+#pragma unroll
+                for (int j = 0; j < WS; ++j)
+#pragma unroll
+                    for (int e = 0; e < NCOMP; ++e)
+                        acc[i][NCOMP * cl + e] = __builtin_fmaf(
+                            av[i][j], xw[AL + NCOMP * (TRANS ? i - j + 2 * P : i + j) + e],
+                            acc[i][NCOMP * cl + e]);
+        }
+    }
+    // group grp stores channels ch0 + grp CHS + cl: 4 pixels x NCOMP
+    // consecutive floats per lane, 16 lanes per contiguous run
+    float *yb = a.y + (int64_t)b * Pp * NCOMP * a.C;
+    const float *zb = a.z ? a.z + (int64_t)b * Pp * NCOMP * a.C : nullptr;
+    const int col0 = f1 + 4 * l16;
+    const int64_t pix0 = col0 + (int64_t)n1 * c2;
+#pragma unroll
+    for (int cl = 0; cl < S::CHS; ++cl) {
+        const int ch = ch0 + grp * S::CHS + cl;
+        if (ch >= a.C) break;
+        float v[kR * NCOMP];
+#pragma unroll
+        for (int i = 0; i < kR; ++i)
+#pragma unroll
+            for (int e = 0; e < NCOMP; ++e) v[NCOMP * i + e] = acc[i][NCOMP * cl + e];
+        float *dst = yb + NCOMP * (pix0 + Pp * ch);
+        const float *zs = a.corr ? zb + NCOMP * (pix0 + Pp * ch) : nullptr;
+        if (col0 + kR <= n1) {
+#pragma unroll
+            for (int h = 0; h < NCOMP; ++h) {
+                f4 r = f4{v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
+                if (a.corr) {
+                    const f4u z = *(const f4u *)(zs + 4 * h);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) r[q] -= asum[(4 * h + q) / NCOMP] * z[q];
+                }
+                *(f4u *)(dst + 4 * h) = r * a.scale;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kR; ++i) {
+                if (col0 + i >= n1) break;
+#pragma unroll
+                for (int e = 0; e < NCOMP; ++e) {
+                    float r = v[NCOMP * i + e];
+                    if (a.corr) r -= asum[i] * zs[NCOMP * i + e];
+                    dst[NCOMP * i + e] = r * a.scale;
+                }
+            }
+        }
+    }
+}
+
+// One wavefront per (64 output pixels of an image row, component pass, unit);
+// work items in XCD bands as in sim_rows_kernel.
+template <int WS, int NCOMP, bool TRANS>
+__global__ __launch_bounds__(64, 2) void apply2_kernel(ApplyArgs a, int nwork) {
+    const int nper = (nwork + 7) >> 3;
+    int it = (int)(blockIdx.x & 7) * nper + (int)(blockIdx.x >> 3);
+    if (it >= nwork) return;
+    const int pass = __builtin_amdgcn_readfirstlane(it % a.gchunk);
+    it /= a.gchunk;
+    const int t1 = __builtin_amdgcn_readfirstlane(it % a.tiles1);
+    it /= a.tiles1;
+    const int c2 = __builtin_amdgcn_readfirstlane(it % a.g.n2);
+    const int b = __builtin_amdgcn_readfirstlane(it / a.g.n2);
+    if (t1 >= a.fa && t1 < a.fb)
+        apply2_body<WS, NCOMP, TRANS, true>(a, pass, t1, c2, b);
+    else
+        apply2_body<WS, NCOMP, TRANS, false>(a, pass, t1, c2, b);
+}
+
 // Interior tile columns [fa, fb): every lane row 2p or more inside dim 1.
 inline void interior_cols(const Geom &g, int &fa, int &fb) {
     const int tw = tile_w(g.nsp), tiles1 = (g.n1 + tw - 1) / tw;
@@ -869,6 +1167,21 @@ inline void interior_cols(const Geom &g, int &fa, int &fb) {
 
 template <int WS, int NCOMP, bool TRANS>
 hipError_t launch_rb(ApplyArgs a, int64_t nb, hipStream_t s) {
+    if (a.g.nsp == 2) {
+        using S = A2<WS, NCOMP, TRANS>;
+        const int tiles1 = (a.g.n1 + 63) / 64;
+        a.tiles1 = tiles1;
+        a.fa = (S::EDGE + 63) / 64;
+        a.fb = a.g.n1 - 64 - S::EDGE >= 0 ? (a.g.n1 - 64 - S::EDGE) / 64 + 1 : 0;
+        if (a.fb > tiles1) a.fb = tiles1;
+        if (a.fb < a.fa) a.fb = a.fa;
+        a.gchunk = (NCOMP * a.C + kCPass - 1) / kCPass;  // component passes
+        const int64_t nwork = (int64_t)tiles1 * a.g.n2 * nb * a.gchunk;
+        const int64_t grid = 8 * ((nwork + 7) / 8);
+        hipLaunchKernelGGL((apply2_kernel<WS, NCOMP, TRANS>), dim3((unsigned)grid), dim3(64),
+                           (size_t)S::LDS * sizeof(float), s, a, (int)nwork);
+        return hipGetLastError();
+    }
     if (!TRANS && a.g.nsp == 2) {
         // whole-row kernel: interior when no x wrap and no slot shift
         const int tiles1 = (a.g.n1 + 63) / 64;
