@@ -861,35 +861,54 @@ __global__ __launch_bounds__(64, 2) void sim_rows_kernel(ApplyArgs a, int nwork)
 // 2D apply, both directions (apply2_kernel): a wavefront owns 64 output
 // pixels of one image row and a pass of 4 x kCG components; lane group g
 // (lane >> 4) owns components g kCG .. g kCG + kCG - 1 of the pass, so no
-// partial sums are exchanged.  Per window row dd it stages, by LDS-DMA, the
-// slot chunk that row needs of every pixel involved (the 64 own pixels for
-// A ⊗ x, the 64 + 2p source pixels for Aᵀ ⊗ x) and reads the lane's 4 x ws
-// coefficients back into registers; the DMA of the next row's chunks is then
-// in flight during the products.  x is staged one channel per lane group and
-// step (the rows' columns f1 - kHalo .. f1 + 63 + kHalo, 16-byte loads), and
-// the loads of the next step are in flight during the products.
+// partial sums are exchanged.  Per window row dd the wavefront needs one slot
+// chunk of every pixel involved (the 64 own pixels for A ⊗ x, the 64 + 2p
+// source pixels for Aᵀ ⊗ x); per step (window row, channel of each group) it
+// needs the x row's columns f1 - kHalo .. f1 + 63 + kHalo.  Both are staged
+// by LDS-DMA into rings (2 chunk buffers, 3 x buffers), x two steps ahead
+// and the chunks of row dd + 1 during row dd, so that the loads' latency is
+// covered by two steps of products.  Loads return in issue order: each step
+// waits with a vmcnt that counts exactly the loads issued after the ones it
+// needs.
 //   forward:    y[o] += A[o, slot(o, (j - p, dd - p))] x[o + (j - p, dd - p)]
 //   transposed: y[o] += A[s, slot(s, (p - j, dd - p))] x[s], s = o - (p - j, dd - p)
 // ---------------------------------------------------------------------------
 constexpr int kCG = 8;          // components per lane group and pass
 constexpr int kCPass = 4 * kCG; // components per pass
 
+// s_waitcnt vmcnt(N) (gfx9 encoding, expcnt and lgkmcnt at their maximum)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt has 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 template <int WS, int NCOMP, bool TRANS>
 struct A2 {
     static constexpr int P = (WS - 1) / 2;
     static constexpr int NSRC = TRANS ? 64 + 2 * P : 64;  // staged chunks per row
-    static constexpr int NZF = NSRC * WS;
-    static constexpr int NZL = (NZF + 63) / 64;           // DMA loads per lane
-    static constexpr int NZB = NZL * 64;                  // nzVal buffer floats
+    static constexpr int WSP = (WS + 3) & ~3;             // LDS floats per chunk
+    static constexpr int Q = WSP / 4;                     // 16-byte pieces per chunk
+    static constexpr int NZ4 = (NSRC * Q + 63) / 64;      // interior: 16-byte DMA loads per lane
+    static constexpr int NZ1 = (NSRC * WSP + 63) / 64;    // border: 4-byte DMA loads per lane
+    static constexpr int NZB = NZ4 * 256 > NZ1 * 64 ? NZ4 * 256 : NZ1 * 64;  // chunk buffer floats
     static constexpr int RF = NCOMP * (64 + 2 * kHalo);   // x floats per group
     static constexpr int XF = 4 * RF;
-    static constexpr int XL = (XF / 4 + 63) / 64;         // 16-byte loads per lane
+    static constexpr int XL = (XF / 4 + 63) / 64;         // interior: 16-byte DMA loads per lane
+    static constexpr int XBF = XL * 256;                  // x buffer floats (border: 4 XL dword loads)
     static constexpr int CHS = kCG / NCOMP;               // channels per group and pass
-    static constexpr int LDS = NZB + XF + 4;  // a lane's last x read may pass its row by 3
+    static constexpr int NZR = 2, NXB = 3;                // ring sizes
+    static constexpr int NZR_SUMS = 4;                    // column sums: chunks 3 rows ahead
+    // a lane's last x read may pass its row by 3 floats
+    static constexpr int LDS = NZR * NZB + NXB * XBF + 4;
+    static constexpr int LDS_SUMS = NZR_SUMS * NZB;
     static constexpr int EDGE = kHalo > 2 * P ? kHalo : 2 * P;  // interior margin
+    static_assert(CHS >= 2, "the step waits assume two or more steps per window row");
 };
 
-template <int WS, int NCOMP, bool TRANS, bool FAST>
+// SUMS: column sums only (x = 1, no products): out[o] = sum of the staged
+// coefficients, written to a.y (one float per pixel).
+template <int WS, int NCOMP, bool TRANS, bool FAST, bool SUMS = false>
 __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1, int c2, int b) {
     using S = A2<WS, NCOMP, TRANS>;
     constexpr int P = S::P;
@@ -897,7 +916,11 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
     constexpr int XW = kR + 2 * P;
     constexpr int AL = (NCOMP * (kHalo - P)) % 4;
     constexpr int KW4 = (NCOMP * XW + AL + 3) / 4;
-    constexpr int NB = FAST ? S::XL : 4 * S::XL;  // x loads per lane per step
+    constexpr int ZI = FAST ? S::NZ4 : S::NZ1;      // chunk loads per lane and row
+    constexpr int XI = FAST ? S::XL : 4 * S::XL;    // x loads per lane and step
+    constexpr int NZR = SUMS ? S::NZR_SUMS : S::NZR;
+    constexpr int T = WS * S::CHS;                  // steps
+    static_assert(ZI + XI < 64 && 3 * ZI < 64, "waits exceed vmcnt");
     typedef __attribute__((address_space(3))) void *lptr;
     const Geom &g = a.g;
     const int n1 = g.n1, n2 = g.n2;
@@ -905,24 +928,38 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
     const int lane = threadIdx.x & 63;
     const int l16 = lane & 15, grp = lane >> 4;
     const int f1 = t1 * 64;
-    float *lz = circatt_lds_apply;   // staged chunks
-    float *lx = lz + S::NZB;         // staged x
+    float *lz = circatt_lds_apply;   // chunk ring
+    float *lx = lz + NZR * S::NZB;   // x ring
     const auto rs = rsrc(a.nz + (int64_t)b * Pp * K, Pp * K * 4);
     const int ubytes = (int)(Pp * NCOMP * a.C * 4);
     const auto rx = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, ubytes);
     const int plane = (int)(NCOMP * Pp * 4);  // bytes per channel
     const int s2own = slot_shift(c2 + 1, n2, P);
 
-    // chunk DMA: lane float f = lane + 64 m of a staged row is element e of
-    // chunk w (source column f1 - off + w, wrapped); its byte offset within
-    // an image row of nzVal does not depend on the window row
-    int zo[S::NZL];
+    // Chunk DMA into lz[w * WSP + j] = slot j of chunk w (source column
+    // f1 - off + w, wrapped), in the order of window offsets: near the border
+    // of dim 1 the reference's circular shift of the slot order is undone
+    // here, by the element each lane loads, so the reads below use constant
+    // offsets in both bodies.  The interior body loads 16-byte pieces (the
+    // last piece of a chunk reads past it into the next chunk, or past the
+    // unit, where the range check returns zeros); the border body loads
+    // single slots.  A lane's byte offset within an image row of nzVal does
+    // not depend on the window row.
+    int zo[ZI];
 #pragma unroll
-    for (int m = 0; m < S::NZL; ++m) {
-        const int f = min(lane + 64 * m, S::NZF - 1);
-        const int w = f / WS, e = f - w * WS;
-        const int col = FAST ? f1 - (TRANS ? P : 0) + w : pmod(f1 - (TRANS ? P : 0) + w, n1);
-        zo[m] = (col * K + e) * 4;
+    for (int m = 0; m < ZI; ++m) {
+        const int off = TRANS ? P : 0;
+        if (FAST) {
+            const int s = min(lane + 64 * m, S::NSRC * S::Q - 1);
+            const int w = s / S::Q, q = s - w * S::Q;
+            zo[m] = ((f1 - off + w) * K + 4 * q) * 4;
+        } else {
+            const int f = min(lane + 64 * m, S::NSRC * S::WSP - 1);
+            const int w = f / S::WSP, j = f - w * S::WSP;
+            const int col = pmod(f1 - off + w, n1);
+            const int e = fold((j < WS ? j : 0) + shift0(col, n1, P), WS);
+            zo[m] = (col * K + e) * 4;
+        }
     }
     // image row and chunk index of window row dd
     auto zrow = [&](int dd, int &r2, int &mm) {
@@ -935,25 +972,33 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
             mm = pmod(dd + s2own, WS);
         }
     };
-    auto stage_z = [&](int dd) {
+    auto stage_z = [&](int dd, int buf) {
         int r2, mm;
         zrow(dd, r2, mm);
+        // the whole offset is in the vector operand, which the range check sees
         const int so = __builtin_amdgcn_readfirstlane((n1 * r2 * K + mm * WS) * 4);
+        float *dst = lz + buf * S::NZB;
 #pragma unroll
-        for (int m = 0; m < S::NZL; ++m) {
+        for (int m = 0; m < ZI; ++m) {
             __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(lz + 64 * m), 4, zo[m], so, 0, 0);
+            if (FAST)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(dst + 256 * m), 16, zo[m] + so,
+                                                        0, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(dst + 64 * m), 4, zo[m] + so, 0,
+                                                        0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    // x staging: lane value (16-byte slot, or float in the border body) of
-    // group gs = f / RF, column w, at step 0 and image row 0.  A group's
-    // channels past C lie past the unit's bytes: the buffer range check makes
-    // their reads zero (they are never stored)
+    // x DMA into lx[grp * RF + NCOMP * w + e] (column f1 - kHalo + w of the
+    // step's channel of group grp): lane value (16-byte piece, or float in
+    // the border body) f of group gs = f / RF.  A group's channels past C lie
+    // past the unit's bytes: the range check makes their reads zero (they
+    // are never stored).
     const int ch0 = pass * (kCPass / NCOMP);  // first channel of the pass
-    int xo[NB];
+    int xo[XI];
 #pragma unroll
-    for (int m = 0; m < NB; ++m) {
+    for (int m = 0; m < XI; ++m) {
         const int f = FAST ? 4 * (lane + 64 * m) : lane + 64 * m;
         const int fr = f < S::XF ? f : 0;
         const int gs = fr / S::RF, w = fr - gs * S::RF;
@@ -965,51 +1010,26 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
             xo[m] = chan + (NCOMP * pmod(f1 - kHalo + u, n1) + e) * 4;
         }
     }
-    auto x_row = [&](int dd) {
+    auto stage_x = [&](int t, int buf) {
+        const int dd = t / S::CHS, cl = t - dd * S::CHS;
         int r2, mm;
-        if (TRANS) {
+        if (TRANS)
             zrow(dd, r2, mm);
-        } else {
+        else
             r2 = pmod(c2 + dd - P, n2);
-        }
-        return r2;
-    };
-    auto load_x = [&](float (&st)[4 * S::XL], int dd, int cl) {
-        // one scalar per step (opaque, so that no per-step offsets are
-        // computed ahead of the loop); the whole offset is in the vector
-        // operand, which the range check sees
-        const int so = __builtin_amdgcn_readfirstlane(NCOMP * n1 * x_row(dd) * 4 + cl * plane);
+        const int so = __builtin_amdgcn_readfirstlane(NCOMP * n1 * r2 * 4 + cl * plane);
+        float *dst = lx + buf * S::XBF;
 #pragma unroll
-        for (int m = 0; m < NB; ++m) {
-            const int f0 = FAST ? 4 * (lane + 64 * m) : lane + 64 * m;
-            if (f0 >= S::XF) continue;
-            const int vo = xo[m] + so;
-            if (FAST) {
-                const f4 v = bload4(rx, vo, 0);
-                st[4 * m] = v[0];
-                st[4 * m + 1] = v[1];
-                st[4 * m + 2] = v[2];
-                st[4 * m + 3] = v[3];
-            } else {
-                st[m] = bload(rx, vo, 0);
-            }
+        for (int m = 0; m < XI; ++m) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (FAST)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lptr)(dst + 256 * m), 16, xo[m] + so,
+                                                        0, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lptr)(dst + 64 * m), 4, xo[m] + so, 0,
+                                                        0, 0);
         }
-    };
-    auto store_x = [&](const float (&st)[4 * S::XL]) {
-        if (FAST) {
-#pragma unroll
-            for (int m = 0; m < S::XL; ++m) {
-                const int s = lane + 64 * m;
-                if (4 * s < S::XF)
-                    *(f4 *)(lx + 4 * s) = f4{st[4 * m], st[4 * m + 1], st[4 * m + 2], st[4 * m + 3]};
-            }
-        } else {
-#pragma unroll
-            for (int m = 0; m < NB; ++m) {
-                const int f = lane + 64 * m;
-                if (f < S::XF) lx[f] = st[m];
-            }
-        }
+        __builtin_amdgcn_sched_barrier(0);
     };
 
     float acc[kR][kCG];
@@ -1020,60 +1040,101 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
 #pragma unroll
         for (int k = 0; k < kCG; ++k) acc[i][k] = 0.f;
     }
-    float st[4 * S::XL];
-    stage_z(0);
-    load_x(st, 0, 0);
-#pragma unroll 1
-    for (int dd = 0; dd < WS; ++dd) {
-        int f1v = f1;
-        asm volatile("" : "+v"(f1v));
-        __builtin_amdgcn_s_waitcnt(kWaitAll);  // this row's chunks are in LDS
-        float av[kR][WS];
+    // the lane's 4 x ws coefficients of window row dd, from chunk buffer zb
+    auto read_av = [&](float (&av)[kR][WS], int zb) {
+        const float *src = lz + zb * S::NZB;
 #pragma unroll
-        for (int i = 0; i < kR; ++i) {
-            int c1 = 0, s1 = 0;
-            if (!FAST) {
-                c1 = pmod(f1v + 4 * l16 + i + (TRANS ? P : 0), n1);
-                if (!TRANS) s1 = shift0(c1, n1, P);
-            }
+        for (int i = 0; i < kR; ++i)
 #pragma unroll
             for (int j = 0; j < WS; ++j) {
                 const int u = TRANS ? 4 * l16 + i - j + 2 * P : 4 * l16 + i;
-                int pos = j;
-                if (!FAST) {
-                    if (TRANS) {
-                        pos = fold(j + shift0(c1, n1, P), WS);
-                        c1 = c1 == 0 ? n1 - 1 : c1 - 1;
-                    } else {
-                        pos = fold(j + s1, WS);
-                    }
-                }
-                av[i][j] = lz[u * WS + pos];
+                av[i][j] = src[u * S::WSP + j];
             }
-        }
-        // the coefficients are in registers before the buffer is refilled
-        __builtin_amdgcn_s_waitcnt(kWaitLgkm);
-        if (dd + 1 < WS) stage_z(dd + 1);
-        if (a.corr) {
+    };
+
+    if (SUMS) {
+        // chunks NZR - 1 rows ahead; at row dd the loads of rows
+        // dd + 1 .. min(WS - 1, dd + NZR - 1) may stay in flight
+#pragma unroll
+        for (int r = 0; r < NZR - 1; ++r)
+            if (r < WS) stage_z(r, r);
+#pragma unroll 1
+        for (int dd = 0; dd < WS; ++dd) {
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm);  // row dd - 1's reads are done
+            if (dd + NZR - 1 < WS) stage_z(dd + NZR - 1, (dd + NZR - 1) % NZR);
+            const int younger = min(NZR - 1, WS - 1 - dd);
+            if (younger >= 3)
+                wait_vm<3 * ZI>();
+            else if (younger == 2)
+                wait_vm<2 * ZI>();
+            else if (younger == 1)
+                wait_vm<ZI>();
+            else
+                wait_vm<0>();
+            float av[kR][WS];
+            read_av(av, dd % NZR);
 #pragma unroll
             for (int i = 0; i < kR; ++i)
 #pragma unroll
                 for (int j = 0; j < WS; ++j) asum[i] += av[i][j];
         }
+        // every lane group holds the same sums; group 0 stores them
+        float *ob = a.y + (int64_t)b * Pp;
+        const int col0 = f1 + 4 * l16;
+        float *dst = ob + col0 + (int64_t)n1 * c2;
+        if (grp == 0) {
+            if (col0 + kR <= n1) {
+                *(f4u *)dst = f4{asum[0], asum[1], asum[2], asum[3]};
+            } else {
+#pragma unroll
+                for (int i = 0; i < kR; ++i)
+                    if (col0 + i < n1) dst[i] = asum[i];
+            }
+        }
+        return;
+    }
+
+    // issue order: chunks(0), x(0), x(1); step t issues [chunks(dd + 1) if
+    // cl == 0] then x(t + 2).  Loads issued after x(t): chunks(dd + 1) when
+    // cl == 1, and x(t + 1).
+    stage_z(0, 0);
+    stage_x(0, 0);
+    if (T > 1) stage_x(1, 1);
+    int xb = 0;  // x buffer of step t (t % NXB)
+    float av[kR][WS];
+#pragma unroll 1
+    for (int dd = 0; dd < WS; ++dd) {
 #pragma unroll
         for (int cl = 0; cl < S::CHS; ++cl) {
-            // nothing is scheduled across steps (the loads of later steps
-            // would be issued early into registers of their own)
+            const int t = dd * S::CHS + cl;
             __builtin_amdgcn_sched_barrier(0);
-            // LDS operations of a wavefront complete in order: the previous
-            // step's reads of lx are done before these writes
-            store_x(st);
-            if (cl + 1 < S::CHS)
-                load_x(st, dd, cl + 1);
-            else if (dd + 1 < WS)
-                load_x(st, dd + 1, 0);
+            const bool zy = cl == 1 && dd + 1 < WS;
+            const bool xy = t + 1 < T;
+            if (zy && xy)
+                wait_vm<ZI + XI>();
+            else if (zy)
+                wait_vm<ZI>();
+            else if (xy)
+                wait_vm<XI>();
+            else
+                wait_vm<0>();
+            if (cl == 0) {
+                // chunks(dd) arrived before x(t), which was issued after them
+                read_av(av, dd & 1);
+                if (a.corr) {
+#pragma unroll
+                    for (int i = 0; i < kR; ++i)
+#pragma unroll
+                        for (int j = 0; j < WS; ++j) asum[i] += av[i][j];
+                }
+            }
+            // the buffers refilled below were last read one step (x) or one
+            // row (chunks) ago; those reads are complete
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+            if (cl == 0 && dd + 1 < WS) stage_z(dd + 1, (dd + 1) & 1);
+            if (t + 2 < T) stage_x(t + 2, xb == 0 ? 2 : xb - 1);
             float xw[4 * KW4];
-            const float *xr = lx + grp * S::RF + NCOMP * (4 * l16 + kHalo - P) - AL;
+            const float *xr = lx + xb * S::XBF + grp * S::RF + NCOMP * (4 * l16 + kHalo - P) - AL;
 #pragma unroll
             for (int h = 0; h < KW4; ++h) {
                 const f4 v = *(const f4 *)(xr + 4 * h);
@@ -1091,6 +1152,7 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
                         acc[i][NCOMP * cl + e] = __builtin_fmaf(
                             av[i][j], xw[AL + NCOMP * (TRANS ? i - j + 2 * P : i + j) + e],
                             acc[i][NCOMP * cl + e]);
+            xb = xb == S::NXB - 1 ? 0 : xb + 1;
         }
     }
     // group grp stores channels ch0 + grp CHS + cl: 4 pixels x NCOMP
@@ -1138,7 +1200,7 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
 
 // One wavefront per (64 output pixels of an image row, component pass, unit);
 // work items in XCD bands as in sim_rows_kernel.
-template <int WS, int NCOMP, bool TRANS>
+template <int WS, int NCOMP, bool TRANS, bool SUMS = false>
 __global__ __launch_bounds__(64, 2) void apply2_kernel(ApplyArgs a, int nwork) {
     const int nper = (nwork + 7) >> 3;
     int it = (int)(blockIdx.x & 7) * nper + (int)(blockIdx.x >> 3);
@@ -1150,9 +1212,9 @@ __global__ __launch_bounds__(64, 2) void apply2_kernel(ApplyArgs a, int nwork) {
     const int c2 = __builtin_amdgcn_readfirstlane(it % a.g.n2);
     const int b = __builtin_amdgcn_readfirstlane(it / a.g.n2);
     if (t1 >= a.fa && t1 < a.fb)
-        apply2_body<WS, NCOMP, TRANS, true>(a, pass, t1, c2, b);
+        apply2_body<WS, NCOMP, TRANS, true, SUMS>(a, pass, t1, c2, b);
     else
-        apply2_body<WS, NCOMP, TRANS, false>(a, pass, t1, c2, b);
+        apply2_body<WS, NCOMP, TRANS, false, SUMS>(a, pass, t1, c2, b);
 }
 
 // Interior tile columns [fa, fb): every lane row 2p or more inside dim 1.
@@ -1225,6 +1287,24 @@ hipError_t dispatch_ws(const ApplyArgs &a, int64_t nb, hipStream_t s) {
 
 template <int WS>
 hipError_t launch_colsum_t(const Geom &g, int64_t nb, const float *nz, float *out, hipStream_t s) {
+    if (g.nsp == 2) {
+        using S = A2<WS, 1, true>;
+        ApplyArgs a{};
+        a.g = g;
+        a.C = 1;
+        a.nz = nz;
+        a.y = out;
+        a.tiles1 = (g.n1 + 63) / 64;
+        a.fa = (S::EDGE + 63) / 64;
+        a.fb = g.n1 - 64 - S::EDGE >= 0 ? (g.n1 - 64 - S::EDGE) / 64 + 1 : 0;
+        if (a.fb > a.tiles1) a.fb = a.tiles1;
+        if (a.fb < a.fa) a.fb = a.fa;
+        a.gchunk = 1;
+        const int64_t nwork = (int64_t)a.tiles1 * g.n2 * nb;
+        hipLaunchKernelGGL((apply2_kernel<WS, 1, true, true>), dim3((unsigned)(8 * ((nwork + 7) / 8))),
+                           dim3(64), (size_t)S::LDS_SUMS * sizeof(float), s, a, (int)nwork);
+        return hipGetLastError();
+    }
     const int tiles1 = (g.n1 + tile_w(g.nsp) - 1) / tile_w(g.nsp);
     const int tiles2 = (g.n2 + tile_h(g.nsp) - 1) / tile_h(g.nsp);
     int fa, fb;
