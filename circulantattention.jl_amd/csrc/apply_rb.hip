@@ -1152,6 +1152,12 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
                         acc[i][NCOMP * cl + e] = __builtin_fmaf(
                             av[i][j], xw[AL + NCOMP * (TRANS ? i - j + 2 * P : i + j) + e],
                             acc[i][NCOMP * cl + e]);
+            // the step's products complete here, before the next step's loads
+            // and reads (otherwise every step's run is read up front and held)
+#pragma unroll
+            for (int i = 0; i < kR; ++i)
+#pragma unroll
+                for (int e = 0; e < NCOMP; ++e) asm volatile("" : "+v"(acc[i][NCOMP * cl + e]));
             xb = xb == S::NXB - 1 ? 0 : xb + 1;
         }
     }
