@@ -9,26 +9,28 @@
 //   sim    nzVal = scale * similarity(x, y) (src/similarity.jl:31-103).
 //
 // nzVal (K floats per pixel) dominates the bytes, so it is read or written
-// in contiguous runs and everything else is arranged around that.  Every
-// lane owns 4 consecutive pixels along dim 1, so one run of 4 + 2p values
-// of x per component serves 4 x ws products.
-//   * 2D apply (apply_rows_kernel): a wavefront owns 64 pixels of one image
-//     row; their 64 K contiguous nzVal floats are loaded into LDS once by
-//     LDS-DMA buffer loads and serve every component chunk; the four lane
-//     groups split the window rows and add their partial sums at the end.
-//   * transposed apply, column sum, 1D apply (apply_rb_kernel,
-//     colsum_rb_kernel): a wavefront owns 4 lane rows of 64 pixels (a 64 x 4
-//     tile in 2D, 256 pixels of the line in 1D); per iteration the slot
-//     chunks it needs (64 + 2p source pixels for the transposed product) are
-//     DMA-loaded, 16 lanes per chunk, into a wave-private LDS buffer and read
-//     back by the owning lanes.  In 2D the transposed product walks source
-//     image rows, whose 4 chunks for the 4 lane rows are adjacent.
-//   * similarity (sim_rows_kernel): row ownership as in the 2D apply; each
-//     pixel's chunk of ws slots is accumulated over the channels in registers
-//     and stored as one run.
-// Read offsets carry the reference's circular shift of the slot order near
-// borders (src/circulant.jl:6-44); wavefronts within 2p of a border of dim 1
-// run a border body that steps wrapped columns, the others use immediates.
+// with wide, coalesced accesses and everything else is arranged around that.
+// Every lane owns 4 consecutive pixels along dim 1, so one run of 4 + 2p
+// values of x per component serves 4 x ws products.
+//   * 2D apply, both directions, and 2D column sums (apply2_kernel): a
+//     wavefront owns 64 output pixels of one image row; its four lane groups
+//     split the components.  Per window row the slot chunk that row needs of
+//     every pixel involved is staged into LDS by 16-byte LDS-DMA pieces, and
+//     x one channel per group and step; both are staged by rings of LDS
+//     buffers two steps ahead.
+//   * similarity (sim_rows_kernel): the same row ownership, lane groups
+//     split the window rows; per channel the key rows and queries are staged
+//     into LDS with 16-byte loads, and results leave through LDS as runs of
+//     each pixel's row.
+//   * 1D apply and column sums (apply_rb_kernel, colsum_rb_kernel): a
+//     wavefront owns 256 pixels of the line in 4 lane rows; per iteration the
+//     slot chunks it needs are DMA-loaded, 16 lanes per chunk, into a
+//     wave-private LDS buffer and read back by the owning lanes.
+// Wavefronts are dealt to XCDs in bands of consecutive image rows, so that
+// rows shared by neighbouring wavefronts stay in one L2.  Near the borders
+// of dim 1 the reference's circular shift of the slot order
+// (src/circulant.jl:6-44) is applied by border bodies with wrapped columns;
+// interior wavefronts use immediate offsets.
 #include <algorithm>
 
 #include "circatt_common.h"
@@ -43,7 +45,6 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));  // 4-byte aligned
 
 constexpr int kR = 4;     // pixels per lane along dim 1
-constexpr int kCC = 8;    // real components per chunk of the whole-row kernel
 constexpr int kCP = 8;    // real components per staging pass of the chunked kernel
 constexpr unsigned kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data
 
@@ -427,192 +428,6 @@ __global__ __launch_bounds__(64, 2) void colsum_rb_kernel(Geom g, int tiles1, in
         colsum_body<WS, true>(g, t1, t2, b, nz, out);
     else
         colsum_body<WS, false>(g, t1, t2, b, nz, out);
-}
-
-// ---------------------------------------------------------------------------
-// A ⊗ x in 2D with whole rows of nzVal: a wavefront owns 64 consecutive pixels
-// of one image row, whose nzVal rows are 64 K contiguous floats; they are
-// staged into LDS once (LDS-DMA, fully coalesced) and serve every component
-// chunk.  The four lane groups take every fourth window row (lane 16 r + l
-// owns pixels 4 l .. 4 l + 3 for window rows r, r + 4, ...) and their partial
-// sums are added across the groups at the end of a chunk.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ float group4_sum(float v) {
-    unsigned u = __float_as_uint(v);
-    auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
-    u = __float_as_uint(v);
-    auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
-}
-
-template <int WS>
-__host__ __device__ constexpr int rows_lds_floats() { return 64 * WS * WS; }
-
-template <int WS, int NCOMP, bool FAST>
-__device__ __forceinline__ void rows_body(const ApplyArgs &a, int gc, int t1, int c2, int b) {
-    constexpr int P = (WS - 1) / 2;
-    constexpr int K = WS * WS;
-    constexpr int XW = kR + 2 * P;
-    constexpr int XN = NCOMP * XW;
-    constexpr int XN4 = (XN + 3) / 4;
-    constexpr int CCH = kCC / NCOMP;
-    constexpr int NIT = (WS + 3) / 4;  // window rows per lane group
-    typedef __attribute__((address_space(3))) void *lptr;
-    const Geom &g = a.g;
-    const int n1 = g.n1, n2 = g.n2;
-    const int64_t Pp = g.P;
-    const int lane = threadIdx.x & 63;
-    const int l16 = lane & 15, rho = lane >> 4;
-    const int f1 = t1 * 64;
-    float *lw = circatt_lds_apply;
-    const auto rs = rsrc(a.nz + (int64_t)b * Pp * K, Pp * K * 4);
-    const auto rx = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, Pp * NCOMP * a.C * 4);
-
-    // stage the 64 rows (pixels f1 .. f1 + 63 of image row c2; rows past the
-    // image row or the unit are never stored, the buffer bound zeroes reads
-    // past the unit)
-    {
-        const int vo = (int)((f1 + (int64_t)n1 * c2) * K * 4) + lane * 4;
-        int so = 0;
-#pragma unroll
-        for (int q = 0; q < K; ++q) {
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(lw + 64 * q), 4, vo,
-                                                    __builtin_amdgcn_readfirstlane(so), 0, 0);
-            so += 256;
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    // slot shift of the lane's pixels (border body)
-    int s1[kR];
-#pragma unroll
-    for (int i = 0; i < kR; ++i) s1[i] = FAST ? 0 : shift0(pmod(f1 + 4 * l16 + i, n1), n1, P);
-    const int s2 = slot_shift(c2 + 1, n2, P);
-    __builtin_amdgcn_s_waitcnt(kWaitAll);
-
-    auto load_x = [&](float (&xw)[4 * XN4], int c, int xr2) {
-        const int cw = c < a.C ? c : a.C - 1;
-        const int rowoff = (int)(NCOMP * ((int64_t)n1 * xr2 + Pp * cw)) * 4;
-        if (FAST) {
-            const int vo = rowoff + NCOMP * (f1 + 4 * l16 - P) * 4;
-#pragma unroll
-            for (int q = 0; q < XN4; ++q) {
-                const f4 v = bload4(rx, vo, 16 * q);
-                xw[4 * q] = v[0];
-                xw[4 * q + 1] = v[1];
-                xw[4 * q + 2] = v[2];
-                xw[4 * q + 3] = v[3];
-            }
-        } else {
-            int xc = pmod(f1 + 4 * l16 - P, n1);
-#pragma unroll
-            for (int w = 0; w < XW; ++w) {
-#pragma unroll
-                for (int e = 0; e < NCOMP; ++e)
-                    xw[NCOMP * w + e] = bload(rx, rowoff + (NCOMP * xc + e) * 4, 0);
-                xc = xc + 1 == n1 ? 0 : xc + 1;
-            }
-        }
-    };
-
-    const int nchunk = (NCOMP * a.C + kCC - 1) / kCC;
-    float *yb = a.y + (int64_t)b * Pp * NCOMP * a.C;
-    const float *zb = a.z ? a.z + (int64_t)b * Pp * NCOMP * a.C : nullptr;
-    const int ch1 = min(nchunk, (gc + 1) * a.ichunk);
-    for (int ch = gc * a.ichunk; ch < ch1; ++ch) {
-        const int k0 = ch * kCC;
-        float acc[kR][kCC];
-        float asum[kR];
-#pragma unroll
-        for (int i = 0; i < kR; ++i) {
-            asum[i] = 0.f;
-#pragma unroll
-            for (int kk = 0; kk < kCC; ++kk) acc[i][kk] = 0.f;
-        }
-        for (int itr = 0; itr < NIT; ++itr) {
-            const int dd = 4 * itr + rho;
-            const bool live = dd < WS;
-            const int ddc = live ? dd : WS - 1;
-            const int xr2 = pmod(c2 + ddc - P, n2);
-            const int mm = pmod(ddc + s2, WS);
-            float av[kR][WS];
-#pragma unroll
-            for (int i = 0; i < kR; ++i)
-#pragma unroll
-                for (int j = 0; j < WS; ++j) {
-                    const int pos = FAST ? j : fold(j + s1[i], WS);
-                    const float v = lw[(4 * l16 + i) * K + mm * WS + pos];
-                    av[i][j] = live ? v : 0.f;
-                }
-            if (a.corr) {
-#pragma unroll
-                for (int i = 0; i < kR; ++i)
-#pragma unroll
-                    for (int j = 0; j < WS; ++j) asum[i] += av[i][j];
-            }
-            float xa[4 * XN4], xb[4 * XN4];
-            load_x(xa, k0 / NCOMP, xr2);
-#pragma unroll
-            for (int cl = 0; cl < CCH; ++cl) {
-                float(&xc)[4 * XN4] = (cl & 1) ? xb : xa;
-                float(&xn)[4 * XN4] = (cl & 1) ? xa : xb;
-                __builtin_amdgcn_sched_barrier(0);
-                if (cl + 1 < CCH) load_x(xn, k0 / NCOMP + cl + 1, xr2);
-#pragma unroll
-                for (int i = 0; i < kR; ++i)
-#pragma unroll
-                    for (int j = 0; j < WS; ++j)
-#pragma unroll
-                        for (int e = 0; e < NCOMP; ++e)
-                            acc[i][NCOMP * cl + e] = __builtin_fmaf(
-                                av[i][j], xc[NCOMP * (i + j) + e], acc[i][NCOMP * cl + e]);
-            }
-        }
-        // add the four lane groups' window rows; group r stores components
-        // 2 r, 2 r + 1 of the chunk
-#pragma unroll
-        for (int i = 0; i < kR; ++i) {
-            if (a.corr) asum[i] = group4_sum(asum[i]);
-#pragma unroll
-            for (int kk = 0; kk < kCC; ++kk) acc[i][kk] = group4_sum(acc[i][kk]);
-        }
-#pragma unroll
-        for (int i = 0; i < kR; ++i) {
-            const int col = f1 + 4 * l16 + i;
-            if (col >= n1) continue;
-            const int64_t pix = col + (int64_t)n1 * c2;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int kk = 2 * rho + h;
-                const int k = k0 + kk;
-                if (k >= NCOMP * a.C) break;
-                const int c = k / NCOMP, e = k - c * NCOMP;
-                const int64_t idx = NCOMP * (pix + Pp * c) + e;
-                float v = acc[i][0];
-#pragma unroll
-                for (int q = 1; q < kCC; ++q) v = kk == q ? acc[i][q] : v;
-                if (a.corr) v -= asum[i] * zb[idx];
-                yb[idx] = v * a.scale;
-            }
-        }
-    }
-}
-
-// One wavefront per (64 pixels of an image row, unit).
-template <int WS, int NCOMP>
-__global__ __launch_bounds__(64, 2) void apply_rows_kernel(ApplyArgs a) {
-    int it = blockIdx.x;
-    const int gc = __builtin_amdgcn_readfirstlane(it % a.gchunk);
-    it /= a.gchunk;
-    const int t1 = __builtin_amdgcn_readfirstlane(it % a.tiles1);
-    it /= a.tiles1;
-    const int c2 = __builtin_amdgcn_readfirstlane(it % a.g.n2);
-    const int b = __builtin_amdgcn_readfirstlane(it / a.g.n2);
-    if (t1 >= a.fa && t1 < a.fb)
-        rows_body<WS, NCOMP, true>(a, gc, t1, c2, b);
-    else
-        rows_body<WS, NCOMP, false>(a, gc, t1, c2, b);
 }
 
 // ---------------------------------------------------------------------------
@@ -1250,25 +1065,6 @@ hipError_t launch_rb(ApplyArgs a, int64_t nb, hipStream_t s) {
                            (size_t)S::LDS * sizeof(float), s, a, (int)nwork);
         return hipGetLastError();
     }
-    if (!TRANS && a.g.nsp == 2) {
-        // whole-row kernel: interior when no x wrap and no slot shift
-        const int tiles1 = (a.g.n1 + 63) / 64;
-        a.tiles1 = tiles1;
-        a.fa = (a.g.p + 63) / 64;
-        a.fb = a.g.n1 - 64 - a.g.p >= 0 ? (a.g.n1 - 64 - a.g.p) / 64 + 1 : 0;
-        if (a.fb > tiles1) a.fb = tiles1;
-        if (a.fb < a.fa) a.fb = a.fa;
-        // component chunks of a row segment in one wavefront (its nzVal rows
-        // staged once) unless that leaves the GPU underfilled
-        const int nchunk = (NCOMP * a.C + kCC - 1) / kCC;
-        const int64_t waves = (int64_t)tiles1 * a.g.n2 * nb;
-        a.ichunk = waves >= 2048 ? nchunk : std::max(1, (int)((int64_t)nchunk * waves / 2048));
-        a.gchunk = (nchunk + a.ichunk - 1) / a.ichunk;
-        const int64_t grid = waves * a.gchunk;
-        hipLaunchKernelGGL((apply_rows_kernel<WS, NCOMP>), dim3((unsigned)grid), dim3(64),
-                           (size_t)rows_lds_floats<WS>() * sizeof(float), s, a);
-        return hipGetLastError();
-    }
     const size_t lds = (size_t)lds_floats(WS, TRANS) * sizeof(float);
     interior_cols(a.g, a.fa, a.fb);
     const int64_t grid = (int64_t)a.gchunk * a.tiles1 * a.tiles2 * nb;
@@ -1397,8 +1193,9 @@ bool apply_rb_supported(const Geom &g, int C, int ncomp, int64_t nb) {
     if (g.ws < 3 || g.ws > 15 || (g.ws & 1) == 0) return false;
     // 32-bit byte offsets into one unit's nzVal and x, grid in one dimension
     if (g.P * g.K * 4 >= (int64_t)1 << 31) return false;
-    if (g.P * ncomp * C * 4 >= (int64_t)1 << 31) return false;
-    const int64_t grid = tiles_of(g) * ((ncomp * C + kCC - 1) / kCC) * nb;  // upper bound
+    // (the 2D kernel forms offsets of up to kCPass channels past C)
+    if (g.P * ncomp * ((int64_t)C + kCPass) * 4 >= (int64_t)1 << 31) return false;
+    const int64_t grid = tiles_of(g) * ((ncomp * C + kCP - 1) / kCP) * nb;  // upper bound
     return grid > 0 && grid < ((int64_t)1 << 31);
 }
 
