@@ -704,8 +704,14 @@ struct A2 {
     static constexpr int NSRC = TRANS ? 64 + 2 * P : 64;  // staged chunks per row
     static constexpr int WSP = (WS + 3) & ~3;             // LDS floats per chunk
     static constexpr int Q = WSP / 4;                     // 16-byte pieces per chunk
-    static constexpr int NZ4 = (NSRC * Q + 63) / 64;      // interior: 16-byte DMA loads per lane
-    static constexpr int NZ1 = (NSRC * WSP + 63) / 64;    // border: 4-byte DMA loads per lane
+    // chunks in blocks of 4, each block followed by one free 16-byte slot:
+    // piece q of chunk w is slot w Q + q + w / 4, so chunks 4 apart (the
+    // lanes of one read) lie an odd number 4 Q + 1 of slots apart and their
+    // reads fall in different banks
+    static constexpr int BLK = 4 * Q + 1;                 // slots per block
+    static constexpr int NSLOT = (NSRC + 3) / 4 * BLK;
+    static constexpr int NZ4 = (NSLOT + 63) / 64;         // interior: 16-byte DMA loads per lane
+    static constexpr int NZ1 = (4 * NSLOT + 63) / 64;     // border: 4-byte DMA loads per lane
     static constexpr int NZB = NZ4 * 256 > NZ1 * 64 ? NZ4 * 256 : NZ1 * 64;  // chunk buffer floats
     static constexpr int RF = NCOMP * (64 + 2 * kHalo);   // x floats per group
     static constexpr int XF = 4 * RF;
@@ -733,9 +739,11 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
     constexpr int KW4 = (NCOMP * XW + AL + 3) / 4;
     constexpr int ZI = FAST ? S::NZ4 : S::NZ1;      // chunk loads per lane and row
     constexpr int XI = FAST ? S::XL : 4 * S::XL;    // x loads per lane and step
-    constexpr int NZR = SUMS ? S::NZR_SUMS : S::NZR;
+    // (column sums: one row fewer ahead where three rows of loads would
+    // exceed the vmcnt field)
+    constexpr int NZR = !SUMS ? S::NZR : ((S::NZR_SUMS - 1) * ZI < 64 ? S::NZR_SUMS : 3);
     constexpr int T = WS * S::CHS;                  // steps
-    static_assert(ZI + XI < 64 && 3 * ZI < 64, "waits exceed vmcnt");
+    static_assert(ZI + XI < 64 && (NZR - 1) * ZI < 64, "waits exceed vmcnt");
     typedef __attribute__((address_space(3))) void *lptr;
     const Geom &g = a.g;
     const int n1 = g.n1, n2 = g.n2;
@@ -751,8 +759,8 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
     const int plane = (int)(NCOMP * Pp * 4);  // bytes per channel
     const int s2own = slot_shift(c2 + 1, n2, P);
 
-    // Chunk DMA into lz[w * WSP + j] = slot j of chunk w (source column
-    // f1 - off + w, wrapped), in the order of window offsets: near the border
+    // Chunk DMA into lz[w * WSP + 4 (w / 4) + j] = slot j of chunk w (source
+    // column f1 - off + w, wrapped), in the order of window offsets: near the border
     // of dim 1 the reference's circular shift of the slot order is undone
     // here, by the element each lane loads, so the reads below use constant
     // offsets in both bodies.  The interior body loads 16-byte pieces (the
@@ -764,13 +772,16 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
 #pragma unroll
     for (int m = 0; m < ZI; ++m) {
         const int off = TRANS ? P : 0;
+        // LDS slot of this lane's piece -> (chunk w, piece q); free slots and
+        // pieces past the last chunk load chunk 0 / the last chunk (unused)
+        const int f = FAST ? lane + 64 * m : (lane + 64 * m) >> 2;
+        const int kb = f / S::BLK, r = f - kb * S::BLK;
+        const int rq = r < 4 * S::Q ? r : 0;
+        const int w = min(4 * kb + rq / S::Q, S::NSRC - 1), q = rq - (rq / S::Q) * S::Q;
         if (FAST) {
-            const int s = min(lane + 64 * m, S::NSRC * S::Q - 1);
-            const int w = s / S::Q, q = s - w * S::Q;
             zo[m] = ((f1 - off + w) * K + 4 * q) * 4;
         } else {
-            const int f = min(lane + 64 * m, S::NSRC * S::WSP - 1);
-            const int w = f / S::WSP, j = f - w * S::WSP;
+            const int j = 4 * q + ((lane + 64 * m) & 3);
             const int col = pmod(f1 - off + w, n1);
             const int e = fold((j < WS ? j : 0) + shift0(col, n1, P), WS);
             zo[m] = (col * K + e) * 4;
@@ -862,8 +873,9 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
         for (int i = 0; i < kR; ++i)
 #pragma unroll
             for (int j = 0; j < WS; ++j) {
-                const int u = TRANS ? 4 * l16 + i - j + 2 * P : 4 * l16 + i;
-                av[i][j] = src[u * S::WSP + j];
+                // chunk u = 4 l16 + c (c >= 0): block l16 + c / 4
+                const int c = TRANS ? i - j + 2 * P : i;
+                av[i][j] = src[(4 * l16 + c) * S::WSP + 4 * (l16 + c / 4) + j];
             }
     };
 
@@ -879,7 +891,7 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
             if (dd + NZR - 1 < WS) stage_z(dd + NZR - 1, (dd + NZR - 1) % NZR);
             const int younger = min(NZR - 1, WS - 1 - dd);
             if (younger >= 3)
-                wait_vm<3 * ZI>();
+                wait_vm<(NZR > 3 ? 3 : 2) * ZI>();  // only reached when NZR > 3
             else if (younger == 2)
                 wait_vm<2 * ZI>();
             else if (younger == 1)
