@@ -728,8 +728,11 @@ struct A2 {
 };
 
 // SUMS: column sums only (x = 1, no products): out[o] = sum of the staged
-// coefficients, written to a.y (one float per pixel).
-template <int WS, int NCOMP, bool TRANS, bool FAST, bool SUMS = false>
+// coefficients, written to a.y (one float per pixel).  XV: x is staged in
+// 16-byte pieces (interior tiles, and border tiles when n1 is a multiple of
+// the 4 / NCOMP pixels of a piece, so that no piece straddles the wrap);
+// otherwise float by float.
+template <int WS, int NCOMP, bool TRANS, bool FAST, bool SUMS = false, bool XV = FAST>
 __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1, int c2, int b) {
     using S = A2<WS, NCOMP, TRANS>;
     constexpr int P = S::P;
@@ -738,7 +741,7 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
     constexpr int AL = (NCOMP * (kHalo - P)) % 4;
     constexpr int KW4 = (NCOMP * XW + AL + 3) / 4;
     constexpr int ZI = FAST ? S::NZ4 : S::NZ1;      // chunk loads per lane and row
-    constexpr int XI = FAST ? S::XL : 4 * S::XL;    // x loads per lane and step
+    constexpr int XI = XV ? S::XL : 4 * S::XL;      // x loads per lane and step
     // (column sums: one row fewer ahead where three rows of loads would
     // exceed the vmcnt field)
     constexpr int NZR = !SUMS ? S::NZR : ((S::NZR_SUMS - 1) * ZI < 64 ? S::NZR_SUMS : 3);
@@ -825,13 +828,15 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
     int xo[XI];
 #pragma unroll
     for (int m = 0; m < XI; ++m) {
-        const int f = FAST ? 4 * (lane + 64 * m) : lane + 64 * m;
+        const int f = XV ? 4 * (lane + 64 * m) : lane + 64 * m;
         const int fr = f < S::XF ? f : 0;
         const int gs = fr / S::RF, w = fr - gs * S::RF;
         const int chan = (ch0 + gs * S::CHS) * plane;
         if (FAST) {
             xo[m] = chan + (NCOMP * (f1 - kHalo) + w) * 4;
         } else {
+            // (with XV, w is the first float of a piece: e = 0 and the piece's
+            // pixels are consecutive columns)
             const int u = w / NCOMP, e = w - u * NCOMP;
             xo[m] = chan + (NCOMP * pmod(f1 - kHalo + u, n1) + e) * 4;
         }
@@ -848,7 +853,7 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
 #pragma unroll
         for (int m = 0; m < XI; ++m) {
             __builtin_amdgcn_sched_barrier(0);
-            if (FAST)
+            if (XV)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lptr)(dst + 256 * m), 16, xo[m] + so,
                                                         0, 0, 0);
             else
@@ -1046,8 +1051,10 @@ __global__ __launch_bounds__(64, 2) void apply2_kernel(ApplyArgs a, int nwork) {
     const int b = __builtin_amdgcn_readfirstlane(it / a.g.n2);
     if (t1 >= a.fa && t1 < a.fb)
         apply2_body<WS, NCOMP, TRANS, true, SUMS>(a, pass, t1, c2, b);
+    else if (!SUMS && a.g.n1 % (4 / NCOMP) == 0)
+        apply2_body<WS, NCOMP, TRANS, false, SUMS, true>(a, pass, t1, c2, b);
     else
-        apply2_body<WS, NCOMP, TRANS, false, SUMS>(a, pass, t1, c2, b);
+        apply2_body<WS, NCOMP, TRANS, false, SUMS, false>(a, pass, t1, c2, b);
 }
 
 // Interior tile columns [fa, fb): every lane row 2p or more inside dim 1.

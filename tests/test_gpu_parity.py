@@ -105,15 +105,17 @@ def test_similarity(ca, cuda, dims, ws, C, cplx, kind):
     assert rel_err(host(S.nzval).reshape(B, -1), ref) < TOL_FWD
 
 
+@pytest.mark.parametrize("dims", [(96, 256), (200, 96)])
 @pytest.mark.parametrize("ws", [7, 11])
 @pytest.mark.parametrize("cplx", [False, True])
 @pytest.mark.parametrize("kind", [0, 1])
-def test_similarity_many_rows(ca, cuda, ws, cplx, kind):
-    """Grids of 2048 or more 64-pixel row segments take the row-blocked
-    similarity kernel (smaller grids take the matrix-core kernel): 96 x 256,
-    4 units, against the oracle; 96 is not a multiple of 64, so partial
-    segments and both border paths run."""
-    dims, C, B = (96, 256), 6, 4
+def test_similarity_many_rows(ca, cuda, dims, ws, cplx, kind):
+    """Grids of 1024 or more 64-pixel row segments take the row-blocked
+    similarity kernel (smaller grids take the matrix-core kernel), 4 units,
+    against the oracle.  Neither width is a multiple of 64, so partial
+    segments and the border body run; rows of 200 pixels also have interior
+    segments."""
+    C, B = 6, 4
     x = seeded(13, shape_of(dims, C, B), cplx)
     y = seeded(14, shape_of(dims, C, B), cplx)
     simfun = ca.DotSimilarity() if kind == 0 else ca.DistanceSimilarity()
@@ -137,7 +139,10 @@ def test_softmax_and_pullback(ca, cuda, K, rows):
 
 
 APPLY_CASES = [((8,), 5, 4), ((8, 8), 5, 4), ((12, 10), 3, 8), ((4, 4), 5, 3), ((2,), 5, 2),
-               ((33, 17), 11, 16)]
+               ((33, 17), 11, 16),
+               # 2D rows with interior 64-pixel segments (and a partial last one);
+               # 203 is odd, so its border segments stage x float by float
+               ((200, 12), 11, 16), ((256, 6), 15, 8), ((203, 5), 7, 4)]
 
 
 @pytest.mark.parametrize("dims,ws,C", APPLY_CASES)
