@@ -430,6 +430,13 @@ __global__ __launch_bounds__(64, 2) void colsum_rb_kernel(Geom g, int tiles1, in
         colsum_body<WS, false>(g, t1, t2, b, nz, out);
 }
 
+// s_waitcnt vmcnt(N) (gfx9 encoding, expcnt and lgkmcnt at their maximum)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt has 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // ---------------------------------------------------------------------------
 // nzVal = scale * similarity(x, y) in 2D (src/similarity.jl:31-103): a
 // wavefront owns 64 consecutive pixels of one image row; lane group r takes
@@ -438,11 +445,12 @@ __global__ __launch_bounds__(64, 2) void colsum_rb_kernel(Geom g, int tiles1, in
 // does), then stores each pixel's chunk of ws slots (contiguous in the row,
 // rotated near borders).
 //
-// Per channel the wavefront stages, with 16-byte loads, the 4 key rows'
-// columns f1 - kHalo .. f1 + 63 + kHalo and its 64 query pixels into LDS
-// (3 load instructions for complex data instead of one overlapping run of
-// 4 + 2p pixels per lane); the lanes read their runs back from LDS.  The
-// loads of channel c + 1 are in flight while channel c is multiplied.
+// Per channel the 4 key rows' columns f1 - kHalo .. f1 + 63 + kHalo and the
+// 64 query pixels are staged into LDS by LDS-DMA, in 16-byte pieces (3 + 1
+// loads for complex data instead of one overlapping run of 4 + 2p pixels per
+// lane), into a ring of 3 buffers two channels ahead; the lanes read their
+// runs back from LDS.  Loads return in issue order, and each channel waits
+// with a vmcnt that counts the loads of the next channel.
 // ---------------------------------------------------------------------------
 constexpr int kHalo = 8;  // staged key columns beyond each side (>= p)
 template <int NCOMP>
@@ -450,12 +458,19 @@ struct SimStage {
     static constexpr int RW = 64 + 2 * kHalo;  // staged key columns per row
     static constexpr int RF = NCOMP * RW;      // floats per key row
     static constexpr int KF = 4 * RF;          // key floats
-    static constexpr int SF = KF + NCOMP * 64; // floats per channel
-    static constexpr int SF4 = SF / 4;
-    static constexpr int NLD = (SF4 + 63) / 64;  // 16-byte loads per lane
+    static constexpr int KS = KF / 4;          // key pieces
+    static constexpr int KL = (KS + 63) / 64;  // 16-byte key loads per lane
+    static constexpr int QF = NCOMP * 64;      // query floats
+    static constexpr int QS = QF / 4;          // query pieces (<= 64)
+    static constexpr int QOFF = KL * 256;      // query area (floats)
+    static constexpr int SB = QOFF + 256;      // floats per ring buffer
+    static constexpr int KL1 = KF / 64, QL1 = QF / 64;  // 4-byte loads (border)
+    static constexpr int NR = 3;               // ring buffers
 };
 
-template <int WS, int NCOMP, bool DIST, bool FAST>
+// XV: pieces of 16 bytes (interior segments, and border segments when n1 is
+// a multiple of the 4 / NCOMP pixels of a piece); otherwise float by float.
+template <int WS, int NCOMP, bool DIST, bool FAST, bool XV = FAST>
 __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int c2, int b) {
     using S = SimStage<NCOMP>;
     constexpr int P = (WS - 1) / 2;
@@ -466,8 +481,12 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
     // from the 16-byte boundary AL floats before
     constexpr int AL = (NCOMP * (kHalo - P)) % 4;
     constexpr int KW4 = (NCOMP * XW + AL + 3) / 4;
-    constexpr int NB = FAST ? S::NLD : 4 * S::NLD;  // loads per lane per channel
+    constexpr int NK = XV ? S::KL : S::KL1;  // key loads per lane and channel
+    constexpr int NQ = XV ? 1 : S::QL1;      // query loads
+    constexpr int NI = NK + NQ;
     static_assert(P <= kHalo, "window wider than the staged halo");
+    static_assert(NI < 64, "vmcnt");
+    typedef __attribute__((address_space(3))) void *lptr;
     const Geom &g = a.g;
     const int n1 = g.n1, n2 = g.n2;
     const int64_t Pp = g.P;
@@ -484,6 +503,18 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
     for (int i = 0; i < kR; ++i) s1[i] = FAST ? 0 : shift0(pmod(f1 + 4 * l16 + i, n1), n1, P);
     const int s2 = slot_shift(c2 + 1, n2, P);
     const int plane = (int)(NCOMP * Pp * 4);  // bytes per channel
+    // query offsets (the lane's piece, or float, of the 64 query pixels)
+    int qo[NQ];
+#pragma unroll
+    for (int m = 0; m < NQ; ++m) {
+        if (XV) {
+            const int u = 4 * min(lane, S::QS - 1) / NCOMP;
+            qo[m] = NCOMP * (n1 * c2 + (FAST ? f1 + u : pmod(f1 + u, n1))) * 4;
+        } else {
+            const int f = lane + 64 * m, u = f / NCOMP, e = f - u * NCOMP;
+            qo[m] = (NCOMP * (n1 * c2 + pmod(f1 + u, n1)) + e) * 4;
+        }
+    }
 
     // window-row iterations [gc * ichunk, ...) of this wavefront
     const int it1 = min(NIT, (gc + 1) * a.ichunk);
@@ -491,67 +522,48 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
         const int dd = 4 * itr + rho;
         const bool live = dd < WS;
         const int mm = pmod(min(dd, WS - 1) + s2, WS);
-        // byte offsets (within a channel) of this lane's staged values; a
-        // value of the staging area is a key (f < KF) or a query
-        int off[NB];
+        // key offsets of this iteration: the lane's piece (or float) of key
+        // row rr = window row 4 itr + rr (clamped)
+        int ko[NK];
 #pragma unroll
-        for (int m = 0; m < NB; ++m) {
-            const int f = FAST ? 4 * (lane + 64 * m) : lane + 64 * m;  // first float
-            const int fr = f < S::SF ? f : 0;
-            if (fr < S::KF) {
-                const int rr = fr / S::RF, w = fr - rr * S::RF;
-                const int kr2 = pmod(c2 + min(4 * itr + rr, WS - 1) - P, n2);
-                if (FAST) {
-                    off[m] = (NCOMP * (n1 * kr2 + f1 - kHalo) + w) * 4;
-                } else {
-                    const int u = w / NCOMP, e = w - u * NCOMP;
-                    off[m] = (NCOMP * (n1 * kr2 + pmod(f1 - kHalo + u, n1)) + e) * 4;
-                }
-            } else {
-                const int w = fr - S::KF;
-                if (FAST) {
-                    off[m] = (NCOMP * (n1 * c2 + f1) + w) * 4;
-                } else {
-                    const int u = w / NCOMP, e = w - u * NCOMP;
-                    off[m] = (NCOMP * (n1 * c2 + pmod(f1 + u, n1)) + e) * 4;
-                }
-            }
+        for (int m = 0; m < NK; ++m) {
+            const int f = XV ? 4 * min(lane + 64 * m, S::KS - 1) : lane + 64 * m;
+            const int rr = f / S::RF, w = f - rr * S::RF;
+            const int kr2 = pmod(c2 + min(4 * itr + rr, WS - 1) - P, n2);
+            const int u = w / NCOMP, e = w - u * NCOMP;  // (e = 0 for a piece)
+            const int col = FAST ? f1 - kHalo + u : pmod(f1 - kHalo + u, n1);
+            ko[m] = (NCOMP * (n1 * kr2 + col) + e) * 4;
         }
-        // staged values of one channel, in registers
-        auto load_stage = [&](float (&st)[4 * S::NLD], int c) {
+        auto stage = [&](int c, int buf) {
             const int cb = __builtin_amdgcn_readfirstlane(c * plane);
+            float *dst = lw + buf * S::SB;
 #pragma unroll
-            for (int m = 0; m < NB; ++m) {
-                const int s = FAST ? lane + 64 * m : (lane + 64 * m) / 4;
-                // the first key / query boundary and the end are multiples of 16
-                // values, so a 16-byte slot is all key or all query
-                const int f0 = FAST ? 4 * s : lane + 64 * m;
-                if (f0 >= S::SF) continue;
-                if (FAST) {
-                    const f4 v = f0 < S::KF ? bload4(rk, off[m], cb) : bload4(rq, off[m], cb);
-                    st[4 * m] = v[0];
-                    st[4 * m + 1] = v[1];
-                    st[4 * m + 2] = v[2];
-                    st[4 * m + 3] = v[3];
+            for (int m = 0; m < NK; ++m) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (XV) {
+                    // (lanes past the last piece load nothing; some lane of
+                    // every instruction is active, so each is issued)
+                    if (lane + 64 * m < S::KS)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lptr)(dst + 256 * m), 16,
+                                                                ko[m], cb, 0, 0);
                 } else {
-                    st[m] = f0 < S::KF ? bload(rk, off[m], cb) : bload(rq, off[m], cb);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lptr)(dst + 64 * m), 4, ko[m],
+                                                            cb, 0, 0);
                 }
             }
-        };
-        auto store_stage = [&](const float (&st)[4 * S::NLD]) {
-            if (FAST) {
 #pragma unroll
-                for (int m = 0; m < S::NLD; ++m) {
-                    const int s = lane + 64 * m;
-                    if (4 * s < S::SF) *(f4 *)(lw + 4 * s) = f4{st[4 * m], st[4 * m + 1], st[4 * m + 2], st[4 * m + 3]};
-                }
-            } else {
-#pragma unroll
-                for (int m = 0; m < NB; ++m) {
-                    const int f = lane + 64 * m;
-                    if (f < S::SF) lw[f] = st[m];
+            for (int m = 0; m < NQ; ++m) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (XV) {
+                    if (lane < S::QS)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lptr)(dst + S::QOFF), 16,
+                                                                qo[m], cb, 0, 0);
+                } else {
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lptr)(dst + S::QOFF + 64 * m), 4,
+                                                            qo[m], cb, 0, 0);
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
         };
 
         float acc[kR][WS];
@@ -559,24 +571,32 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
         for (int i = 0; i < kR; ++i)
 #pragma unroll
             for (int j = 0; j < WS; ++j) acc[i][j] = 0.f;
-        float st[4 * S::NLD];
-        load_stage(st, 0);
+        // the previous iteration's reads of the LDS area are complete
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+        stage(0, 0);
+        if (a.C > 1) stage(1, 1);
+        int cur = 0;
 #pragma unroll 1
         for (int c = 0; c < a.C; ++c) {
-            // the previous channel's LDS reads were consumed by its products,
-            // and LDS operations of a wavefront complete in order
-            store_stage(st);
-            if (c + 1 < a.C) load_stage(st, c + 1);
+            // loads issued after channel c's: channel c + 1's
+            if (c + 1 < a.C)
+                wait_vm<NI>();
+            else
+                wait_vm<0>();
+            // the buffer refilled here was read for channel c - 1
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+            if (c + 2 < a.C) stage(c + 2, cur == 0 ? 2 : cur - 1);
+            const float *sb = lw + cur * S::SB;
             float q[4 * NCOMP], kw[4 * KW4];
 #pragma unroll
             for (int h = 0; h < NCOMP; ++h) {
-                const f4 v = *(const f4 *)(lw + S::KF + NCOMP * 4 * l16 + 4 * h);
+                const f4 v = *(const f4 *)(sb + S::QOFF + NCOMP * 4 * l16 + 4 * h);
                 q[4 * h] = v[0];
                 q[4 * h + 1] = v[1];
                 q[4 * h + 2] = v[2];
                 q[4 * h + 3] = v[3];
             }
-            const float *kr = lw + rho * S::RF + NCOMP * (4 * l16 + kHalo - P) - AL;
+            const float *kr = sb + rho * S::RF + NCOMP * (4 * l16 + kHalo - P) - AL;
 #pragma unroll
             for (int h = 0; h < KW4; ++h) {
                 const f4 v = *(const f4 *)(kr + 4 * h);
@@ -599,9 +619,12 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
                             acc[i][j] = __builtin_fmaf(xv, yv, acc[i][j]);
                         }
                     }
+            cur = cur == S::NR - 1 ? 0 : cur + 1;
         }
-        // the slot shifts are redefined here, so that the store addresses
-        // are not computed before the channel loop and held through it
+        // (the ring area is rewritten below: its last reads are complete, as
+        // LDS operations of a wavefront complete in order, and no load is in
+        // flight.)  The slot shifts are redefined here, so that the store
+        // addresses are not computed before the channel loop and held
 #pragma unroll
         for (int i = 0; i < kR; ++i) asm volatile("" : "+v"(s1[i]));
         const float sc = DIST ? -0.5f * a.scale : a.scale;
@@ -610,23 +633,24 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
         const int nlive = min(4, WS - 4 * itr);
         const int mm0 = pmod(4 * itr + s2, WS);
         if (mm0 + nlive <= WS) {
-            // through LDS (the staging area is free: LDS operations complete
-            // in order), then 16 lanes per pixel store its run of nlive * ws
-            // floats with 16-byte stores, 4 pixels per instruction
+            // through LDS, then 16 lanes per pixel store its run of nlive * ws
+            // floats with 16-byte stores, 4 pixels per instruction.  Pixel px
+            // sits at px PS + 4 (px / 4): the writing lanes (pixels 4 apart)
+            // then fall in different banks
             constexpr int PS = 4 * WS;  // LDS floats per pixel
             if (live) {
 #pragma unroll
                 for (int i = 0; i < kR; ++i)
 #pragma unroll
                     for (int j = 0; j < WS; ++j)
-                        lw[(4 * l16 + i) * PS + rho * WS + (FAST ? j : fold(j + s1[i], WS))] =
-                            acc[i][j] * sc;
+                        lw[(4 * l16 + i) * PS + 4 * l16 + rho * WS +
+                           (FAST ? j : fold(j + s1[i], WS))] = acc[i][j] * sc;
             }
             const int run = nlive * WS, tq = lane & 15, g4 = lane >> 4;
 #pragma unroll 4
             for (int m = 0; m < 16; ++m) {
                 const int px = 4 * m + g4, col = f1 + px;
-                const f4 v = *(const f4 *)(lw + px * PS + 4 * tq);
+                const f4 v = *(const f4 *)(lw + px * PS + 4 * m + 4 * tq);
                 float *dst = nzb + (col + (int64_t)n1 * c2) * K + mm0 * WS + 4 * tq;
                 if (col >= n1 || 4 * tq >= run) continue;
                 if (4 * tq + 4 <= run) {
@@ -668,8 +692,10 @@ __global__ __launch_bounds__(64, 2) void sim_rows_kernel(ApplyArgs a, int nwork)
     const int b = __builtin_amdgcn_readfirstlane(it / a.g.n2);
     if (t1 >= a.fa && t1 < a.fb)
         sim_body<WS, NCOMP, DIST, true>(a, gc, t1, c2, b);
+    else if (a.g.n1 % (4 / NCOMP) == 0)
+        sim_body<WS, NCOMP, DIST, false, true>(a, gc, t1, c2, b);
     else
-        sim_body<WS, NCOMP, DIST, false>(a, gc, t1, c2, b);
+        sim_body<WS, NCOMP, DIST, false, false>(a, gc, t1, c2, b);
 }
 
 // ---------------------------------------------------------------------------
@@ -690,13 +716,6 @@ __global__ __launch_bounds__(64, 2) void sim_rows_kernel(ApplyArgs a, int nwork)
 // ---------------------------------------------------------------------------
 constexpr int kCG = 8;          // components per lane group and pass
 constexpr int kCPass = 4 * kCG; // components per pass
-
-// s_waitcnt vmcnt(N) (gfx9 encoding, expcnt and lgkmcnt at their maximum)
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt has 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 template <int WS, int NCOMP, bool TRANS>
 struct A2 {
@@ -1157,10 +1176,12 @@ hipError_t launch_sim_t(ApplyArgs a, int64_t nb, hipStream_t s) {
     a.gchunk = (NIT + a.ichunk - 1) / a.ichunk;
     const int64_t nwork = waves * a.gchunk;
     const int64_t grid = 8 * ((nwork + 7) / 8);
-    // LDS: the staging area, which also holds 64 pixels x 4 window rows of
-    // results before they are stored (plus the 16 floats that the last
-    // pixel's 16 lanes read past its 4 ws)
-    const size_t lds = (size_t)std::max(SimStage<NCOMP>::SF, 64 * 4 * WS + 64) * sizeof(float);
+    // LDS: the staging ring, which also holds 64 pixels x 4 window rows of
+    // results before they are stored (skewed by 4 floats per 4 pixels, plus
+    // the 16 floats that the last pixel's 16 lanes read past its 4 ws)
+    const size_t lds =
+        (size_t)std::max(SimStage<NCOMP>::NR * SimStage<NCOMP>::SB, 64 * 4 * WS + 64 + 64) *
+        sizeof(float);
     hipLaunchKernelGGL((sim_rows_kernel<WS, NCOMP, DIST>), dim3((unsigned)grid), dim3(64), lds, s,
                        a, (int)nwork);
     return hipGetLastError();
