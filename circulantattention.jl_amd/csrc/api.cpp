@@ -140,9 +140,11 @@ int circatt_similarity(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int
     pr.q = static_cast<const float *>(x);
     pr.k = static_cast<const float *>(y);
     pr.nz = nzval;
+    // 2D windows up to 15 wide: the row kernel (faster than the matrix-core
+    // kernel at every measured size); otherwise the matrix-core kernel
     const bool rows_ok = sim_rows_supported(g, (int)C, ncomp, nb);
     const bool mfma_ok = fused_supported(MODE_SIM, pr);
-    if (rows_ok && (!mfma_ok || sim_rows_preferred(g, nb)))
+    if (rows_ok)
         return hip_result(launch_sim_rows(kind == CIRCATT_DISTANCE, ncomp, g, (int)C, nb, scale,
                                           pr.q, pr.k, nzval, as_stream(stream)),
                           "circatt_similarity");

@@ -1210,12 +1210,6 @@ bool sim_rows_supported(const Geom &g, int C, int ncomp, int64_t nb) {
     const int64_t grid = (int64_t)((g.n1 + 63) / 64) * g.n2 * nb * ((g.ws + 3) / 4) + 8;
     return grid > 0 && grid < ((int64_t)1 << 31);
 }
-bool sim_rows_preferred(const Geom &g, int64_t nb) {
-    // the vector kernel needs many row segments to hide its load latency;
-    // small grids go to the matrix-core kernel when it supports the shape
-    return (int64_t)((g.n1 + 63) / 64) * g.n2 * nb >= 1024;
-}
-
 hipError_t launch_sim_rows(bool dist, int ncomp, const Geom &g, int C, int64_t nb, float scale,
                            const float *x, const float *y, float *nz, hipStream_t s) {
     ApplyArgs a{};

@@ -23,7 +23,6 @@ hipError_t launch_apply_rb(bool trans, bool corr, int ncomp, const Geom &g, int 
                            hipStream_t s);
 // nzVal = scale * similarity for 2D windows 3 .. 15 (apply_rb.hip)
 bool sim_rows_supported(const Geom &g, int C, int ncomp, int64_t nb);
-bool sim_rows_preferred(const Geom &g, int64_t nb);
 hipError_t launch_sim_rows(bool dist, int ncomp, const Geom &g, int C, int64_t nb, float scale,
                            const float *x, const float *y, float *nz, hipStream_t s);
 // colsum (sum(A; dims=1)) through the transposed product's offset tables

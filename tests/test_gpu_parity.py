@@ -110,9 +110,8 @@ def test_similarity(ca, cuda, dims, ws, C, cplx, kind):
 @pytest.mark.parametrize("cplx", [False, True])
 @pytest.mark.parametrize("kind", [0, 1])
 def test_similarity_many_rows(ca, cuda, dims, ws, cplx, kind):
-    """Grids of 1024 or more 64-pixel row segments take the row-blocked
-    similarity kernel (smaller grids take the matrix-core kernel), 4 units,
-    against the oracle.  Neither width is a multiple of 64, so partial
+    """The row-blocked similarity kernel on many 64-pixel row segments, 4
+    units, against the oracle.  Neither width is a multiple of 64, so partial
     segments and the border body run; rows of 200 pixels also have interior
     segments."""
     C, B = 6, 4
