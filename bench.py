@@ -104,7 +104,12 @@ def cpu_baseline(name, budget_s=12.0):
 OPS_CONFIGS = {
     "cfg2": ((128, 96), 64, 2, 15, False),
     "cfg5": ((320, 320), 16, 4, 11, True),
+    # the large-window configurations (unfused path, windows past 15); only
+    # timed when named with --ops-config
+    "cfg4a": ((512, 512), 32, 1, 31, False),
+    "cfg4b": ((262144,), 32, 2, 63, False),
 }
+OPS_DEFAULT = ("cfg2", "cfg5")
 
 
 def bench_ops(args):
@@ -123,9 +128,9 @@ def bench_ops(args):
     g = torch.Generator(device=dev)
     g.manual_seed(2000)
     only_ops = set(filter(None, args.op.split(",")))
-    only_cfg = set(filter(None, args.ops_config.split(",")))
+    only_cfg = set(filter(None, args.ops_config.split(","))) or set(OPS_DEFAULT)
     for name, (dims, C, nb, ws, cplx) in OPS_CONFIGS.items():
-        if only_cfg and name not in only_cfg:
+        if name not in only_cfg:
             continue
         nsp = len(dims)
         n1, n2 = dims[0], (dims[1] if nsp == 2 else 1)
@@ -223,7 +228,8 @@ def main():
     ap.add_argument("--op", default="",
                     help="with --ops: comma-separated entry points to time (default: all)")
     ap.add_argument("--ops-config", default="",
-                    help="with --ops: comma-separated shapes to time (cfg2, cfg5; default: both)")
+                    help="with --ops: comma-separated shapes to time (cfg2, cfg5, cfg4a, cfg4b; "
+                         "default: cfg2,cfg5)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the (head, batch) units "

@@ -1076,6 +1076,384 @@ __global__ __launch_bounds__(64, 2) void apply2_kernel(ApplyArgs a, int nwork) {
         apply2_body<WS, NCOMP, TRANS, false, SUMS, false>(a, pass, t1, c2, b);
 }
 
+// ---------------------------------------------------------------------------
+// Wide windows (any odd ws, 1D or 2D; apply_wide_kernel): as apply2_kernel,
+// with every window row (the whole window in 1D) split into sub-rows of kJC
+// window columns.  Sub-row (dd, jc) covers slots j0 = kJC jc .. j0 + kJC - 1
+// of window row dd (horizontal offsets h = j0 + j - p) and is processed like
+// a window row of width kJC: per sub-row the wavefront stages one 16-float
+// sub-chunk of every pixel involved (64, or 64 + kJC - 1 source pixels for
+// the transposed product), and per step the x row's 80 columns that its
+// lanes' runs of 4 + kJC - 1 pixels cover.  Slots past the window (the last
+// sub-row of a row) are read as zeros.  ws and the dimension are run-time
+// values.
+// ---------------------------------------------------------------------------
+constexpr int kJC = 16;
+
+template <int NCOMP, bool TRANS>
+struct AW {
+    static constexpr int NSRC = TRANS ? 64 + kJC - 1 : 64;  // staged sub-chunks
+    static constexpr int Q = kJC / 4;                       // 16-byte pieces per sub-chunk
+    static constexpr int BLK = 4 * Q + 1;                   // slots per block of 4 (skewed)
+    static constexpr int NSLOT = (NSRC + 3) / 4 * BLK;
+    static constexpr int NZ4 = (NSLOT + 63) / 64;
+    static constexpr int NZ1 = (4 * NSLOT + 63) / 64;
+    static constexpr int NZB = NZ4 * 256 > NZ1 * 64 ? NZ4 * 256 : NZ1 * 64;
+    static constexpr int RW = 64 + kJC;                     // staged x columns
+    static constexpr int RF = NCOMP * RW;
+    static constexpr int XF = 4 * RF;
+    static constexpr int XL = (XF / 4 + 63) / 64;
+    static constexpr int XBF = XL * 256;
+    static constexpr int CHS = kCG / NCOMP;
+    static constexpr int NZR = 2, NXB = 3;
+    static constexpr int LDS = NZR * NZB + NXB * XBF + 4;
+    static constexpr int LDS_SUMS = 4 * NZB;
+    static_assert(CHS >= 2, "the step waits assume two or more steps per sub-row");
+};
+
+template <int NCOMP, bool TRANS, bool FAST, bool SUMS>
+__device__ __forceinline__ void apply_wide_body(const ApplyArgs &a, int pass, int t1, int c2,
+                                                int b) {
+    using S = AW<NCOMP, TRANS>;
+    constexpr int KW4 = (NCOMP * (kR + kJC - 1) + 3) / 4;
+    constexpr int ZI = FAST ? S::NZ4 : S::NZ1;
+    constexpr int XI = FAST ? S::XL : 4 * S::XL;
+    constexpr int NZR = !SUMS ? S::NZR : (3 * ZI < 64 ? 4 : 3);
+    static_assert(ZI + XI < 64 && (NZR - 1) * ZI < 64, "waits exceed vmcnt");
+    typedef __attribute__((address_space(3))) void *lptr;
+    const Geom &g = a.g;
+    const int WS = g.ws, P = g.p, K = g.K;
+    const bool two = g.nsp == 2;
+    const int n1 = g.n1, n2 = two ? g.n2 : 1;
+    const int WR = two ? WS : 1;              // window rows
+    const int NJC = (WS + kJC - 1) / kJC;     // sub-rows per window row
+    const int NSR = WR * NJC;                 // sub-rows
+    const int64_t Pp = g.P;
+    const int lane = threadIdx.x & 63;
+    const int l16 = lane & 15, grp = lane >> 4;
+    const int f1 = t1 * 64;
+    float *lz = circatt_lds_apply;
+    float *lx = lz + NZR * S::NZB;
+    const auto rs = rsrc(a.nz + (int64_t)b * Pp * K, Pp * K * 4);
+    const int ubytes = (int)(Pp * NCOMP * a.C * 4);
+    const auto rx = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, ubytes);
+    const int plane = (int)(NCOMP * Pp * 4);
+    const int s2own = two ? slot_shift(c2 + 1, n2, P) : 0;
+
+    // first horizontal offset and first staged column (sub-chunks, x) of a
+    // sub-row
+    auto h0_of = [&](int jc) { return kJC * jc - P; };
+    auto col0 = [&](int jc) { return TRANS ? f1 - h0_of(jc) - (kJC - 1) : f1; };
+    auto xcol0 = [&](int jc) { return TRANS ? f1 - h0_of(jc) - (kJC - 1) : f1 + h0_of(jc); };
+    // image row and chunk index of window row dd
+    auto zrow = [&](int dd, int &r2, int &mm) {
+        if (!two) {
+            r2 = 0;
+            mm = 0;
+        } else if (TRANS) {
+            r2 = pmod(c2 - (dd - P), n2);
+            mm = pmod(dd + slot_shift(r2 + 1, n2, P), WS);
+        } else {
+            r2 = c2;
+            mm = pmod(dd + s2own, WS);
+        }
+    };
+    // interior body: the lane's piece of sub-chunk w (LDS slot layout as in
+    // apply2_kernel), relative to the sub-row's first column and slot
+    int zo[ZI];
+    if (FAST) {
+#pragma unroll
+        for (int m = 0; m < ZI; ++m) {
+            const int f = lane + 64 * m;
+            const int kb = f / S::BLK, r = f - kb * S::BLK;
+            const int rq = r < 4 * S::Q ? r : 0;
+            const int w = min(4 * kb + rq / S::Q, S::NSRC - 1), q = rq - (rq / S::Q) * S::Q;
+            zo[m] = (w * K + 4 * q) * 4;
+        }
+    }
+    // border body: single slots, rotated by the column's slot shift; the
+    // offsets depend on the sub-row and are formed when it is staged
+    auto zo_border = [&](int m, int jc) {
+        const int f = (lane + 64 * m) >> 2;
+        const int kb = f / S::BLK, r = f - kb * S::BLK;
+        const int rq = r < 4 * S::Q ? r : 0;
+        const int w = min(4 * kb + rq / S::Q, S::NSRC - 1), q = rq - (rq / S::Q) * S::Q;
+        const int j = kJC * jc + 4 * q + ((lane + 64 * m) & 3);
+        const int col = pmod(col0(jc) + w, n1);
+        const int e = j < WS ? fold(j + shift0(col, n1, P), WS) : 0;
+        return (col * K + e) * 4;
+    };
+    auto stage_z = [&](int sr, int buf) {
+        const int dd = sr / NJC, jc = sr - dd * NJC;
+        int r2, mm;
+        zrow(dd, r2, mm);
+        float *dst = lz + buf * S::NZB;
+        if (FAST) {
+            const int so = __builtin_amdgcn_readfirstlane(
+                ((n1 * r2 + col0(jc)) * K + mm * WS + kJC * jc) * 4);
+#pragma unroll
+            for (int m = 0; m < ZI; ++m) {
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(dst + 256 * m), 16, zo[m] + so,
+                                                        0, 0, 0);
+            }
+        } else {
+            const int so = __builtin_amdgcn_readfirstlane((n1 * r2 * K + mm * WS) * 4);
+#pragma unroll
+            for (int m = 0; m < ZI; ++m) {
+                const int vo = zo_border(m, jc) + so;
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(dst + 64 * m), 4, vo, 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // x: group gs's channel ch0 + gs CHS + cl, columns xcol0 .. xcol0 + RW - 1
+    const int ch0 = pass * (kCPass / NCOMP);
+    int xo[XI];
+#pragma unroll
+    for (int m = 0; m < XI; ++m) {
+        const int f = FAST ? 4 * (lane + 64 * m) : lane + 64 * m;
+        const int fr = f < S::XF ? f : 0;
+        const int gs = fr / S::RF, w = fr - gs * S::RF;
+        xo[m] = (ch0 + gs * S::CHS) * plane + (FAST ? w * 4 : 0);
+    }
+    auto stage_x = [&](int t, int buf) {
+        const int sr = t / S::CHS, cl = t - sr * S::CHS;
+        const int dd = sr / NJC, jc = sr - dd * NJC;
+        int r2, mm;
+        if (TRANS)
+            zrow(dd, r2, mm);
+        else
+            r2 = two ? pmod(c2 + dd - P, n2) : 0;
+        float *dst = lx + buf * S::XBF;
+        if (FAST) {
+            const int so = __builtin_amdgcn_readfirstlane(NCOMP * (n1 * r2 + xcol0(jc)) * 4 +
+                                                          cl * plane);
+#pragma unroll
+            for (int m = 0; m < XI; ++m) {
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lptr)(dst + 256 * m), 16, xo[m] + so,
+                                                        0, 0, 0);
+            }
+        } else {
+            const int so = __builtin_amdgcn_readfirstlane(NCOMP * n1 * r2 * 4 + cl * plane);
+            const int xc = xcol0(jc);
+#pragma unroll
+            for (int m = 0; m < XI; ++m) {
+                const int f = lane + 64 * m;
+                const int fr = f < S::XF ? f : 0;
+                const int w = fr - (fr / S::RF) * S::RF, u = w / NCOMP, e = w - u * NCOMP;
+                const int vo = xo[m] + (NCOMP * pmod(xc + u, n1) + e) * 4 + so;
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lptr)(dst + 64 * m), 4, vo, 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    float acc[kR][kCG];
+    float asum[kR];
+#pragma unroll
+    for (int i = 0; i < kR; ++i) {
+        asum[i] = 0.f;
+#pragma unroll
+        for (int k = 0; k < kCG; ++k) acc[i][k] = 0.f;
+    }
+    // the lane's 4 x kJC coefficients of sub-row sr (zero past the window)
+    auto read_av = [&](float (&av)[kR][kJC], int zb, int sr) {
+        const int jn = WS - kJC * (sr % NJC);
+        const float *src = lz + zb * S::NZB;
+#pragma unroll
+        for (int i = 0; i < kR; ++i)
+#pragma unroll
+            for (int j = 0; j < kJC; ++j) {
+                const int c = TRANS ? i - j + kJC - 1 : i;
+                const float v = src[(4 * l16 + c) * kJC + 4 * (l16 + c / 4) + j];
+                av[i][j] = j < jn ? v : 0.f;
+            }
+    };
+
+    if (SUMS) {
+#pragma unroll
+        for (int r = 0; r < NZR - 1; ++r)
+            if (r < NSR) stage_z(r, r);
+#pragma unroll 1
+        for (int sr = 0; sr < NSR; ++sr) {
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+            if (sr + NZR - 1 < NSR) stage_z(sr + NZR - 1, (sr + NZR - 1) % NZR);
+            const int younger = min(NZR - 1, NSR - 1 - sr);
+            if (younger >= 3)
+                wait_vm<(NZR > 3 ? 3 : 2) * ZI>();
+            else if (younger == 2)
+                wait_vm<2 * ZI>();
+            else if (younger == 1)
+                wait_vm<ZI>();
+            else
+                wait_vm<0>();
+            float av[kR][kJC];
+            read_av(av, sr % NZR, sr);
+#pragma unroll
+            for (int i = 0; i < kR; ++i)
+#pragma unroll
+                for (int j = 0; j < kJC; ++j) asum[i] += av[i][j];
+        }
+        float *dst = a.y + (int64_t)b * Pp + f1 + 4 * l16 + (int64_t)n1 * c2;
+        const int col0l = f1 + 4 * l16;
+        if (grp == 0) {
+            if (col0l + kR <= n1) {
+                *(f4u *)dst = f4{asum[0], asum[1], asum[2], asum[3]};
+            } else {
+#pragma unroll
+                for (int i = 0; i < kR; ++i)
+                    if (col0l + i < n1) dst[i] = asum[i];
+            }
+        }
+        return;
+    }
+
+    // issue order and waits as in apply2_body, over T = NSR x CHS steps
+    const int T = NSR * S::CHS;
+    stage_z(0, 0);
+    stage_x(0, 0);
+    if (T > 1) stage_x(1, 1);
+    int xb = 0;
+    float av[kR][kJC];
+#pragma unroll 1
+    for (int sr = 0; sr < NSR; ++sr) {
+#pragma unroll
+        for (int cl = 0; cl < S::CHS; ++cl) {
+            const int t = sr * S::CHS + cl;
+            __builtin_amdgcn_sched_barrier(0);
+            const bool zy = cl == 1 && sr + 1 < NSR;
+            const bool xy = t + 1 < T;
+            if (zy && xy)
+                wait_vm<ZI + XI>();
+            else if (zy)
+                wait_vm<ZI>();
+            else if (xy)
+                wait_vm<XI>();
+            else
+                wait_vm<0>();
+            if (cl == 0) {
+                read_av(av, sr & 1, sr);
+                if (a.corr) {
+#pragma unroll
+                    for (int i = 0; i < kR; ++i)
+#pragma unroll
+                        for (int j = 0; j < kJC; ++j) asum[i] += av[i][j];
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+            if (cl == 0 && sr + 1 < NSR) stage_z(sr + 1, (sr + 1) & 1);
+            if (t + 2 < T) stage_x(t + 2, xb == 0 ? 2 : xb - 1);
+            float xw[4 * KW4];
+            const float *xr = lx + xb * S::XBF + grp * S::RF + NCOMP * 4 * l16;
+#pragma unroll
+            for (int h = 0; h < KW4; ++h) {
+                const f4 v = *(const f4 *)(xr + 4 * h);
+                xw[4 * h] = v[0];
+                xw[4 * h + 1] = v[1];
+                xw[4 * h + 2] = v[2];
+                xw[4 * h + 3] = v[3];
+            }
+#pragma unroll
+            for (int i = 0; i < kR; ++i)
+#pragma unroll
+                for (int j = 0; j < kJC; ++j)
+#pragma unroll
+                    for (int e = 0; e < NCOMP; ++e)
+                        acc[i][NCOMP * cl + e] = __builtin_fmaf(
+                            av[i][j], xw[NCOMP * (TRANS ? i - j + kJC - 1 : i + j) + e],
+                            acc[i][NCOMP * cl + e]);
+#pragma unroll
+            for (int i = 0; i < kR; ++i)
+#pragma unroll
+                for (int e = 0; e < NCOMP; ++e) asm volatile("" : "+v"(acc[i][NCOMP * cl + e]));
+            xb = xb == S::NXB - 1 ? 0 : xb + 1;
+        }
+    }
+    float *yb = a.y + (int64_t)b * Pp * NCOMP * a.C;
+    const float *zb = a.z ? a.z + (int64_t)b * Pp * NCOMP * a.C : nullptr;
+    const int colf = f1 + 4 * l16;
+    const int64_t pix0 = colf + (int64_t)n1 * c2;
+#pragma unroll
+    for (int cl = 0; cl < S::CHS; ++cl) {
+        const int ch = ch0 + grp * S::CHS + cl;
+        if (ch >= a.C) break;
+        float v[kR * NCOMP];
+#pragma unroll
+        for (int i = 0; i < kR; ++i)
+#pragma unroll
+            for (int e = 0; e < NCOMP; ++e) v[NCOMP * i + e] = acc[i][NCOMP * cl + e];
+        float *dst = yb + NCOMP * (pix0 + Pp * ch);
+        const float *zs = a.corr ? zb + NCOMP * (pix0 + Pp * ch) : nullptr;
+        if (colf + kR <= n1) {
+#pragma unroll
+            for (int h = 0; h < NCOMP; ++h) {
+                f4 r = f4{v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
+                if (a.corr) {
+                    const f4u z = *(const f4u *)(zs + 4 * h);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) r[q] -= asum[(4 * h + q) / NCOMP] * z[q];
+                }
+                *(f4u *)(dst + 4 * h) = r * a.scale;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kR; ++i) {
+                if (colf + i >= n1) break;
+#pragma unroll
+                for (int e = 0; e < NCOMP; ++e) {
+                    float r = v[NCOMP * i + e];
+                    if (a.corr) r -= asum[i] * zs[NCOMP * i + e];
+                    dst[NCOMP * i + e] = r * a.scale;
+                }
+            }
+        }
+    }
+}
+
+// One wavefront per (64 output pixels of an image row or of the line,
+// component pass, unit); work items in XCD bands.
+template <int NCOMP, bool TRANS, bool SUMS>
+__global__ __launch_bounds__(64, 2) void apply_wide_kernel(ApplyArgs a, int nwork) {
+    const int nper = (nwork + 7) >> 3;
+    int it = (int)(blockIdx.x & 7) * nper + (int)(blockIdx.x >> 3);
+    if (it >= nwork) return;
+    const int pass = __builtin_amdgcn_readfirstlane(it % a.gchunk);
+    it /= a.gchunk;
+    const int t1 = __builtin_amdgcn_readfirstlane(it % a.tiles1);
+    it /= a.tiles1;
+    const int n2 = a.g.nsp == 2 ? a.g.n2 : 1;
+    const int c2 = __builtin_amdgcn_readfirstlane(it % n2);
+    const int b = __builtin_amdgcn_readfirstlane(it / n2);
+    if (t1 >= a.fa && t1 < a.fb)
+        apply_wide_body<NCOMP, TRANS, true, SUMS>(a, pass, t1, c2, b);
+    else
+        apply_wide_body<NCOMP, TRANS, false, SUMS>(a, pass, t1, c2, b);
+}
+
+template <int NCOMP, bool TRANS, bool SUMS>
+hipError_t launch_wide(ApplyArgs a, int64_t nb, hipStream_t s) {
+    using S = AW<NCOMP, TRANS>;
+    const int n1 = a.g.n1, n2 = a.g.nsp == 2 ? a.g.n2 : 1;
+    a.tiles1 = (n1 + 63) / 64;
+    // interior segments: staged sub-chunk and x columns in range, no slot
+    // shift (2p + kJC columns of margin on either side)
+    const int edge = 2 * a.g.p + kJC;
+    a.fa = (edge + 63) / 64;
+    a.fb = n1 - 64 - edge >= 0 ? (n1 - 64 - edge) / 64 + 1 : 0;
+    if (a.fb > a.tiles1) a.fb = a.tiles1;
+    if (a.fb < a.fa) a.fb = a.fa;
+    a.gchunk = SUMS ? 1 : (NCOMP * a.C + kCPass - 1) / kCPass;
+    const int64_t nwork = (int64_t)a.tiles1 * n2 * nb * a.gchunk;
+    const size_t lds = (size_t)(SUMS ? S::LDS_SUMS : S::LDS) * sizeof(float);
+    hipLaunchKernelGGL((apply_wide_kernel<NCOMP, TRANS, SUMS>), dim3((unsigned)(8 * ((nwork + 7) / 8))),
+                       dim3(64), lds, s, a, (int)nwork);
+    return hipGetLastError();
+}
+
 // Interior tile columns [fa, fb): every lane row 2p or more inside dim 1.
 inline void interior_cols(const Geom &g, int &fa, int &fb) {
     const int tw = tile_w(g.nsp), tiles1 = (g.n1 + tw - 1) / tw;
@@ -1255,6 +1633,44 @@ hipError_t launch_apply_rb(bool trans, bool corr, int ncomp, const Geom &g, int 
     a.y = y;
     if (ncomp == 1) return trans ? dispatch_ws<1, true>(a, nb, s) : dispatch_ws<1, false>(a, nb, s);
     return trans ? dispatch_ws<2, true>(a, nb, s) : dispatch_ws<2, false>(a, nb, s);
+}
+
+bool apply_wide_supported(const Geom &g, int C, int ncomp, int64_t nb) {
+    if (g.ws < 3 || (g.ws & 1) == 0 || (g.nsp != 1 && g.nsp != 2)) return false;
+    // 32-bit byte offsets (reads reach kJC slots past a window row and up to
+    // kCPass channels past C), grid in one dimension
+    if ((g.P * g.K + kJC) * 4 >= (int64_t)1 << 31) return false;
+    if (g.P * ncomp * ((int64_t)C + kCPass) * 4 >= (int64_t)1 << 31) return false;
+    const int64_t n2 = g.nsp == 2 ? g.n2 : 1;
+    const int64_t grid = 8 + (int64_t)((g.n1 + 63) / 64) * n2 * nb * ((ncomp * C + kCPass - 1) / kCPass);
+    return grid > 0 && grid < ((int64_t)1 << 31);
+}
+
+hipError_t launch_apply_wide(bool trans, bool corr, int ncomp, const Geom &g, int C, int64_t nb,
+                             float scale, const float *nz, const float *x, const float *z, float *y,
+                             hipStream_t s) {
+    ApplyArgs a{};
+    a.g = g;
+    a.C = C;
+    a.corr = corr ? 1 : 0;
+    a.scale = scale;
+    a.nz = nz;
+    a.x = x;
+    a.z = z;
+    a.y = y;
+    if (ncomp == 1)
+        return trans ? launch_wide<1, true, false>(a, nb, s) : launch_wide<1, false, false>(a, nb, s);
+    return trans ? launch_wide<2, true, false>(a, nb, s) : launch_wide<2, false, false>(a, nb, s);
+}
+
+hipError_t launch_colsum_wide(const Geom &g, int64_t nb, const float *nz, float *out,
+                              hipStream_t s) {
+    ApplyArgs a{};
+    a.g = g;
+    a.C = 1;
+    a.nz = nz;
+    a.y = out;
+    return launch_wide<1, true, true>(a, nb, s);
 }
 
 hipError_t launch_colsum_rb(const Geom &g, int64_t nb, const float *nz, float *out, hipStream_t s) {

@@ -27,6 +27,14 @@ hipError_t launch_sim_rows(bool dist, int ncomp, const Geom &g, int C, int64_t n
                            const float *x, const float *y, float *nz, hipStream_t s);
 // colsum (sum(A; dims=1)) through the transposed product's offset tables
 hipError_t launch_colsum_rb(const Geom &g, int64_t nb, const float *nz, float *out, hipStream_t s);
+// Windows of any odd width in 1D and 2D (sub-rows of 16 window columns);
+// launch_apply / launch_sum route there for windows wider than 15.
+bool apply_wide_supported(const Geom &g, int C, int ncomp, int64_t nb);
+hipError_t launch_apply_wide(bool trans, bool corr, int ncomp, const Geom &g, int C, int64_t nb,
+                             float scale, const float *nz, const float *x, const float *z, float *y,
+                             hipStream_t s);
+hipError_t launch_colsum_wide(const Geom &g, int64_t nb, const float *nz, float *out,
+                              hipStream_t s);
 hipError_t launch_similarity(bool dist, int ncomp, const Geom &g, int C, int64_t nb, float scale,
                              const float *x, const float *y, float *nz, hipStream_t s);
 hipError_t launch_sum(bool col, const Geom &g, int64_t nb, const float *nz, float *out,

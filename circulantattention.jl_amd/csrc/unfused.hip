@@ -502,6 +502,8 @@ hipError_t launch_apply(bool trans, bool corr, int ncomp, const Geom &g, int C, 
                         hipStream_t s) {
     if (apply_rb_supported(g, C, ncomp, nb))
         return launch_apply_rb(trans, corr, ncomp, g, C, nb, scale, nz, x, z, y, s);
+    if (apply_wide_supported(g, C, ncomp, nb))
+        return launch_apply_wide(trans, corr, ncomp, g, C, nb, scale, nz, x, z, y, s);
 #define CIRCATT_APPLY_CASE(NC, T, CR)                                       \
     if (ncomp == NC && trans == T && corr == CR)                            \
         return launch_apply_t<NC, T, CR>(g, C, nb, scale, nz, x, z, y, s);
@@ -539,6 +541,7 @@ hipError_t launch_sum(bool col, const Geom &g, int64_t nb, const float *nz, floa
         return hipGetLastError();
     }
     if (col && apply_rb_supported(g, 1, 1, nb)) return launch_colsum_rb(g, nb, nz, out, s);
+    if (col && apply_wide_supported(g, 1, 1, nb)) return launch_colsum_wide(g, nb, nz, out, s);
     const unsigned grid = grid_for(g.P * nb, 256, 1LL << 31);
     if (col)
         hipLaunchKernelGGL(sum_kernel<true>, dim3(grid), dim3(256), 0, s, g, nb, nz, out);

@@ -141,7 +141,11 @@ APPLY_CASES = [((8,), 5, 4), ((8, 8), 5, 4), ((12, 10), 3, 8), ((4, 4), 5, 3), (
                ((33, 17), 11, 16),
                # 2D rows with interior 64-pixel segments (and a partial last one);
                # 203 is odd, so its border segments stage x float by float
-               ((200, 12), 11, 16), ((256, 6), 15, 8), ((203, 5), 7, 4)]
+               ((200, 12), 11, 16), ((256, 6), 15, 8), ((203, 5), 7, 4),
+               # windows past 15 (sub-rows of 16 window columns), 2D and 1D,
+               # with and without interior segments
+               ((70, 40), 31, 8), ((400, 3), 17, 4), ((300,), 63, 8), ((1000,), 63, 4),
+               ((37, 9), 19, 3)]
 
 
 @pytest.mark.parametrize("dims,ws,C", APPLY_CASES)
