@@ -453,6 +453,7 @@ __device__ __forceinline__ void wait_vm() {
 // with a vmcnt that counts the loads of the next channel.
 // ---------------------------------------------------------------------------
 constexpr int kHalo = 8;  // staged key columns beyond each side (>= p)
+constexpr int kJC = 16;   // window columns per sub-row (windows wider than 15)
 template <int NCOMP>
 struct SimStage {
     static constexpr int RW = 64 + 2 * kHalo;  // staged key columns per row
@@ -696,6 +697,248 @@ __global__ __launch_bounds__(64, 2) void sim_rows_kernel(ApplyArgs a, int nwork)
         sim_body<WS, NCOMP, DIST, false, true>(a, gc, t1, c2, b);
     else
         sim_body<WS, NCOMP, DIST, false, false>(a, gc, t1, c2, b);
+}
+
+// ---------------------------------------------------------------------------
+// Similarity for wide windows (any odd ws, 1D or 2D; sim_wide_kernel): tasks
+// are sub-rows (window row dd, columns j0 = 16 jc .. j0 + 15), and lane group
+// r takes task 4 itr + r, so that 1D windows (one window row) use all four
+// groups.  Per channel the four tasks' key rows (80 columns from
+// f1 + j0 - p) and the 64 queries are staged by LDS-DMA (a ring of 3, two
+// channels ahead).  Interior segments store through LDS, 4 lanes per
+// (pixel, task) run of 16 slots; border segments, whose slots are rotated,
+// store directly.
+// ---------------------------------------------------------------------------
+template <int NCOMP, bool DIST, bool FAST>
+__device__ __forceinline__ void sim_wide_body(const ApplyArgs &a, int t1, int c2, int b) {
+    using S = SimStage<NCOMP>;  // key rows of 80 columns, queries, ring
+    constexpr int KW4 = (NCOMP * (kR + kJC - 1) + 3) / 4;
+    constexpr int NK = FAST ? S::KL : S::KL1;
+    constexpr int NQ = FAST ? 1 : S::QL1;
+    constexpr int NI = NK + NQ;
+    static_assert(NI < 64, "vmcnt");
+    typedef __attribute__((address_space(3))) void *lptr;
+    const Geom &g = a.g;
+    const int WS = g.ws, P = g.p, K = g.K;
+    const bool two = g.nsp == 2;
+    const int n1 = g.n1, n2 = two ? g.n2 : 1;
+    const int WR = two ? WS : 1;
+    const int NJC = (WS + kJC - 1) / kJC;
+    const int NT = WR * NJC;                 // tasks
+    const int64_t Pp = g.P;
+    const int lane = threadIdx.x & 63;
+    const int l16 = lane & 15, rho = lane >> 4;
+    const int f1 = t1 * 64;
+    const int ubytes = (int)(Pp * NCOMP * a.C * 4);
+    const auto rq = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, ubytes);
+    const auto rk = rsrc(a.z + (int64_t)b * Pp * NCOMP * a.C, ubytes);
+    float *nzb = a.y + (int64_t)b * Pp * K;
+    float *lw = circatt_lds_apply;
+    const int s2 = two ? slot_shift(c2 + 1, n2, P) : 0;
+    const int plane = (int)(NCOMP * Pp * 4);
+    int qo[NQ];
+#pragma unroll
+    for (int m = 0; m < NQ; ++m) {
+        if (FAST) {
+            const int u = 4 * min(lane, S::QS - 1) / NCOMP;
+            qo[m] = NCOMP * (n1 * c2 + f1 + u) * 4;
+        } else {
+            const int f = lane + 64 * m, u = f / NCOMP, e = f - u * NCOMP;
+            qo[m] = (NCOMP * (n1 * c2 + pmod(f1 + u, n1)) + e) * 4;
+        }
+    }
+    // task -> window row, sub-row
+    auto task = [&](int tau, int &dd, int &jc) {
+        const int tc = min(tau, NT - 1);
+        dd = tc / NJC;
+        jc = tc - dd * NJC;
+    };
+
+    const int nit = (NT + 3) / 4;
+#pragma unroll 1
+    for (int itr = 0; itr < nit; ++itr) {
+        int ko[NK];
+#pragma unroll
+        for (int m = 0; m < NK; ++m) {
+            const int f = FAST ? 4 * min(lane + 64 * m, S::KS - 1) : lane + 64 * m;
+            const int rr = f / S::RF, w = f - rr * S::RF;
+            int dd, jc;
+            task(4 * itr + rr, dd, jc);
+            const int kr2 = two ? pmod(c2 + dd - P, n2) : 0;
+            const int u = w / NCOMP, e = w - u * NCOMP;
+            const int c0 = f1 + kJC * jc - P;
+            const int col = FAST ? c0 + u : pmod(c0 + u, n1);
+            ko[m] = (NCOMP * (n1 * kr2 + col) + e) * 4;
+        }
+        auto stage = [&](int c, int buf) {
+            const int cb = __builtin_amdgcn_readfirstlane(c * plane);
+            float *dst = lw + buf * S::SB;
+#pragma unroll
+            for (int m = 0; m < NK; ++m) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (FAST) {
+                    if (lane + 64 * m < S::KS)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lptr)(dst + 256 * m), 16,
+                                                                ko[m], cb, 0, 0);
+                } else {
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lptr)(dst + 64 * m), 4, ko[m],
+                                                            cb, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < NQ; ++m) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (FAST) {
+                    if (lane < S::QS)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lptr)(dst + S::QOFF), 16,
+                                                                qo[m], cb, 0, 0);
+                } else {
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lptr)(dst + S::QOFF + 64 * m), 4,
+                                                            qo[m], cb, 0, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        float acc[kR][kJC];
+#pragma unroll
+        for (int i = 0; i < kR; ++i)
+#pragma unroll
+            for (int j = 0; j < kJC; ++j) acc[i][j] = 0.f;
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+        stage(0, 0);
+        if (a.C > 1) stage(1, 1);
+        int cur = 0;
+#pragma unroll 1
+        for (int c = 0; c < a.C; ++c) {
+            if (c + 1 < a.C)
+                wait_vm<NI>();
+            else
+                wait_vm<0>();
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+            if (c + 2 < a.C) stage(c + 2, cur == 0 ? 2 : cur - 1);
+            const float *sb = lw + cur * S::SB;
+            float q[4 * NCOMP], kw[4 * KW4];
+#pragma unroll
+            for (int h = 0; h < NCOMP; ++h) {
+                const f4 v = *(const f4 *)(sb + S::QOFF + NCOMP * 4 * l16 + 4 * h);
+                q[4 * h] = v[0];
+                q[4 * h + 1] = v[1];
+                q[4 * h + 2] = v[2];
+                q[4 * h + 3] = v[3];
+            }
+            const float *kr = sb + rho * S::RF + NCOMP * 4 * l16;
+#pragma unroll
+            for (int h = 0; h < KW4; ++h) {
+                const f4 v = *(const f4 *)(kr + 4 * h);
+                kw[4 * h] = v[0];
+                kw[4 * h + 1] = v[1];
+                kw[4 * h + 2] = v[2];
+                kw[4 * h + 3] = v[3];
+            }
+#pragma unroll
+            for (int i = 0; i < kR; ++i)
+#pragma unroll
+                for (int j = 0; j < kJC; ++j)
+#pragma unroll
+                    for (int e = 0; e < NCOMP; ++e) {
+                        const float xv = q[NCOMP * i + e], yv = kw[NCOMP * (i + j) + e];
+                        if (DIST) {
+                            const float d = xv - yv;
+                            acc[i][j] = __builtin_fmaf(d, d, acc[i][j]);
+                        } else {
+                            acc[i][j] = __builtin_fmaf(xv, yv, acc[i][j]);
+                        }
+                    }
+            cur = cur == S::NR - 1 ? 0 : cur + 1;
+        }
+        // this group's task; slots past the window are not stored
+        const float sc = DIST ? -0.5f * a.scale : a.scale;
+        const int tau = 4 * itr + rho;
+        int dd, jc;
+        task(tau, dd, jc);
+        const bool live = tau < NT;
+        const int mm = two ? pmod(dd + s2, WS) : 0;
+        const int j0 = kJC * jc, jn = min(kJC, WS - j0);
+        if (FAST) {
+            // through LDS (the ring area is free: its last reads are complete
+            // and no load is in flight): pixel px, task r at
+            // px 64 + 4 (px / 4) + 16 r
+            if (live) {
+#pragma unroll
+                for (int i = 0; i < kR; ++i)
+#pragma unroll
+                    for (int j = 0; j < kJC; ++j)
+                        lw[(4 * l16 + i) * 64 + 4 * l16 + 16 * rho + j] = acc[i][j] * sc;
+            }
+            // 16 lanes per pixel: lane tq stores piece tq % 4 of task tq / 4
+            const int tq = lane & 15, g4 = lane >> 4, tr = tq >> 2, pc = tq & 3;
+            int ddt, jct;
+            task(4 * itr + tr, ddt, jct);
+            const bool livet = 4 * itr + tr < NT;
+            const int mmt = two ? pmod(ddt + s2, WS) : 0;
+            const int j0t = kJC * jct, jnt = min(kJC, WS - j0t);
+#pragma unroll 4
+            for (int m = 0; m < 16; ++m) {
+                const int px = 4 * m + g4, col = f1 + px;
+                const f4 v = *(const f4 *)(lw + px * 64 + 4 * m + 16 * tr + 4 * pc);
+                float *dst = nzb + (col + (int64_t)n1 * c2) * K + mmt * WS + j0t + 4 * pc;
+                if (!livet || col >= n1 || 4 * pc >= jnt) continue;
+                if (4 * pc + 4 <= jnt) {
+                    *(f4u *)dst = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 3; ++e)
+                        if (4 * pc + e < jnt) dst[e] = v[e];
+                }
+            }
+        } else if (live) {
+#pragma unroll
+            for (int i = 0; i < kR; ++i) {
+                const int col = f1 + 4 * l16 + i;
+                if (col >= n1) continue;
+                const int s1 = shift0(pmod(col, n1), n1, P);
+                float *row = nzb + (col + (int64_t)n1 * c2) * K + mm * WS;
+#pragma unroll
+                for (int j = 0; j < kJC; ++j)
+                    if (j < jn) row[fold(j0 + j + s1, WS)] = acc[i][j] * sc;
+            }
+        }
+    }
+}
+
+template <int NCOMP, bool DIST>
+__global__ __launch_bounds__(64, 2) void sim_wide_kernel(ApplyArgs a, int nwork) {
+    const int nper = (nwork + 7) >> 3;
+    int it = (int)(blockIdx.x & 7) * nper + (int)(blockIdx.x >> 3);
+    if (it >= nwork) return;
+    const int t1 = __builtin_amdgcn_readfirstlane(it % a.tiles1);
+    it /= a.tiles1;
+    const int n2 = a.g.nsp == 2 ? a.g.n2 : 1;
+    const int c2 = __builtin_amdgcn_readfirstlane(it % n2);
+    const int b = __builtin_amdgcn_readfirstlane(it / n2);
+    if (t1 >= a.fa && t1 < a.fb)
+        sim_wide_body<NCOMP, DIST, true>(a, t1, c2, b);
+    else
+        sim_wide_body<NCOMP, DIST, false>(a, t1, c2, b);
+}
+
+template <int NCOMP, bool DIST>
+hipError_t launch_sim_wide_t(ApplyArgs a, int64_t nb, hipStream_t s) {
+    using S = SimStage<NCOMP>;
+    const int n1 = a.g.n1, n2 = a.g.nsp == 2 ? a.g.n2 : 1;
+    a.tiles1 = (n1 + 63) / 64;
+    // interior: staged key columns f1 - p .. f1 + p + 79 in range, own
+    // columns free of slot shifts
+    const int edge = a.g.p + kJC;
+    a.fa = (edge + 63) / 64;
+    a.fb = n1 - 64 - edge >= 0 ? (n1 - 64 - edge) / 64 + 1 : 0;
+    if (a.fb > a.tiles1) a.fb = a.tiles1;
+    if (a.fb < a.fa) a.fb = a.fa;
+    const int64_t nwork = (int64_t)a.tiles1 * n2 * nb;
+    const size_t lds = (size_t)std::max(S::NR * S::SB, 64 * 64 + 64 + 64) * sizeof(float);
+    hipLaunchKernelGGL((sim_wide_kernel<NCOMP, DIST>), dim3((unsigned)(8 * ((nwork + 7) / 8))),
+                       dim3(64), lds, s, a, (int)nwork);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -1088,7 +1331,6 @@ __global__ __launch_bounds__(64, 2) void apply2_kernel(ApplyArgs a, int nwork) {
 // sub-row of a row) are read as zeros.  ws and the dimension are run-time
 // values.
 // ---------------------------------------------------------------------------
-constexpr int kJC = 16;
 
 template <int NCOMP, bool TRANS>
 struct AW {
@@ -1599,6 +1841,29 @@ hipError_t launch_sim_rows(bool dist, int ncomp, const Geom &g, int C, int64_t n
     a.y = nz;
     if (ncomp == 1) return dist ? sim_ws<1, true>(a, nb, s) : sim_ws<1, false>(a, nb, s);
     return dist ? sim_ws<2, true>(a, nb, s) : sim_ws<2, false>(a, nb, s);
+}
+
+bool sim_wide_supported(const Geom &g, int C, int ncomp, int64_t nb) {
+    if (g.ws < 3 || (g.ws & 1) == 0 || (g.nsp != 1 && g.nsp != 2)) return false;
+    if (g.P * g.K * 4 >= (int64_t)1 << 31) return false;
+    if (g.P * ncomp * (int64_t)C * 4 >= (int64_t)1 << 31) return false;
+    const int64_t n2 = g.nsp == 2 ? g.n2 : 1;
+    const int64_t grid = 8 + (int64_t)((g.n1 + 63) / 64) * n2 * nb;
+    return grid > 0 && grid < ((int64_t)1 << 31);
+}
+
+hipError_t launch_sim_wide(bool dist, int ncomp, const Geom &g, int C, int64_t nb, float scale,
+                           const float *x, const float *y, float *nz, hipStream_t s) {
+    ApplyArgs a{};
+    a.g = g;
+    a.C = C;
+    a.scale = scale;
+    a.x = x;
+    a.z = y;
+    a.y = nz;
+    if (ncomp == 1)
+        return dist ? launch_sim_wide_t<1, true>(a, nb, s) : launch_sim_wide_t<1, false>(a, nb, s);
+    return dist ? launch_sim_wide_t<2, true>(a, nb, s) : launch_sim_wide_t<2, false>(a, nb, s);
 }
 
 bool apply_rb_supported(const Geom &g, int C, int ncomp, int64_t nb) {

@@ -35,6 +35,10 @@ hipError_t launch_apply_wide(bool trans, bool corr, int ncomp, const Geom &g, in
                              hipStream_t s);
 hipError_t launch_colsum_wide(const Geom &g, int64_t nb, const float *nz, float *out,
                               hipStream_t s);
+// Similarity for windows of any odd width in 1D and 2D (sub-row tasks).
+bool sim_wide_supported(const Geom &g, int C, int ncomp, int64_t nb);
+hipError_t launch_sim_wide(bool dist, int ncomp, const Geom &g, int C, int64_t nb, float scale,
+                           const float *x, const float *y, float *nz, hipStream_t s);
 hipError_t launch_similarity(bool dist, int ncomp, const Geom &g, int C, int64_t nb, float scale,
                              const float *x, const float *y, float *nz, hipStream_t s);
 hipError_t launch_sum(bool col, const Geom &g, int64_t nb, const float *nz, float *out,
