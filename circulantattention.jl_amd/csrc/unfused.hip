@@ -37,6 +37,10 @@ __global__ void pattern_kernel(Geom g, int64_t nb, int32_t *__restrict__ rowptr,
 // row, the row's border shifts computed once per lane, each slot's window
 // offsets from t = mm * ws + m0 (quotient by a float reciprocal, exact for
 // t < 2^22), all batch copies written from the same column.
+typedef int i4u __attribute__((ext_vector_type(4), aligned(4)));  // 4-byte aligned
+// v folded into [0, n) for -n <= v < 2n
+__device__ __forceinline__ int fold_n(int v, int n) { return v < 0 ? v + n : (v >= n ? v - n : v); }
+
 __global__ __launch_bounds__(256) void pattern32_kernel(int nsp, int n1, int n2, int ws, int nb,
                                                         int32_t *__restrict__ rowptr,
                                                         int32_t *__restrict__ colval) {
@@ -46,21 +50,42 @@ __global__ __launch_bounds__(256) void pattern32_kernel(int nsp, int n1, int n2,
     const int PK = P * K;
     const float inv_ws = 1.f / (float)ws;
     const int gl = threadIdx.x & 15;
+    // every offset is within one period of the image (p < n1, n2): wrapped
+    // indices by one compare each instead of a remainder
+    const bool near = p < n1 && (nsp == 1 || p < n2);
     for (int r = blockIdx.x * 16 + (threadIdx.x >> 4); r < P; r += gridDim.x * 16) {
         const int i1 = r % n1, i2 = r / n1;
         const int s1 = slot_shift(i1 + 1, n1, p);
         const int s2 = nsp == 2 ? slot_shift(i2 + 1, n2, p) : 0;
-        for (int t = gl; t < K; t += 16) {
-            int mm = nsp == 2 ? (int)(((float)t + 0.5f) * inv_ws) : 0;
-            const int m0 = t - mm * ws;
-            const int d1 = slot_to_offset(m0, s1, ws, p);
-            int col = pmod(i1 + d1, n1);
-            if (nsp == 2) {
-                const int d2 = slot_to_offset(mm, s2, ws, p);
-                col += n1 * pmod(i2 + d2, n2);
+        // 16 lanes per row, 4 consecutive slots per lane and store
+        for (int t0 = 4 * gl; t0 < K; t0 += 64) {
+            int v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = min(t0 + e, K - 1);
+                const int mm = nsp == 2 ? (int)(((float)t + 0.5f) * inv_ws) : 0;
+                const int m0 = t - mm * ws;
+                int col;
+                if (near) {
+                    col = fold_n(i1 + fold_n(m0 - s1, ws) - p, n1);
+                    if (nsp == 2) col += n1 * fold_n(i2 + fold_n(mm - s2, ws) - p, n2);
+                } else {
+                    col = pmod(i1 + slot_to_offset(m0, s1, ws, p), n1);
+                    if (nsp == 2) col += n1 * pmod(i2 + slot_to_offset(mm, s2, ws, p), n2);
+                }
+                v[e] = col + 1;
             }
-            const int n = r * K + t;
-            for (int b = 0; b < nb; ++b) colval[n + (int64_t)b * PK] = col + 1;
+            const int n = r * K + t0;
+            for (int b = 0; b < nb; ++b) {
+                int32_t *dst = colval + n + (int64_t)b * PK;
+                if (t0 + 4 <= K) {
+                    *(i4u *)dst = i4u{v[0], v[1], v[2], v[3]};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 3; ++e)
+                        if (t0 + e < K) dst[e] = v[e];
+                }
+            }
         }
     }
     for (int r = blockIdx.x * blockDim.x + threadIdx.x; r <= P; r += gridDim.x * blockDim.x)
