@@ -89,7 +89,8 @@ def test_readme_quickstart_shape(ca, cuda):
 SIM_CASES = [((8,), 5, 4), ((8, 8), 5, 4), ((12, 10), 3, 8), ((32, 32), 7, 16), ((4, 4), 5, 4),
              ((2,), 5, 3), ((20, 13), 15, 64), ((9, 7), 3, 80), ((70,), 63, 32),
              # windows past 15 (sub-row kernel), with and without interior segments
-             ((70, 40), 31, 8), ((160, 6), 17, 4), ((700,), 63, 4), ((37, 9), 19, 3)]
+             ((70, 40), 31, 8), ((160, 6), 17, 4), ((700,), 63, 4), ((37, 9), 19, 3),
+             ((10, 40), 17, 3), ((40,), 63, 2)]
 
 
 @pytest.mark.parametrize("dims,ws,C", SIM_CASES)
@@ -147,7 +148,9 @@ APPLY_CASES = [((8,), 5, 4), ((8, 8), 5, 4), ((12, 10), 3, 8), ((4, 4), 5, 3), (
                # windows past 15 (sub-rows of 16 window columns), 2D and 1D,
                # with and without interior segments
                ((70, 40), 31, 8), ((400, 3), 17, 4), ((300,), 63, 8), ((1000,), 63, 4),
-               ((37, 9), 19, 3)]
+               ((37, 9), 19, 3),
+               # window wider than the image along dim 1 (columns wrap more than once)
+               ((10, 40), 17, 3), ((40,), 63, 2)]
 
 
 @pytest.mark.parametrize("dims,ws,C", APPLY_CASES)
