@@ -52,7 +52,7 @@ struct ApplyArgs {
     Geom g;
     int C;           // channels per unit
     int corr;        // subtract sums(A) .* z
-    int tiles1, tiles2;
+    int tiles1;      // 64-pixel (2D) or 256-pixel (1D) segments per row
     int fa, fb;      // tile columns [fa, fb) are interior
     int gchunk;      // chunk groups on the grid
     int ichunk;      // chunks per wavefront
@@ -77,32 +77,31 @@ __device__ __forceinline__ f4 bload4(__amdgpu_buffer_rsrc_t r, int voff, int sof
     return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
-// Per-lane geometry shared by the apply and the column sum.
+// ---------------------------------------------------------------------------
+// 1D products and column sums for windows up to 15 (apply_rb_kernel,
+// colsum_rb_kernel; 2D and wider windows have the kernels further below).
+// A wavefront owns 256 pixels of the line in 4 lane rows of 64 (lane row
+// rho = lane >> 4, pixels f1 = 256 t1 + 64 rho ..).
+// ---------------------------------------------------------------------------
 template <int WS>
 struct Lane {
     static constexpr int P = (WS - 1) / 2;
     int l16, rho;   // lane within its lane row, lane row
     int f1;         // first column of the lane row
-    int c2;         // image row of the lane row (wrapped into range)
-    bool row_ok;
-    __device__ Lane(const Geom &g, int t1, int t2) {
+    __device__ explicit Lane(int t1) {
         const int lane = threadIdx.x & 63;
         l16 = lane & 15;
         rho = lane >> 4;
-        const bool two = g.nsp == 2;
-        f1 = two ? t1 * 64 : t1 * 256 + 64 * rho;
-        const int c2u = two ? t2 * 4 + rho : 0;
-        row_ok = c2u < g.n2;
-        c2 = row_ok ? c2u : c2u % g.n2;
+        f1 = t1 * 256 + 64 * rho;
     }
     __device__ int col(int i) const { return f1 + 4 * l16 + i; }
 };
 
-// Stages the slot chunks of one window row into the wavefront's LDS buffer
-// with LDS-DMA buffer loads (no registers): chunk u (0 <= u < NS) of source
-// column f1 - off + u (wrapped) of each lane row.  A load instruction covers
-// chunk u of all 4 lane rows; lane 4 e + r loads element e of lane row r, and
-// the instruction's 64 dwords land at u * kPU, so element e of chunk u of lane
+// Stages the slot chunks of the line into the wavefront's LDS buffer with
+// LDS-DMA buffer loads (no registers): chunk u (0 <= u < NS) of source column
+// f1 - off + u (wrapped) of each lane row.  A load instruction covers chunk u
+// of all 4 lane rows; lane 4 e + r loads element e of lane row r, and the
+// instruction's 64 dwords land at u * kPU, so element e of chunk u of lane
 // row r sits at u * kPU + 4 e + r.  With kPU = 65 the owners' reads
 // (u = 4 l16 + i, lane row r) fall in 64 different banks.
 constexpr int kPU = 65;
@@ -110,13 +109,14 @@ __host__ __device__ constexpr int lds_floats(int ws, bool trans) { return nsrc(w
 
 template <int WS, int NS, bool FAST>
 __device__ __forceinline__ void stage_dma(float *lw, const Geom &g, __amdgpu_buffer_rsrc_t rs,
-                                          int f1r, int r2r, int mmr, int off, int k4) {
+                                          int t1, int off, int k4) {
     const int e = min((int)(threadIdx.x & 63) >> 2, WS - 1);
+    const int f1r = t1 * 256 + 64 * (threadIdx.x & 3);  // first column of lane row lane & 3
     typedef __attribute__((address_space(3))) void *lptr;
     // each load's offset is formed right before it (fences keep the
     // scheduler from computing all of them up front into registers)
     if (FAST) {
-        const int vo = (f1r - off + g.n1 * r2r) * k4 + (mmr * WS + e) * 4;
+        const int vo = (f1r - off) * k4 + e * 4;
         int so = 0;
 #pragma unroll
         for (int u = 0; u < NS; ++u) {
@@ -126,7 +126,7 @@ __device__ __forceinline__ void stage_dma(float *lw, const Geom &g, __amdgpu_buf
             so += k4;
         }
     } else {
-        const int vo = g.n1 * r2r * k4 + (mmr * WS + e) * 4;
+        const int vo = e * 4;
         int c = pmod(f1r - off, g.n1);
 #pragma unroll
         for (int u = 0; u < NS; ++u) {
@@ -143,46 +143,6 @@ __device__ __forceinline__ void stage_dma(float *lw, const Geom &g, __amdgpu_buf
 constexpr int kWaitAll = 0;
 constexpr int kWaitLgkm = 0x0070 | 0xC000 | 0x000F;  // lgkmcnt(0), vmcnt and expcnt at max
 
-// Geometry of the lane row whose chunks this lane stages (lane & 3): first
-// source column, source image row and chunk index at iteration dd.
-//   forward (A ⊗ x): iteration dd is window row d2 = dd - p of the lane
-//     row's own pixels;
-//   transposed, 2D: iteration dd is source image row t2 * 4 - p + dd, shared
-//     by the 4 lane rows (output rows t2 * 4 + r), which need its chunks of
-//     window rows d2 = r + p - dd: 4 adjacent chunks of every source pixel,
-//     one contiguous run per load instruction.  Lane rows whose d2 falls
-//     outside the window stage a clamped chunk they do not use.
-template <int WS>
-__device__ __forceinline__ int trans_d2(int r, int dd) {
-    constexpr int P = (WS - 1) / 2;
-    return r + P - dd;
-}
-template <int WS>
-__device__ __forceinline__ void staging_row(const Geom &g, int t1, int t2, int dd, bool trans,
-                                            int &f1r, int &r2r, int &mmr) {
-    constexpr int P = (WS - 1) / 2;
-    const int r = threadIdx.x & 3;
-    const bool two = g.nsp == 2;
-    f1r = two ? t1 * 64 : t1 * 256 + 64 * r;
-    if (two && trans) {
-        r2r = pmod(t2 * 4 - P + dd, g.n2);
-        const int d2 = min(P, max(-P, trans_d2<WS>(r, dd)));
-        mmr = pmod(d2 + P + slot_shift(r2r + 1, g.n2, P), WS);
-    } else if (two) {
-        const int c2u = t2 * 4 + r;
-        r2r = c2u < g.n2 ? c2u : c2u % g.n2;
-        mmr = pmod(dd + slot_shift(r2r + 1, g.n2, P), WS);
-    } else {
-        r2r = 0;
-        mmr = 0;
-    }
-}
-// iterations of the staging loop
-template <int WS>
-__host__ __device__ constexpr int n_iter(bool two, bool trans) {
-    return two ? (trans ? WS + 3 : WS) : 1;
-}
-
 // slot_shift of 0-based column c (same case order as slot_shift)
 __device__ __forceinline__ int shift0(int c, int n, int p) {
     return c + 1 <= p ? c - p : (c + 1 > n - p ? p - n + c + 1 : 0);
@@ -193,7 +153,7 @@ __device__ __forceinline__ int fold(int v, int ws) {
 }
 
 template <int WS, int NCOMP, bool TRANS, bool FAST>
-__device__ __forceinline__ void apply_body(const ApplyArgs &a, int gc, int t1, int t2, int b) {
+__device__ __forceinline__ void apply_body(const ApplyArgs &a, int gc, int t1, int b) {
     using L_ = Lane<WS>;
     constexpr int P = L_::P;
     constexpr int XW = kR + 2 * P;                 // x run per lane
@@ -202,21 +162,17 @@ __device__ __forceinline__ void apply_body(const ApplyArgs &a, int gc, int t1, i
     constexpr int NS = nsrc(WS, TRANS);
     constexpr int CCH = kCP / NCOMP;               // channels per staging pass
     const Geom &g = a.g;
-    const bool two = g.nsp == 2;
-    const int n1 = g.n1, n2 = g.n2, K = g.K;
+    const int n1 = g.n1, K = g.K;
     const int64_t Pp = g.P;
-    const L_ L(g, t1, t2);
+    const L_ L(t1);
     float *lw = circatt_lds_apply;
     const auto rs = rsrc(a.nz + (int64_t)b * Pp * K, Pp * K * 4);
     const auto rx = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, Pp * NCOMP * a.C * 4);
-    const int nd2 = n_iter<WS>(two, TRANS);
 
-    // x run of channel c at iteration dd (window row dd - p of the own image
-    // row, or the source image row of the transposed product)
-    auto load_x = [&](float (&xw)[4 * XN4], int c, int dd, int f1) {
-        const int xr2 = two ? pmod(TRANS ? t2 * 4 - P + dd : L.c2 + dd - P, n2) : 0;
+    // x run of channel c: columns f1 + 4 l16 - p .. (wrapped in the border body)
+    auto load_x = [&](float (&xw)[4 * XN4], int c, int f1) {
         const int cw = c < a.C ? c : a.C - 1;
-        const int rowoff = (int)(NCOMP * ((int64_t)n1 * xr2 + Pp * cw)) * 4;
+        const int rowoff = (int)(NCOMP * Pp * cw) * 4;
         if (FAST) {
             const int vo = rowoff + NCOMP * (f1 + 4 * L.l16 - P) * 4;
 #pragma unroll
@@ -238,11 +194,6 @@ __device__ __forceinline__ void apply_body(const ApplyArgs &a, int gc, int t1, i
             }
         }
     };
-    auto stage = [&](int dd, int k4) {
-        int f1r, r2r, mmr;
-        staging_row<WS>(g, t1, t2, dd, TRANS, f1r, r2r, mmr);
-        stage_dma<WS, NS, FAST>(lw, g, rs, f1r, r2r, mmr, TRANS ? P : 0, k4);
-    };
 
     for (int ci = 0; ci < a.ichunk; ++ci) {
         const int k0 = (gc * a.ichunk + ci) * kCP;
@@ -257,80 +208,72 @@ __device__ __forceinline__ void apply_body(const ApplyArgs &a, int gc, int t1, i
         }
         // the buffer is free: the previous chunk's reads completed before
         // its last products
-        stage(0, 4 * K);
-        for (int dd = 0; dd < nd2; ++dd) {
-            // f1 and k4 are redefined in every iteration so that per-chunk
-            // and per-column offsets are recomputed here instead of being
-            // hoisted out of the loop as tables of registers
-            int f1 = L.f1, k4 = 4 * K;
-            asm volatile("" : "+v"(f1), "+s"(k4));
-            __builtin_amdgcn_s_waitcnt(kWaitAll);  // this iteration's chunks are in LDS
-            // transposed, 2D: this lane row's window row at this source row
-            const int d2t = trans_d2<WS>(L.rho, dd);
-            const bool live = !(TRANS && two) || (d2t >= -P && d2t <= P);
-            float av[kR][WS];
+        stage_dma<WS, NS, FAST>(lw, g, rs, t1, TRANS ? P : 0, 4 * K);
+        // f1 is redefined here so that per-column offsets are recomputed
+        // instead of being hoisted out of the chunk loop as register tables
+        int f1 = L.f1;
+        asm volatile("" : "+v"(f1));
+        __builtin_amdgcn_s_waitcnt(kWaitAll);  // the chunks are in LDS
+        float av[kR][WS];
 #pragma unroll
-            for (int i = 0; i < kR; ++i) {
-                // border body: wrapped source column of offset j, stepped
-                // from one modulo per pixel
-                int c1 = 0, s1 = 0;
+        for (int i = 0; i < kR; ++i) {
+            // border body: wrapped source column of offset j, stepped from
+            // one modulo per pixel
+            int c1 = 0, s1 = 0;
+            if (!FAST) {
+                c1 = pmod(f1 + 4 * L.l16 + i + (TRANS ? P : 0), n1);
+                if (!TRANS) s1 = shift0(c1, n1, P);
+            }
+#pragma unroll
+            for (int j = 0; j < WS; ++j) {
+                const int u = TRANS ? 4 * L.l16 + i - j + 2 * P : 4 * L.l16 + i;
+                int pos = j;
                 if (!FAST) {
-                    c1 = pmod(f1 + 4 * L.l16 + i + (TRANS ? P : 0), n1);
-                    if (!TRANS) s1 = shift0(c1, n1, P);
-                }
-#pragma unroll
-                for (int j = 0; j < WS; ++j) {
-                    const int u = TRANS ? 4 * L.l16 + i - j + 2 * P : 4 * L.l16 + i;
-                    int pos = j;
-                    if (!FAST) {
-                        if (TRANS) {
-                            pos = fold(j + shift0(c1, n1, P), WS);
-                            c1 = c1 == 0 ? n1 - 1 : c1 - 1;
-                        } else {
-                            pos = fold(j + s1, WS);
-                        }
+                    if (TRANS) {
+                        pos = fold(j + shift0(c1, n1, P), WS);
+                        c1 = c1 == 0 ? n1 - 1 : c1 - 1;
+                    } else {
+                        pos = fold(j + s1, WS);
                     }
-                    const float v = lw[u * kPU + 4 * pos + L.rho];
-                    av[i][j] = live ? v : 0.f;
                 }
-            }
-            // every read of the buffer has returned before the next
-            // iteration's chunks are loaded into it
-            __builtin_amdgcn_s_waitcnt(kWaitLgkm);
-            if (dd + 1 < nd2) stage(dd + 1, k4);
-            if (a.corr) {
-#pragma unroll
-                for (int i = 0; i < kR; ++i)
-#pragma unroll
-                    for (int j = 0; j < WS; ++j) asum[i] += av[i][j];
-            }
-            // products, one channel (NCOMP components) at a time; channels
-            // past C are computed on a clamped channel and not stored
-#pragma unroll
-            for (int cl = 0; cl < CCH; ++cl) {
-                float xc[4 * XN4];
-                // nothing crosses these fences, so the loads of later channels
-                // are not hoisted over the products into registers
-                __builtin_amdgcn_sched_barrier(0);
-                load_x(xc, k0 / NCOMP + cl, dd, f1);
-#pragma unroll
-                for (int i = 0; i < kR; ++i)
-#pragma unroll
-                    for (int j = 0; j < WS; ++j)
-#pragma unroll
-                        for (int e = 0; e < NCOMP; ++e)
-                            acc[i][NCOMP * cl + e] = __builtin_fmaf(
-                                av[i][j], xc[NCOMP * (TRANS ? i - j + 2 * P : i + j) + e],
-                                acc[i][NCOMP * cl + e]);
+                av[i][j] = lw[u * kPU + 4 * pos + L.rho];
             }
         }
+        if (a.corr) {
+#pragma unroll
+            for (int i = 0; i < kR; ++i)
+#pragma unroll
+                for (int j = 0; j < WS; ++j) asum[i] += av[i][j];
+        }
+        // products, one channel (NCOMP components) at a time; channels past C
+        // are computed on a clamped channel and not stored
+#pragma unroll
+        for (int cl = 0; cl < CCH; ++cl) {
+            float xc[4 * XN4];
+            // nothing crosses these fences, so the loads of later channels are
+            // not hoisted over the products into registers
+            __builtin_amdgcn_sched_barrier(0);
+            load_x(xc, k0 / NCOMP + cl, f1);
+#pragma unroll
+            for (int i = 0; i < kR; ++i)
+#pragma unroll
+                for (int j = 0; j < WS; ++j)
+#pragma unroll
+                    for (int e = 0; e < NCOMP; ++e)
+                        acc[i][NCOMP * cl + e] =
+                            __builtin_fmaf(av[i][j], xc[NCOMP * (TRANS ? i - j + 2 * P : i + j) + e],
+                                           acc[i][NCOMP * cl + e]);
+        }
+        // every read of the buffer has returned before the next chunk's
+        // loads refill it
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm);
         // store the chunk
         float *yb = a.y + (int64_t)b * Pp * NCOMP * a.C;
         const float *zb = a.z ? a.z + (int64_t)b * Pp * NCOMP * a.C : nullptr;
 #pragma unroll
         for (int i = 0; i < kR; ++i) {
-            if (!L.row_ok || L.col(i) >= n1) continue;
-            const int64_t pix = L.col(i) + (int64_t)n1 * L.c2;
+            if (L.col(i) >= n1) continue;
+            const int64_t pix = L.col(i);
 #pragma unroll
             for (int kk = 0; kk < kCP; ++kk) {
                 const int k = k0 + kk;
@@ -345,10 +288,10 @@ __device__ __forceinline__ void apply_body(const ApplyArgs &a, int gc, int t1, i
     }
 }
 
-// One wavefront per (chunk group, 64 x 4 tile, unit).  Tile columns [fa, fb)
-// lie 2p or more inside dim 1 (no wrap of x or of source rows, no slot shift)
-// and take the interior body, whose offsets are immediates; the others take
-// the border body, which computes wrapped columns and shifted slots per value.
+// One wavefront per (chunk group, 256 pixels, unit).  Tiles [fa, fb) lie 2p
+// or more inside the line (no wrap of x, no slot shift) and take the interior
+// body, whose offsets are immediates; the others take the border body, which
+// computes wrapped columns and shifted slots per value.
 template <int WS, int NCOMP, bool TRANS>
 __global__ __launch_bounds__(64, 2) void apply_rb_kernel(ApplyArgs a) {
     // item indices (integer division runs on the vector unit: bring the
@@ -358,76 +301,52 @@ __global__ __launch_bounds__(64, 2) void apply_rb_kernel(ApplyArgs a) {
     const int gc = __builtin_amdgcn_readfirstlane(it % a.gchunk);
     it /= a.gchunk;
     const int t1 = __builtin_amdgcn_readfirstlane(it % a.tiles1);
-    it /= a.tiles1;
-    const int t2 = __builtin_amdgcn_readfirstlane(it % a.tiles2);
-    const int b = __builtin_amdgcn_readfirstlane(it / a.tiles2);
+    const int b = __builtin_amdgcn_readfirstlane(it / a.tiles1);
     if (t1 >= a.fa && t1 < a.fb)
-        apply_body<WS, NCOMP, TRANS, true>(a, gc, t1, t2, b);
+        apply_body<WS, NCOMP, TRANS, true>(a, gc, t1, b);
     else
-        apply_body<WS, NCOMP, TRANS, false>(a, gc, t1, t2, b);
+        apply_body<WS, NCOMP, TRANS, false>(a, gc, t1, b);
 }
 
 // sum(A; dims=1): out[c] = sum over window offsets d of A[c - d, slot(c - d, d)]
 template <int WS, bool FAST>
-__device__ __forceinline__ void colsum_body(const Geom &g, int t1, int t2, int b, const float *nz,
+__device__ __forceinline__ void colsum_body(const Geom &g, int t1, int b, const float *nz,
                                             float *out) {
     using L_ = Lane<WS>;
     constexpr int P = L_::P;
     constexpr int NS = nsrc(WS, true);
-    const bool two = g.nsp == 2;
     const int n1 = g.n1, K = g.K;
-    const L_ L(g, t1, t2);
+    const L_ L(t1);
     float *lw = circatt_lds_apply;
     const auto rs = rsrc(nz + (int64_t)b * g.P * K, g.P * K * 4);
     float s[kR] = {0.f, 0.f, 0.f, 0.f};
-    const int nd2 = n_iter<WS>(two, true);
-    auto stage = [&](int dd, int k4) {
-        int f1r, r2r, mmr;
-        staging_row<WS>(g, t1, t2, dd, true, f1r, r2r, mmr);
-        stage_dma<WS, NS, FAST>(lw, g, rs, f1r, r2r, mmr, P, k4);
-    };
-    stage(0, 4 * K);
-    for (int dd = 0; dd < nd2; ++dd) {
-        int f1 = L.f1, k4 = 4 * K;
-        asm volatile("" : "+v"(f1), "+s"(k4));
-        __builtin_amdgcn_s_waitcnt(kWaitAll);
-        const int d2t = trans_d2<WS>(L.rho, dd);
-        const bool live = !two || (d2t >= -P && d2t <= P);
-        float v[kR][WS];
-#pragma unroll
-        for (int i = 0; i < kR; ++i)
-#pragma unroll
-            for (int j = 0; j < WS; ++j) {
-                const int u = 4 * L.l16 + i - j + 2 * P;
-                int pos = j;
-                if (!FAST) pos = fold(j + shift0(pmod(f1 - P + u, n1), n1, P), WS);
-                const float x = lw[u * kPU + 4 * pos + L.rho];
-                v[i][j] = live ? x : 0.f;
-            }
-        __builtin_amdgcn_s_waitcnt(kWaitLgkm);
-        if (dd + 1 < nd2) stage(dd + 1, k4);
-#pragma unroll
-        for (int i = 0; i < kR; ++i)
-#pragma unroll
-            for (int j = 0; j < WS; ++j) s[i] += v[i][j];
-    }
+    stage_dma<WS, NS, FAST>(lw, g, rs, t1, P, 4 * K);
+    int f1 = L.f1;
+    asm volatile("" : "+v"(f1));
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
 #pragma unroll
     for (int i = 0; i < kR; ++i)
-        if (L.row_ok && L.col(i) < n1) out[(int64_t)b * g.P + L.col(i) + (int64_t)n1 * L.c2] = s[i];
+#pragma unroll
+        for (int j = 0; j < WS; ++j) {
+            const int u = 4 * L.l16 + i - j + 2 * P;
+            int pos = j;
+            if (!FAST) pos = fold(j + shift0(pmod(f1 - P + u, n1), n1, P), WS);
+            s[i] += lw[u * kPU + 4 * pos + L.rho];
+        }
+#pragma unroll
+    for (int i = 0; i < kR; ++i)
+        if (L.col(i) < n1) out[(int64_t)b * g.P + L.col(i)] = s[i];
 }
 
 template <int WS>
-__global__ __launch_bounds__(64, 2) void colsum_rb_kernel(Geom g, int tiles1, int tiles2, int fa,
-                                                          int fb, const float *nz, float *out) {
-    int it = blockIdx.x;
-    const int t1 = __builtin_amdgcn_readfirstlane(it % tiles1);
-    it /= tiles1;
-    const int t2 = __builtin_amdgcn_readfirstlane(it % tiles2);
-    const int b = __builtin_amdgcn_readfirstlane(it / tiles2);
+__global__ __launch_bounds__(64, 2) void colsum_rb_kernel(Geom g, int tiles1, int fa, int fb,
+                                                          const float *nz, float *out) {
+    const int t1 = __builtin_amdgcn_readfirstlane((int)blockIdx.x % tiles1);
+    const int b = __builtin_amdgcn_readfirstlane((int)blockIdx.x / tiles1);
     if (t1 >= fa && t1 < fb)
-        colsum_body<WS, true>(g, t1, t2, b, nz, out);
+        colsum_body<WS, true>(g, t1, b, nz, out);
     else
-        colsum_body<WS, false>(g, t1, t2, b, nz, out);
+        colsum_body<WS, false>(g, t1, b, nz, out);
 }
 
 // s_waitcnt vmcnt(N) (gfx9 encoding, expcnt and lgkmcnt at their maximum)
@@ -1725,7 +1644,7 @@ hipError_t launch_rb(ApplyArgs a, int64_t nb, hipStream_t s) {
     }
     const size_t lds = (size_t)lds_floats(WS, TRANS) * sizeof(float);
     interior_cols(a.g, a.fa, a.fb);
-    const int64_t grid = (int64_t)a.gchunk * a.tiles1 * a.tiles2 * nb;
+    const int64_t grid = (int64_t)a.gchunk * a.tiles1 * nb;
     hipLaunchKernelGGL((apply_rb_kernel<WS, NCOMP, TRANS>), dim3((unsigned)grid), dim3(64), lds, s,
                        a);
     return hipGetLastError();
@@ -1766,12 +1685,11 @@ hipError_t launch_colsum_t(const Geom &g, int64_t nb, const float *nz, float *ou
         return hipGetLastError();
     }
     const int tiles1 = (g.n1 + tile_w(g.nsp) - 1) / tile_w(g.nsp);
-    const int tiles2 = (g.n2 + tile_h(g.nsp) - 1) / tile_h(g.nsp);
     int fa, fb;
     interior_cols(g, fa, fb);
-    hipLaunchKernelGGL(colsum_rb_kernel<WS>, dim3((unsigned)((int64_t)tiles1 * tiles2 * nb)),
-                       dim3(64), (size_t)lds_floats(WS, true) * sizeof(float), s, g, tiles1,
-                       tiles2, fa, fb, nz, out);
+    hipLaunchKernelGGL(colsum_rb_kernel<WS>, dim3((unsigned)((int64_t)tiles1 * nb)), dim3(64),
+                       (size_t)lds_floats(WS, true) * sizeof(float), s, g, tiles1, fa, fb, nz,
+                       out);
     return hipGetLastError();
 }
 
@@ -1884,7 +1802,6 @@ hipError_t launch_apply_rb(bool trans, bool corr, int ncomp, const Geom &g, int 
     a.C = C;
     a.corr = corr ? 1 : 0;
     a.tiles1 = (g.n1 + tile_w(g.nsp) - 1) / tile_w(g.nsp);
-    a.tiles2 = (g.n2 + tile_h(g.nsp) - 1) / tile_h(g.nsp);
     // staging passes of one tile run in one wavefront (nzVal re-read from L2)
     // unless the grid would be too small to fill the GPU
     const int npass = (ncomp * C + kCP - 1) / kCP;
