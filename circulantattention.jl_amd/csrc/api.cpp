@@ -215,6 +215,15 @@ int circatt_similarity_bwd(int kind, int dtype, int nsp, int64_t n1, int64_t n2,
     const bool dist = kind == CIRCATT_DISTANCE;
     const float *xf = static_cast<const float *>(x);
     const float *yf = static_cast<const float *>(y);
+    if (dx && dy && apply_pair_supported(g, (int)C, ncomp, nb)) {
+        // both products in one grid
+        if (dx == x || dx == y) return fail(CIRCATT_ERR_INVALID, "dx must not alias x or y");
+        if (dy == x || dy == y) return fail(CIRCATT_ERR_INVALID, "dy must not alias x or y");
+        return hip_result(launch_apply_pair(dist, ncomp, g, (int)C, nb, scale, dS, xf, yf,
+                                            static_cast<float *>(dx), static_cast<float *>(dy),
+                                            as_stream(stream)),
+                          "circatt_similarity_bwd");
+    }
     if (dx) {
         if (dx == x || dx == y) return fail(CIRCATT_ERR_INVALID, "dx must not alias x or y");
         hipError_t e = launch_apply(false, dist, ncomp, g, (int)C, nb, scale, dS, yf, xf,

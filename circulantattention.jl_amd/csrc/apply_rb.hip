@@ -1217,6 +1217,18 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
     }
 }
 
+// the body for tile column t1: interior, border with 16-byte x pieces, or
+// border float by float
+template <int WS, int NCOMP, bool TRANS, bool SUMS>
+__device__ __forceinline__ void apply2_tile(const ApplyArgs &a, int pass, int t1, int c2, int b) {
+    if (t1 >= a.fa && t1 < a.fb)
+        apply2_body<WS, NCOMP, TRANS, true, SUMS>(a, pass, t1, c2, b);
+    else if (!SUMS && a.g.n1 % (4 / NCOMP) == 0)
+        apply2_body<WS, NCOMP, TRANS, false, SUMS, true>(a, pass, t1, c2, b);
+    else
+        apply2_body<WS, NCOMP, TRANS, false, SUMS, false>(a, pass, t1, c2, b);
+}
+
 // One wavefront per (64 output pixels of an image row, component pass, unit);
 // work items in XCD bands as in sim_rows_kernel.
 template <int WS, int NCOMP, bool TRANS, bool SUMS = false>
@@ -1230,12 +1242,32 @@ __global__ __launch_bounds__(64, 2) void apply2_kernel(ApplyArgs a, int nwork) {
     it /= a.tiles1;
     const int c2 = __builtin_amdgcn_readfirstlane(it % a.g.n2);
     const int b = __builtin_amdgcn_readfirstlane(it / a.g.n2);
-    if (t1 >= a.fa && t1 < a.fb)
-        apply2_body<WS, NCOMP, TRANS, true, SUMS>(a, pass, t1, c2, b);
-    else if (!SUMS && a.g.n1 % (4 / NCOMP) == 0)
-        apply2_body<WS, NCOMP, TRANS, false, SUMS, true>(a, pass, t1, c2, b);
+    apply2_tile<WS, NCOMP, TRANS, SUMS>(a, pass, t1, c2, b);
+}
+
+// The similarity pullback's two products in one grid: work items
+// [0, nwork) are A ⊗ y (args af), [nwork, 2 nwork) are Aᵀ ⊗ x (args at), each
+// half in XCD bands, so that the two share the GPU instead of running one
+// after the other.
+template <int WS, int NCOMP>
+__global__ __launch_bounds__(64, 2) void apply2_pair_kernel(ApplyArgs af, ApplyArgs at, int nwork) {
+    const int nall = 2 * nwork;
+    const int nper = (nall + 7) >> 3;
+    int it = (int)(blockIdx.x & 7) * nper + (int)(blockIdx.x >> 3);
+    if (it >= nall) return;
+    const bool trans = it >= nwork;
+    if (trans) it -= nwork;
+    const ApplyArgs &a = trans ? at : af;
+    const int pass = __builtin_amdgcn_readfirstlane(it % a.gchunk);
+    it /= a.gchunk;
+    const int t1 = __builtin_amdgcn_readfirstlane(it % a.tiles1);
+    it /= a.tiles1;
+    const int c2 = __builtin_amdgcn_readfirstlane(it % a.g.n2);
+    const int b = __builtin_amdgcn_readfirstlane(it / a.g.n2);
+    if (trans)
+        apply2_tile<WS, NCOMP, true, false>(at, pass, t1, c2, b);
     else
-        apply2_body<WS, NCOMP, TRANS, false, SUMS, false>(a, pass, t1, c2, b);
+        apply2_tile<WS, NCOMP, false, false>(af, pass, t1, c2, b);
 }
 
 // ---------------------------------------------------------------------------
@@ -1650,6 +1682,45 @@ hipError_t launch_rb(ApplyArgs a, int64_t nb, hipStream_t s) {
     return hipGetLastError();
 }
 
+// geometry fields of the 2D row kernel (segments, interior range, passes)
+template <int WS, int NCOMP, bool TRANS>
+void set_rows2(ApplyArgs &a) {
+    using S = A2<WS, NCOMP, TRANS>;
+    a.tiles1 = (a.g.n1 + 63) / 64;
+    a.fa = (S::EDGE + 63) / 64;
+    a.fb = a.g.n1 - 64 - S::EDGE >= 0 ? (a.g.n1 - 64 - S::EDGE) / 64 + 1 : 0;
+    if (a.fb > a.tiles1) a.fb = a.tiles1;
+    if (a.fb < a.fa) a.fb = a.fa;
+    a.gchunk = (NCOMP * a.C + kCPass - 1) / kCPass;
+}
+
+template <int WS, int NCOMP>
+hipError_t launch_pair_t(ApplyArgs f, ApplyArgs t, int64_t nb, hipStream_t s) {
+    set_rows2<WS, NCOMP, false>(f);
+    set_rows2<WS, NCOMP, true>(t);
+    const int64_t nwork = (int64_t)f.tiles1 * f.g.n2 * nb * f.gchunk;
+    const int64_t grid = 8 * ((2 * nwork + 7) / 8);
+    const size_t lds = (size_t)std::max(A2<WS, NCOMP, false>::LDS, A2<WS, NCOMP, true>::LDS) *
+                       sizeof(float);
+    hipLaunchKernelGGL((apply2_pair_kernel<WS, NCOMP>), dim3((unsigned)grid), dim3(64), lds, s, f,
+                       t, (int)nwork);
+    return hipGetLastError();
+}
+
+template <int NCOMP>
+hipError_t dispatch_pair(const ApplyArgs &f, const ApplyArgs &t, int64_t nb, hipStream_t s) {
+    switch (f.g.ws) {
+        case 3: return launch_pair_t<3, NCOMP>(f, t, nb, s);
+        case 5: return launch_pair_t<5, NCOMP>(f, t, nb, s);
+        case 7: return launch_pair_t<7, NCOMP>(f, t, nb, s);
+        case 9: return launch_pair_t<9, NCOMP>(f, t, nb, s);
+        case 11: return launch_pair_t<11, NCOMP>(f, t, nb, s);
+        case 13: return launch_pair_t<13, NCOMP>(f, t, nb, s);
+        case 15: return launch_pair_t<15, NCOMP>(f, t, nb, s);
+        default: return hipErrorNotSupported;
+    }
+}
+
 template <int NCOMP, bool TRANS>
 hipError_t dispatch_ws(const ApplyArgs &a, int64_t nb, hipStream_t s) {
     switch (a.g.ws) {
@@ -1843,6 +1914,32 @@ hipError_t launch_apply_wide(bool trans, bool corr, int ncomp, const Geom &g, in
     if (ncomp == 1)
         return trans ? launch_wide<1, true, false>(a, nb, s) : launch_wide<1, false, false>(a, nb, s);
     return trans ? launch_wide<2, true, false>(a, nb, s) : launch_wide<2, false, false>(a, nb, s);
+}
+
+bool apply_pair_supported(const Geom &g, int C, int ncomp, int64_t nb) {
+    if (g.nsp != 2 || !apply_rb_supported(g, C, ncomp, nb)) return false;
+    const int64_t nwork = (int64_t)((g.n1 + 63) / 64) * g.n2 * nb *
+                          ((ncomp * C + kCPass - 1) / kCPass);
+    return 2 * nwork + 8 < ((int64_t)1 << 31);
+}
+
+hipError_t launch_apply_pair(bool corr, int ncomp, const Geom &g, int C, int64_t nb, float scale,
+                             const float *nz, const float *x, const float *y, float *dx,
+                             float *dy, hipStream_t s) {
+    // dx = A ⊗ y (- rowsum(A) .* x), dy = Aᵀ ⊗ x (- colsum(A) .* y)
+    ApplyArgs f{}, t{};
+    f.g = t.g = g;
+    f.C = t.C = C;
+    f.corr = t.corr = corr ? 1 : 0;
+    f.scale = t.scale = scale;
+    f.nz = t.nz = nz;
+    f.x = y;
+    f.z = x;
+    f.y = dx;
+    t.x = x;
+    t.z = y;
+    t.y = dy;
+    return ncomp == 1 ? dispatch_pair<1>(f, t, nb, s) : dispatch_pair<2>(f, t, nb, s);
 }
 
 hipError_t launch_colsum_wide(const Geom &g, int64_t nb, const float *nz, float *out,

@@ -35,6 +35,12 @@ hipError_t launch_apply_wide(bool trans, bool corr, int ncomp, const Geom &g, in
                              hipStream_t s);
 hipError_t launch_colsum_wide(const Geom &g, int64_t nb, const float *nz, float *out,
                               hipStream_t s);
+// The similarity pullback's two products (2D, ws <= 15) in one grid:
+// dx = A ⊗ y, dy = Aᵀ ⊗ x, with the Distance terms when corr.
+bool apply_pair_supported(const Geom &g, int C, int ncomp, int64_t nb);
+hipError_t launch_apply_pair(bool corr, int ncomp, const Geom &g, int C, int64_t nb, float scale,
+                             const float *nz, const float *x, const float *y, float *dx,
+                             float *dy, hipStream_t s);
 // Similarity for windows of any odd width in 1D and 2D (sub-row tasks).
 bool sim_wide_supported(const Geom &g, int C, int ncomp, int64_t nb);
 hipError_t launch_sim_wide(bool dist, int ncomp, const Geom &g, int C, int64_t nb, float scale,
