@@ -1607,30 +1607,60 @@ __device__ __forceinline__ void apply_wide_body(const ApplyArgs &a, int pass, in
     }
 }
 
-// One wavefront per (64 output pixels of an image row or of the line,
-// component pass, unit); work items in XCD bands.
-template <int NCOMP, bool TRANS, bool SUMS>
-__global__ __launch_bounds__(64, 2) void apply_wide_kernel(ApplyArgs a, int nwork) {
-    const int nper = (nwork + 7) >> 3;
-    int it = (int)(blockIdx.x & 7) * nper + (int)(blockIdx.x >> 3);
-    if (it >= nwork) return;
-    const int pass = __builtin_amdgcn_readfirstlane(it % a.gchunk);
+// work item it (XCD-banded) -> (pass, tile column, image row, unit)
+__device__ __forceinline__ void wide_item(const ApplyArgs &a, int it, int &pass, int &t1, int &c2,
+                                          int &b) {
+    pass = __builtin_amdgcn_readfirstlane(it % a.gchunk);
     it /= a.gchunk;
-    const int t1 = __builtin_amdgcn_readfirstlane(it % a.tiles1);
+    t1 = __builtin_amdgcn_readfirstlane(it % a.tiles1);
     it /= a.tiles1;
     const int n2 = a.g.nsp == 2 ? a.g.n2 : 1;
-    const int c2 = __builtin_amdgcn_readfirstlane(it % n2);
-    const int b = __builtin_amdgcn_readfirstlane(it / n2);
+    c2 = __builtin_amdgcn_readfirstlane(it % n2);
+    b = __builtin_amdgcn_readfirstlane(it / n2);
+}
+template <int NCOMP, bool TRANS, bool SUMS>
+__device__ __forceinline__ void apply_wide_tile(const ApplyArgs &a, int pass, int t1, int c2,
+                                                int b) {
     if (t1 >= a.fa && t1 < a.fb)
         apply_wide_body<NCOMP, TRANS, true, SUMS>(a, pass, t1, c2, b);
     else
         apply_wide_body<NCOMP, TRANS, false, SUMS>(a, pass, t1, c2, b);
 }
 
+// One wavefront per (64 output pixels of an image row or of the line,
+// component pass, unit); work items in XCD bands.
 template <int NCOMP, bool TRANS, bool SUMS>
-hipError_t launch_wide(ApplyArgs a, int64_t nb, hipStream_t s) {
-    using S = AW<NCOMP, TRANS>;
-    const int n1 = a.g.n1, n2 = a.g.nsp == 2 ? a.g.n2 : 1;
+__global__ __launch_bounds__(64, 2) void apply_wide_kernel(ApplyArgs a, int nwork) {
+    const int nper = (nwork + 7) >> 3;
+    const int it = (int)(blockIdx.x & 7) * nper + (int)(blockIdx.x >> 3);
+    if (it >= nwork) return;
+    int pass, t1, c2, b;
+    wide_item(a, it, pass, t1, c2, b);
+    apply_wide_tile<NCOMP, TRANS, SUMS>(a, pass, t1, c2, b);
+}
+
+// The similarity pullback's two products in one grid (as apply2_pair_kernel)
+template <int NCOMP>
+__global__ __launch_bounds__(64, 2) void apply_wide_pair_kernel(ApplyArgs af, ApplyArgs at,
+                                                                int nwork) {
+    const int nall = 2 * nwork;
+    const int nper = (nall + 7) >> 3;
+    int it = (int)(blockIdx.x & 7) * nper + (int)(blockIdx.x >> 3);
+    if (it >= nall) return;
+    const bool trans = it >= nwork;
+    if (trans) it -= nwork;
+    int pass, t1, c2, b;
+    wide_item(trans ? at : af, it, pass, t1, c2, b);
+    if (trans)
+        apply_wide_tile<NCOMP, true, false>(at, pass, t1, c2, b);
+    else
+        apply_wide_tile<NCOMP, false, false>(af, pass, t1, c2, b);
+}
+
+// geometry fields of the wide kernel (segments, interior range, passes)
+template <int NCOMP, bool SUMS>
+void set_wide(ApplyArgs &a) {
+    const int n1 = a.g.n1;
     a.tiles1 = (n1 + 63) / 64;
     // interior segments: staged sub-chunk and x columns in range, no slot
     // shift (2p + kJC columns of margin on either side)
@@ -1640,6 +1670,25 @@ hipError_t launch_wide(ApplyArgs a, int64_t nb, hipStream_t s) {
     if (a.fb > a.tiles1) a.fb = a.tiles1;
     if (a.fb < a.fa) a.fb = a.fa;
     a.gchunk = SUMS ? 1 : (NCOMP * a.C + kCPass - 1) / kCPass;
+}
+
+template <int NCOMP>
+hipError_t launch_wide_pair(ApplyArgs af, ApplyArgs at, int64_t nb, hipStream_t s) {
+    set_wide<NCOMP, false>(af);
+    set_wide<NCOMP, false>(at);
+    const int64_t nwork = (int64_t)af.tiles1 * (af.g.nsp == 2 ? af.g.n2 : 1) * nb * af.gchunk;
+    const size_t lds =
+        (size_t)std::max(AW<NCOMP, false>::LDS, AW<NCOMP, true>::LDS) * sizeof(float);
+    hipLaunchKernelGGL((apply_wide_pair_kernel<NCOMP>), dim3((unsigned)(8 * ((2 * nwork + 7) / 8))),
+                       dim3(64), lds, s, af, at, (int)nwork);
+    return hipGetLastError();
+}
+
+template <int NCOMP, bool TRANS, bool SUMS>
+hipError_t launch_wide(ApplyArgs a, int64_t nb, hipStream_t s) {
+    using S = AW<NCOMP, TRANS>;
+    const int n2 = a.g.nsp == 2 ? a.g.n2 : 1;
+    set_wide<NCOMP, SUMS>(a);
     const int64_t nwork = (int64_t)a.tiles1 * n2 * nb * a.gchunk;
     const size_t lds = (size_t)(SUMS ? S::LDS_SUMS : S::LDS) * sizeof(float);
     hipLaunchKernelGGL((apply_wide_kernel<NCOMP, TRANS, SUMS>), dim3((unsigned)(8 * ((nwork + 7) / 8))),
@@ -1916,9 +1965,17 @@ hipError_t launch_apply_wide(bool trans, bool corr, int ncomp, const Geom &g, in
     return trans ? launch_wide<2, true, false>(a, nb, s) : launch_wide<2, false, false>(a, nb, s);
 }
 
+// the pair goes to the 2D row kernel (ws <= 15) or the wide kernel (ws > 15)
+static bool pair_rows(const Geom &g, int C, int ncomp, int64_t nb) {
+    return g.nsp == 2 && apply_rb_supported(g, C, ncomp, nb);
+}
+static bool pair_wide(const Geom &g, int C, int ncomp, int64_t nb) {
+    return !apply_rb_supported(g, C, ncomp, nb) && apply_wide_supported(g, C, ncomp, nb);
+}
 bool apply_pair_supported(const Geom &g, int C, int ncomp, int64_t nb) {
-    if (g.nsp != 2 || !apply_rb_supported(g, C, ncomp, nb)) return false;
-    const int64_t nwork = (int64_t)((g.n1 + 63) / 64) * g.n2 * nb *
+    if (!pair_rows(g, C, ncomp, nb) && !pair_wide(g, C, ncomp, nb)) return false;
+    const int64_t n2 = g.nsp == 2 ? g.n2 : 1;
+    const int64_t nwork = (int64_t)((g.n1 + 63) / 64) * n2 * nb *
                           ((ncomp * C + kCPass - 1) / kCPass);
     return 2 * nwork + 8 < ((int64_t)1 << 31);
 }
@@ -1939,7 +1996,9 @@ hipError_t launch_apply_pair(bool corr, int ncomp, const Geom &g, int C, int64_t
     t.x = x;
     t.z = y;
     t.y = dy;
-    return ncomp == 1 ? dispatch_pair<1>(f, t, nb, s) : dispatch_pair<2>(f, t, nb, s);
+    if (pair_rows(g, C, ncomp, nb))
+        return ncomp == 1 ? dispatch_pair<1>(f, t, nb, s) : dispatch_pair<2>(f, t, nb, s);
+    return ncomp == 1 ? launch_wide_pair<1>(f, t, nb, s) : launch_wide_pair<2>(f, t, nb, s);
 }
 
 hipError_t launch_colsum_wide(const Geom &g, int64_t nb, const float *nz, float *out,

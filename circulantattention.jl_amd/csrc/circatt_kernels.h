@@ -35,7 +35,8 @@ hipError_t launch_apply_wide(bool trans, bool corr, int ncomp, const Geom &g, in
                              hipStream_t s);
 hipError_t launch_colsum_wide(const Geom &g, int64_t nb, const float *nz, float *out,
                               hipStream_t s);
-// The similarity pullback's two products (2D, ws <= 15) in one grid:
+// The similarity pullback's two products in one grid (2D windows up to 15,
+// and windows past 15 in 1D and 2D):
 // dx = A ⊗ y, dy = Aᵀ ⊗ x, with the Distance terms when corr.
 bool apply_pair_supported(const Geom &g, int C, int ncomp, int64_t nb);
 hipError_t launch_apply_pair(bool corr, int ncomp, const Geom &g, int C, int64_t nb, float scale,
