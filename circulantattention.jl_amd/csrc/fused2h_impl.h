@@ -181,9 +181,15 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     constexpr int CHP = (NPAIR + NCH - 1) / NCH;
     // pair at which the next item's loads are issued (the forward issues them
     // in its apply walk; with two chunks, at the last pair of the first, so
-    // that the loads are in flight over the whole second chunk)
+    // that the loads are in flight over the whole second chunk).  Backward:
+    // pair NPAIR / PFD; measured on gfx950, the query-centric pass is fastest
+    // with its loads issued at a quarter of the walk (200 against 205 us at
+    // cfg3), the key-centric pass at half of it
 #ifndef CIRCATT_F2H_BWD_PFD
 #define CIRCATT_F2H_BWD_PFD 2
+#endif
+#ifndef CIRCATT_F2H_BWDQ_PFD
+#define CIRCATT_F2H_BWDQ_PFD 4
 #endif
 #ifndef CIRCATT_F2H_BWD_FSTEP
 #define CIRCATT_F2H_BWD_FSTEP 1
@@ -191,7 +197,11 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     // forward with a reference maximum from the central block row (rows 8, 9
     // of the key region lie in every query's window when 2P >= 9)
     constexpr bool STREAM = MODE == FWD && NKW == 2 && P >= 5;
-    constexpr int PFP = STREAM ? 1 : (MODE == FWD && NCH == 2) ? CHP - 1 : NPAIR / CIRCATT_F2H_BWD_PFD;
+    constexpr int PFP = STREAM                    ? 1
+                        : (MODE == FWD && NCH == 2) ? CHP - 1
+                        : MODE == BWDQ              ? NPAIR / CIRCATT_F2H_BWDQ_PFD
+                                                    : NPAIR / CIRCATT_F2H_BWD_PFD;
+    static_assert(PFP >= 0 && PFP < NPAIR, "the next item's loads must be issued in the walk");
     static_assert(NPX <= 1024, "one staged pixel per thread");
     static_assert(HH % 2 == 0, "row pairs");
     char *const lds = reinterpret_cast<char *>(circatt_lds2);
