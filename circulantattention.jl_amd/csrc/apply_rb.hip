@@ -373,14 +373,18 @@ __device__ __forceinline__ void wait_vm() {
 // ---------------------------------------------------------------------------
 constexpr int kHalo = 8;  // staged key columns beyond each side (>= p)
 constexpr int kJC = 16;   // window columns per sub-row (windows wider than 15)
-template <int NCOMP>
+template <int NCOMP, int CP = 1>
 struct SimStage {
+    // CP channels per step (the row kernel pairs real channels, so that a
+    // step stages and multiplies as much as one complex channel)
     static constexpr int RW = 64 + 2 * kHalo;  // staged key columns per row
-    static constexpr int RF = NCOMP * RW;      // floats per key row
+    static constexpr int CR = NCOMP * RW;      // floats per key row and channel
+    static constexpr int RF = CP * CR;         // floats per key row
     static constexpr int KF = 4 * RF;          // key floats
     static constexpr int KS = KF / 4;          // key pieces
     static constexpr int KL = (KS + 63) / 64;  // 16-byte key loads per lane
-    static constexpr int QF = NCOMP * 64;      // query floats
+    static constexpr int QC = NCOMP * 64;      // query floats per channel
+    static constexpr int QF = CP * QC;         // query floats
     static constexpr int QS = QF / 4;          // query pieces (<= 64)
     static constexpr int QOFF = KL * 256;      // query area (floats)
     static constexpr int SB = QOFF + 256;      // floats per ring buffer
@@ -392,7 +396,8 @@ struct SimStage {
 // a multiple of the 4 / NCOMP pixels of a piece); otherwise float by float.
 template <int WS, int NCOMP, bool DIST, bool FAST, bool XV = FAST>
 __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int c2, int b) {
-    using S = SimStage<NCOMP>;
+    constexpr int CP = NCOMP == 1 ? 2 : 1;  // channels per step
+    using S = SimStage<NCOMP, CP>;
     constexpr int P = (WS - 1) / 2;
     constexpr int K = WS * WS;
     constexpr int XW = kR + 2 * P;
@@ -423,18 +428,20 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
     for (int i = 0; i < kR; ++i) s1[i] = FAST ? 0 : shift0(pmod(f1 + 4 * l16 + i, n1), n1, P);
     const int s2 = slot_shift(c2 + 1, n2, P);
     const int plane = (int)(NCOMP * Pp * 4);  // bytes per channel
-    // query offsets (the lane's piece, or float, of the 64 query pixels)
+    // query offsets (the lane's piece, or float, of the 64 query pixels of
+    // channel h of the step)
     int qo[NQ];
 #pragma unroll
     for (int m = 0; m < NQ; ++m) {
-        if (XV) {
-            const int u = 4 * min(lane, S::QS - 1) / NCOMP;
-            qo[m] = NCOMP * (n1 * c2 + (FAST ? f1 + u : pmod(f1 + u, n1))) * 4;
-        } else {
-            const int f = lane + 64 * m, u = f / NCOMP, e = f - u * NCOMP;
-            qo[m] = (NCOMP * (n1 * c2 + pmod(f1 + u, n1)) + e) * 4;
-        }
+        const int f = XV ? 4 * min(lane, S::QS - 1) : lane + 64 * m;
+        const int h = f / S::QC, w = f - h * S::QC;
+        const int u = w / NCOMP, e = w - u * NCOMP;  // (e = 0 for a piece)
+        const int col = FAST ? f1 + u : pmod(f1 + u, n1);
+        qo[m] = h * plane + (NCOMP * (n1 * c2 + col) + e) * 4;
     }
+    // steps of CP channels; a second channel past C lies past the unit's
+    // bytes and reads as zeros, which add nothing to either similarity
+    const int nst = (a.C + CP - 1) / CP;
 
     // window-row iterations [gc * ichunk, ...) of this wavefront
     const int it1 = min(NIT, (gc + 1) * a.ichunk);
@@ -448,14 +455,17 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
 #pragma unroll
         for (int m = 0; m < NK; ++m) {
             const int f = XV ? 4 * min(lane + 64 * m, S::KS - 1) : lane + 64 * m;
-            const int rr = f / S::RF, w = f - rr * S::RF;
+            const int rr = f / S::RF, rf = f - rr * S::RF;
+            const int h = rf / S::CR, w = rf - h * S::CR;
             const int kr2 = pmod(c2 + min(4 * itr + rr, WS - 1) - P, n2);
             const int u = w / NCOMP, e = w - u * NCOMP;  // (e = 0 for a piece)
             const int col = FAST ? f1 - kHalo + u : pmod(f1 - kHalo + u, n1);
-            ko[m] = (NCOMP * (n1 * kr2 + col) + e) * 4;
+            ko[m] = h * plane + (NCOMP * (n1 * kr2 + col) + e) * 4;
         }
+        // step c: channels c CP ..; the whole offset is in the vector
+        // operand, which the range check sees
         auto stage = [&](int c, int buf) {
-            const int cb = __builtin_amdgcn_readfirstlane(c * plane);
+            const int cb = __builtin_amdgcn_readfirstlane(c * CP * plane);
             float *dst = lw + buf * S::SB;
 #pragma unroll
             for (int m = 0; m < NK; ++m) {
@@ -465,10 +475,10 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
                     // every instruction is active, so each is issued)
                     if (lane + 64 * m < S::KS)
                         __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lptr)(dst + 256 * m), 16,
-                                                                ko[m], cb, 0, 0);
+                                                                ko[m] + cb, 0, 0, 0);
                 } else {
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lptr)(dst + 64 * m), 4, ko[m],
-                                                            cb, 0, 0);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lptr)(dst + 64 * m), 4,
+                                                            ko[m] + cb, 0, 0, 0);
                 }
             }
 #pragma unroll
@@ -477,10 +487,10 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
                 if (XV) {
                     if (lane < S::QS)
                         __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lptr)(dst + S::QOFF), 16,
-                                                                qo[m], cb, 0, 0);
+                                                                qo[m] + cb, 0, 0, 0);
                 } else {
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lptr)(dst + S::QOFF + 64 * m), 4,
-                                                            qo[m], cb, 0, 0);
+                                                            qo[m] + cb, 0, 0, 0);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -494,51 +504,55 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
         // the previous iteration's reads of the LDS area are complete
         __builtin_amdgcn_s_waitcnt(kWaitLgkm);
         stage(0, 0);
-        if (a.C > 1) stage(1, 1);
+        if (nst > 1) stage(1, 1);
         int cur = 0;
 #pragma unroll 1
-        for (int c = 0; c < a.C; ++c) {
-            // loads issued after channel c's: channel c + 1's
-            if (c + 1 < a.C)
+        for (int c = 0; c < nst; ++c) {
+            // loads issued after step c's: step c + 1's
+            if (c + 1 < nst)
                 wait_vm<NI>();
             else
                 wait_vm<0>();
-            // the buffer refilled here was read for channel c - 1
+            // the buffer refilled here was read for step c - 1
             __builtin_amdgcn_s_waitcnt(kWaitLgkm);
-            if (c + 2 < a.C) stage(c + 2, cur == 0 ? 2 : cur - 1);
+            if (c + 2 < nst) stage(c + 2, cur == 0 ? 2 : cur - 1);
             const float *sb = lw + cur * S::SB;
-            float q[4 * NCOMP], kw[4 * KW4];
 #pragma unroll
-            for (int h = 0; h < NCOMP; ++h) {
-                const f4 v = *(const f4 *)(sb + S::QOFF + NCOMP * 4 * l16 + 4 * h);
-                q[4 * h] = v[0];
-                q[4 * h + 1] = v[1];
-                q[4 * h + 2] = v[2];
-                q[4 * h + 3] = v[3];
-            }
-            const float *kr = sb + rho * S::RF + NCOMP * (4 * l16 + kHalo - P) - AL;
+            for (int hc = 0; hc < CP; ++hc) {
+                float q[4 * NCOMP], kw[4 * KW4];
 #pragma unroll
-            for (int h = 0; h < KW4; ++h) {
-                const f4 v = *(const f4 *)(kr + 4 * h);
-                kw[4 * h] = v[0];
-                kw[4 * h + 1] = v[1];
-                kw[4 * h + 2] = v[2];
-                kw[4 * h + 3] = v[3];
-            }
+                for (int h = 0; h < NCOMP; ++h) {
+                    const f4 v = *(const f4 *)(sb + S::QOFF + hc * S::QC + NCOMP * 4 * l16 + 4 * h);
+                    q[4 * h] = v[0];
+                    q[4 * h + 1] = v[1];
+                    q[4 * h + 2] = v[2];
+                    q[4 * h + 3] = v[3];
+                }
+                const float *kr =
+                    sb + rho * S::RF + hc * S::CR + NCOMP * (4 * l16 + kHalo - P) - AL;
 #pragma unroll
-            for (int i = 0; i < kR; ++i)
+                for (int h = 0; h < KW4; ++h) {
+                    const f4 v = *(const f4 *)(kr + 4 * h);
+                    kw[4 * h] = v[0];
+                    kw[4 * h + 1] = v[1];
+                    kw[4 * h + 2] = v[2];
+                    kw[4 * h + 3] = v[3];
+                }
 #pragma unroll
-                for (int j = 0; j < WS; ++j)
+                for (int i = 0; i < kR; ++i)
 #pragma unroll
-                    for (int e = 0; e < NCOMP; ++e) {
-                        const float xv = q[NCOMP * i + e], yv = kw[AL + NCOMP * (i + j) + e];
-                        if (DIST) {
-                            const float d = xv - yv;
-                            acc[i][j] = __builtin_fmaf(d, d, acc[i][j]);
-                        } else {
-                            acc[i][j] = __builtin_fmaf(xv, yv, acc[i][j]);
+                    for (int j = 0; j < WS; ++j)
+#pragma unroll
+                        for (int e = 0; e < NCOMP; ++e) {
+                            const float xv = q[NCOMP * i + e], yv = kw[AL + NCOMP * (i + j) + e];
+                            if (DIST) {
+                                const float d = xv - yv;
+                                acc[i][j] = __builtin_fmaf(d, d, acc[i][j]);
+                            } else {
+                                acc[i][j] = __builtin_fmaf(xv, yv, acc[i][j]);
+                            }
                         }
-                    }
+            }
             cur = cur == S::NR - 1 ? 0 : cur + 1;
         }
         // (the ring area is rewritten below: its last reads are complete, as
@@ -1838,7 +1852,8 @@ hipError_t launch_sim_t(ApplyArgs a, int64_t nb, hipStream_t s) {
     // results before they are stored (skewed by 4 floats per 4 pixels, plus
     // the 16 floats that the last pixel's 16 lanes read past its 4 ws)
     const size_t lds =
-        (size_t)std::max(SimStage<NCOMP>::NR * SimStage<NCOMP>::SB, 64 * 4 * WS + 64 + 64) *
+        (size_t)std::max(SimStage<NCOMP, NCOMP == 1 ? 2 : 1>::NR * SimStage<NCOMP, NCOMP == 1 ? 2 : 1>::SB,
+                         64 * 4 * WS + 64 + 64) *
         sizeof(float);
     hipLaunchKernelGGL((sim_rows_kernel<WS, NCOMP, DIST>), dim3((unsigned)grid), dim3(64), lds, s,
                        a, (int)nwork);

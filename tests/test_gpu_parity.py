@@ -90,7 +90,9 @@ SIM_CASES = [((8,), 5, 4), ((8, 8), 5, 4), ((12, 10), 3, 8), ((32, 32), 7, 16), 
              ((2,), 5, 3), ((20, 13), 15, 64), ((9, 7), 3, 80), ((70,), 63, 32),
              # windows past 15 (sub-row kernel), with and without interior segments
              ((70, 40), 31, 8), ((160, 6), 17, 4), ((700,), 63, 4), ((37, 9), 19, 3),
-             ((10, 40), 17, 3), ((40,), 63, 2)]
+             ((10, 40), 17, 3), ((40,), 63, 2),
+             # odd channel counts (the row kernel stages real channels in pairs)
+             ((12, 10), 5, 7), ((200, 4), 9, 3)]
 
 
 @pytest.mark.parametrize("dims,ws,C", SIM_CASES)
