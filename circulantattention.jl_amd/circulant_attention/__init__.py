@@ -10,14 +10,16 @@ Julia name              -> here
                         -> same names
   ⊗, ⨷                  -> otimes (also ``A @ x``), Otimes
   NNlib.softmax(!)      -> softmax(_)
-  CirculantAttention.scale, sum(A; dims), +, -, *
-                        -> scale, Circulant.sum, operators
+  CirculantAttention.scale, sum(A; dims), +, -, *, ==, dot
+                        -> scale, Circulant.sum, operators, Circulant.dot
+  cat(As...; dims), repeat(A, counts...)
+                        -> cat, Circulant.repeat
 Gradients flow through torch.autograd with the reference's rrules
 (src/rrules.jl); Zygote.accum's role is played by autograd accumulation.
 """
 from . import _lib
 from .circulant import (AbstractSimilarity, Circulant, DistanceSimilarity, DotSimilarity, Otimes,
-                        circulant, circulant_adjacency, circulant_adjacency_, circulant_attention,
+                        cat, circulant, circulant_adjacency, circulant_adjacency_, circulant_attention,
                         circulant_mh_adjacency, circulant_mh_attention,
                         circulant_mh_transposed_attention, circulant_similarity,
                         circulant_similarity_, circulant_transposed_attention, otimes, scale,
@@ -27,7 +29,7 @@ Circulant.__matmul__ = lambda A, x: otimes(A, x)
 
 __all__ = [
     "AbstractSimilarity", "Circulant", "DistanceSimilarity", "DotSimilarity", "Otimes",
-    "circulant", "circulant_adjacency", "circulant_adjacency_", "circulant_attention",
+    "cat", "circulant", "circulant_adjacency", "circulant_adjacency_", "circulant_attention",
     "circulant_mh_adjacency", "circulant_mh_attention", "circulant_mh_transposed_attention",
     "circulant_similarity", "circulant_similarity_", "circulant_transposed_attention", "otimes",
     "scale", "softmax", "softmax_",

@@ -191,6 +191,32 @@ class Circulant:
         nz = self.nzval.reshape(*reversed(batch), self.P, self.K)
         return Circulant(nz, self.kernel_length, self.spatial_size)
 
+    def repeat(self, *counts):
+        """repeat(A, 1, 1, n3, n4, ...) (src/array.jl:49-52, the same call
+        that replicates the pattern over the batch at src/array.jl:9): tiles
+        the batch dims; the two (P, P) dims cannot be repeated."""
+        counts = [int(c) for c in counts]
+        if len(counts) < 2 or counts[0] != 1 or counts[1] != 1:
+            raise AssertionError("repeat(A, 1, 1, counts...): the (P, P) dims of a Circulant "
+                                 "cannot be repeated")
+        batch = list(self.batch) + [1] * max(0, len(counts) - 2 - len(self.batch))
+        reps = counts[2:] + [1] * (len(batch) - len(counts[2:]))
+        nz = self.nzval.reshape(*reversed(batch), self.P, self.K)
+        return Circulant(nz.repeat(*reversed(reps), 1, 1), self.kernel_length, self.spatial_size)
+
+    def __eq__(self, other):
+        """A == B (src/array.jl:101-115): sizes, spatial size, kernel length
+        and the CSR data.  rowPtr and colVal are a function of (spatial size,
+        kernel length), so equal metadata means equal indices and only nzVal
+        is compared."""
+        if not isinstance(other, Circulant):
+            return NotImplemented
+        return (self.size() == other.size() and self.spatial_size == other.spatial_size
+                and self.kernel_length == other.kernel_length
+                and torch.equal(self.nzval, other.nzval))
+
+    __hash__ = None
+
     def copy(self):
         return Circulant(self.nzval.clone(), self.kernel_length, self.spatial_size)
 
@@ -310,6 +336,40 @@ class CirculantSum(torch.autograd.Function):
 # ---------------------------------------------------------------------------
 # API (src/similarity.jl, src/attention.jl)
 # ---------------------------------------------------------------------------
+
+def cat(*As: Circulant, dims: int = 3) -> Circulant:
+    """cat(As...; dims=3) (src/array.jl:62-64): concatenate along a batch
+    dim (Julia dim >= 3), e.g. cat(A, B; dims=3) gives (P, P, 2nheads, B)
+    (README.md:145-148).  The reference body names the array type instead of
+    a Circulant for the spatial size (`spatial_size(A)` with A the type
+    parameter) and so throws; here the first argument's spatial size and
+    kernel length are used, and all arguments must share them."""
+    if not As:
+        raise AssertionError("cat needs at least one Circulant")
+    A0 = As[0]
+    dims = int(dims)
+    if dims < 3:
+        raise AssertionError("Circulants concatenate along batch dims (dims >= 3) only")
+    for A in As:
+        if not isinstance(A, Circulant):
+            raise AssertionError("cat concatenates Circulants")
+        if A.kernel_length != A0.kernel_length or A.spatial_size != A0.spatial_size:
+            raise AssertionError("cat needs equal kernel length and spatial size")
+    nd = max(dims - 2, max(len(A.batch) for A in As))
+
+    def padded(A):
+        b = list(A.batch) + [1] * (nd - len(A.batch))
+        return A.nzval.reshape(*reversed(b), A.P, A.K), b
+
+    parts = [padded(A) for A in As]
+    ax = dims - 3                      # Julia batch dim -> index into Julia-order batch
+    for _, b in parts[1:]:
+        if [d for i, d in enumerate(b) if i != ax] != \
+                [d for i, d in enumerate(parts[0][1]) if i != ax]:
+            raise AssertionError("cat: batch dims other than `dims` must match")
+    nz = torch.cat([p for p, _ in parts], dim=nd - 1 - ax)
+    return Circulant(nz, A0.kernel_length, A0.spatial_size)
+
 
 def circulant(M: int, x: torch.Tensor) -> Circulant:
     """circulant(M, x): Float32 Circulant of x's spatial size with batch

@@ -365,6 +365,29 @@ def test_composition_cfg5_style(ca, cuda):
     assert rel_err(host(s3.nzval).reshape(Bb, -1), ref3) < TOL_FWD
 
 
+def test_cat_heads_then_otimes(ca, cuda):
+    """README.md:145-148: D = cat(A, B; dims=3) has 2·nheads heads; D ⨷ w
+    splits w into 2·nheads heads and applies head g's matrix to it."""
+    dims, ws, Cc, Bb, nh = (12, 10), 5, 16, 2, 2
+    shape = shape_of(dims, Cc, Bb)
+    q, k, v, w = (seeded(700 + i, shape) for i in range(4))
+    tq, tk, tv = (dev(a, cuda) for a in (q, k, v))
+    _, A = ca.circulant_mh_attention(ca.DotSimilarity(), tq, tk, tv, ws, nh)
+    _, Bm = ca.circulant_mh_attention(ca.DotSimilarity(), tv, tq, tk, ws, nh)
+    D = ca.cat(A, Bm, dims=3)
+    P = int(np.prod(dims))
+    assert D.size() == (P, P, 2 * nh, Bb)
+    assert D == ca.cat(A, Bm, dims=3) and not (D == ca.cat(Bm, A, dims=3))
+    z = ca.Otimes(D, dev(w, cuda))
+    _, Ar = O.attention_fwd(0, q, k, v, ws, nh)
+    _, Br = O.attention_fwd(0, v, q, k, ws, nh)
+    K = ws ** len(dims)
+    Dr = np.concatenate([Ar.reshape(Bb, nh, P * K), Br.reshape(Bb, nh, P * K)], axis=1)
+    zr = O.apply(Dr.reshape(Bb * 2 * nh, P * K), w.reshape(Bb * 2 * nh, Cc // (2 * nh), P),
+                 dims, ws).reshape(shape)
+    assert rel_err(host(z), zr) < TOL_FWD
+
+
 def test_scale_rrule(ca, cuda):
     """test/rrule.jl:22 scale(a, A) with a (1,1,2,2) against A (P,P,1,2):
     broadcast over the batch dims; gradients by the rrule of src/rrules.jl:94-114."""

@@ -1,0 +1,75 @@
+"""Host logic of the Circulant batch utilities: cat (src/array.jl:62-64,
+README.md:145-148), repeat (src/array.jl:49-52) and == (src/array.jl:101-115).
+They move nzVal between batch slots only, so the expected values are written
+out slot by slot."""
+import pytest
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ca():
+    import circulant_attention
+    return circulant_attention
+
+
+def circ(ca, nh, B, base, dims=(4, 3), ws=3):
+    P, K = dims[0] * dims[1], ws ** len(dims)
+    nz = torch.arange(B * nh * P * K, dtype=torch.float32).reshape(B, nh, P, K) + base
+    return ca.Circulant(nz, ws, dims)
+
+
+def test_cat_dims3_stacks_heads(ca):
+    A, Bm = circ(ca, 2, 3, 0.0), circ(ca, 1, 3, 1000.0)
+    D = ca.cat(A, Bm, dims=3)
+    assert D.size() == (12, 12, 3, 3)
+    for b in range(3):
+        assert torch.equal(D.nzval[b, 0], A.nzval[b, 0])
+        assert torch.equal(D.nzval[b, 1], A.nzval[b, 1])
+        assert torch.equal(D.nzval[b, 2], Bm.nzval[b, 0])
+
+
+def test_cat_dims4_stacks_batches(ca):
+    A, Bm = circ(ca, 2, 1, 0.0), circ(ca, 2, 2, 500.0)
+    D = ca.cat(A, Bm, dims=4)
+    assert D.size() == (12, 12, 2, 3)
+    assert torch.equal(D.nzval[0], A.nzval[0])
+    assert torch.equal(D.nzval[1], Bm.nzval[0])
+    assert torch.equal(D.nzval[2], Bm.nzval[1])
+
+
+def test_cat_dims5_adds_a_batch_dim(ca):
+    A, Bm = circ(ca, 2, 2, 0.0), circ(ca, 2, 2, 7.0)
+    D = ca.cat(A, Bm, dims=5)
+    assert D.size() == (12, 12, 2, 2, 2)
+    assert torch.equal(D.nzval[0], A.nzval) and torch.equal(D.nzval[1], Bm.nzval)
+
+
+def test_cat_rejects_mismatches(ca):
+    A = circ(ca, 2, 2, 0.0)
+    with pytest.raises(AssertionError, match="batch dims"):
+        ca.cat(A, circ(ca, 2, 3, 0.0), dims=3)
+    with pytest.raises(AssertionError, match="kernel length"):
+        ca.cat(A, circ(ca, 2, 2, 0.0, dims=(4, 3), ws=1), dims=3)
+    with pytest.raises(AssertionError, match="batch dims"):
+        ca.cat(A, A, dims=2)
+
+
+def test_repeat_tiles_batch_dims(ca):
+    A = circ(ca, 2, 1, 0.0)
+    R = A.repeat(1, 1, 2, 3)
+    assert R.size() == (12, 12, 4, 3)
+    for b in range(3):
+        for h in range(4):
+            assert torch.equal(R.nzval[b, h], A.nzval[0, h % 2])
+    with pytest.raises(AssertionError, match="cannot be repeated"):
+        A.repeat(2, 1, 1, 1)
+
+
+def test_equality(ca):
+    A = circ(ca, 2, 2, 0.0)
+    assert A == A.copy()
+    assert not (A == circ(ca, 2, 2, 1.0))
+    assert not (A == A.reshape(12, 12, 4, 1))
+    assert not (A == circ(ca, 2, 2, 0.0, dims=(3, 4)))
+    assert ca.cat(A, A, dims=3) == A.repeat(1, 1, 2, 1)
