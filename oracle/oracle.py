@@ -219,10 +219,13 @@ def attention_fwd(kind, q, k, v, ws, nheads=1, precision="f64"):
     return y.reshape(q.shape), A
 
 
-def attention_bwd(kind, q, k, v, dy, ws, nheads=1, precision="f64", A=None):
+def attention_bwd(kind, q, k, v, dy, ws, nheads=1, precision="f64", A=None, dA_out=None):
     """(dq, dk, dv) for the composition adjacency -> ⊗ (the path
     test/grad.jl:17-21 differentiates) with the rrules of src/rrules.jl:
       ⊗ (:58-72):        dA = sim_Dot(dy, v), dv = Aᵀ ⊠ dy
+                         (+ dA_out, a cotangent on the returned A, shaped
+                         like A_nz: circulant_attention returns (y, A),
+                         src/attention.jl:19-25, and both can enter a loss)
       softmax (:42-56):  dS = A ∘ (dA - rowsum(A ∘ dA))
       Dot (:18-32):      dq̃ = dS ⊠ k̃, dk̃ = dSᵀ ⊠ q̃
       Distance (:1-16):  dq̃ = dS ⊠ k̃ - rowsum(dS)∘q̃, dk̃ = dSᵀ ⊠ q̃ - colsum(dS)∘k̃
@@ -236,6 +239,8 @@ def attention_bwd(kind, q, k, v, dy, ws, nheads=1, precision="f64", A=None):
     if A is None:
         _, A = attention_fwd(kind, q, k, v, ws, nheads, precision)
     dA = similarity(DOT, dyf, vf, dims, ws, 1.0, precision)
+    if dA_out is not None:
+        dA = dA + np.asarray(dA_out, dA.dtype).reshape(dA.shape)
     dv = apply(A, dyf, dims, ws, True, precision)
     dS = softmax_bwd(A, dA, K, precision)
     qt, kt = qf * s4, kf * s4

@@ -241,6 +241,33 @@ def test_attention_fused(ca, cuda, case, cplx, kind):
     _attention_case(ca, cuda, *case, cplx, kind, materialize=False)
 
 
+@pytest.mark.parametrize("case", [ATT_CASES[0], ATT_CASES[3], ATT_CASES[5], ATT_CASES[9]],
+                         ids=lambda c: f"{c[0]}-ws{c[1]}-C{c[2]}-h{c[4]}")
+@pytest.mark.parametrize("cplx", [False, True])
+@pytest.mark.parametrize("kind", [0, 1])
+def test_attention_grad_through_A(ca, cuda, case, cplx, kind):
+    """circulant_attention / circulant_mh_attention return (y, A)
+    (src/attention.jl:19-25, 38-42); a loss on both, Re<y, dy> + <A_nz, G>,
+    differentiates through A's softmax and similarity as well."""
+    dims, ws, C, B, nheads, seed = case
+    shape = shape_of(dims, C, B)
+    q, k, v, dy = (seeded(seed + 50 + i, shape, cplx) for i in range(4))
+    tq, tk, tv = (dev(a, cuda).requires_grad_(True) for a in (q, k, v))
+    simfun = ca.DotSimilarity() if kind == 0 else ca.DistanceSimilarity()
+    if nheads == 1:
+        y, A = ca.circulant_attention(simfun, tq, tk, tv, ws)
+    else:
+        y, A = ca.circulant_mh_attention(simfun, tq, tk, tv, ws, nheads, honor_simfun=True)
+    G = seeded(seed + 60, tuple(A.nzval.shape))
+    td = dev(dy, cuda)
+    ly = (y * td.conj()).real.sum() if y.is_complex() else (y * td).sum()
+    (ly + (A.nzval * dev(G, cuda)).sum()).backward()
+    gq, gk, gv = O.attention_bwd(kind, q, k, v, dy, ws, nheads, dA_out=G.reshape(B * nheads, -1))
+    assert rel_err(host(tq.grad), gq) < TOL_GRAD
+    assert rel_err(host(tk.grad), gk) < TOL_GRAD
+    assert rel_err(host(tv.grad), gv) < TOL_GRAD
+
+
 # the 2D compile-time-window cases again, with the Float32 matrix-core kernels
 # (the default above is the split-half arithmetic)
 F32_CASES = [c for c in ATT_CASES if len(c[0]) == 2 and c[1] in (3, 5, 7, 11, 15)

@@ -286,6 +286,43 @@ def test_attention_bwd_fd(dims, ws, nheads, cplx, kind):
         np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("dims,ws,nheads", [((4, 3), 3, 1), ((6,), 5, 2)])
+@pytest.mark.parametrize("cplx", [False, True])
+@pytest.mark.parametrize("kind", [O.DOT, O.DISTANCE])
+def test_attention_bwd_with_A_cotangent_fd(dims, ws, nheads, cplx, kind):
+    """A loss on both outputs (y, A) of circulant_attention (src/attention.jl:19-25):
+    L = Re<y, dy> + <A_nz, G>, against central finite differences."""
+    B, C = 2, 2 * nheads
+    shape = (B, C, *reversed(dims))
+    q, k, v, dy = (rand_signal(shape, cplx) for _ in range(4))
+    _, A0 = O.attention_fwd(kind, q, k, v, ws, nheads)
+    G = np.random.default_rng(77).standard_normal(A0.shape)
+
+    def loss(qq, kk, vv):
+        y, A = O.attention_fwd(kind, qq, kk, vv, ws, nheads)
+        return np.sum(np.real(y * np.conj(dy))) + np.sum(A * G)
+
+    got = O.attention_bwd(kind, q, k, v, dy, ws, nheads, dA_out=G)
+    h = 1e-6
+    for which, g_got in enumerate(got):
+        args = [q.copy(), k.copy(), v.copy()]
+        flat = args[which].reshape(-1)
+        ref = np.zeros_like(flat)
+        for i in range(flat.size):
+            for unit in ([1.0, 1j] if np.iscomplexobj(flat) else [1.0]):
+                old = flat[i]
+                flat[i] = old + h * unit
+                lp = loss(*args)
+                flat[i] = old - h * unit
+                lm = loss(*args)
+                flat[i] = old
+                ref[i] += (lp - lm) / (2 * h) * unit
+        np.testing.assert_allclose(g_got.reshape(-1), ref, rtol=1e-6, atol=1e-7)
+    # the A term matters: without it the gradients differ
+    plain = O.attention_bwd(kind, q, k, v, dy, ws, nheads)
+    assert max(np.max(np.abs(a - b)) for a, b in zip(plain[:2], got[:2])) > 1e-3
+
+
 def _dk_without_distance_correction(q, k, v, dy, ws):
     """A planted mistake: the Distance rrule's colsum(dS) .* k term dropped
     (the Dot pullback applied to a Distance forward).  The rowsum term of dq
