@@ -14,6 +14,8 @@ Julia name              -> here
                         -> scale, Circulant.sum, operators, Circulant.dot
   cat(As...; dims), repeat(A, counts...)
                         -> cat, Circulant.repeat
+  kernel_length, spatial_dims, spatial_size (unexported accessors)
+                        -> same names
 Gradients flow through torch.autograd with the reference's rrules
 (src/rrules.jl); Zygote.accum's role is played by autograd accumulation.
 """
@@ -23,7 +25,7 @@ from .circulant import (AbstractSimilarity, Circulant, DistanceSimilarity, DotSi
                         circulant_mh_adjacency, circulant_mh_attention,
                         circulant_mh_transposed_attention, circulant_similarity,
                         circulant_similarity_, circulant_transposed_attention, otimes, scale,
-                        softmax, softmax_)
+                        kernel_length, softmax, softmax_, spatial_dims, spatial_size)
 
 Circulant.__matmul__ = lambda A, x: otimes(A, x)
 
@@ -32,5 +34,5 @@ __all__ = [
     "cat", "circulant", "circulant_adjacency", "circulant_adjacency_", "circulant_attention",
     "circulant_mh_adjacency", "circulant_mh_attention", "circulant_mh_transposed_attention",
     "circulant_similarity", "circulant_similarity_", "circulant_transposed_attention", "otimes",
-    "scale", "softmax", "softmax_",
+    "kernel_length", "scale", "softmax", "softmax_", "spatial_dims", "spatial_size",
 ]

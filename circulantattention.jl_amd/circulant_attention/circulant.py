@@ -337,6 +337,21 @@ class CirculantSum(torch.autograd.Function):
 # API (src/similarity.jl, src/attention.jl)
 # ---------------------------------------------------------------------------
 
+def kernel_length(A: Circulant) -> int:
+    """kernel_length(A) (src/array.jl:31): the window size ws."""
+    return A.kernel_length
+
+
+def spatial_dims(A: Circulant) -> int:
+    """spatial_dims(A) (src/array.jl:32): 1 or 2."""
+    return A.nsp
+
+
+def spatial_size(A: Circulant) -> tuple:
+    """spatial_size(A) (src/array.jl:33): (N1,) or (N1, N2), fastest first."""
+    return A.spatial_size
+
+
 def cat(*As: Circulant, dims: int = 3) -> Circulant:
     """cat(As...; dims=3) (src/array.jl:62-64): concatenate along a batch
     dim (Julia dim >= 3), e.g. cat(A, B; dims=3) gives (P, P, 2nheads, B)

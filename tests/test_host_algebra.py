@@ -73,3 +73,14 @@ def test_equality(ca):
     assert not (A == A.reshape(12, 12, 4, 1))
     assert not (A == circ(ca, 2, 2, 0.0, dims=(3, 4)))
     assert ca.cat(A, A, dims=3) == A.repeat(1, 1, 2, 1)
+
+
+def test_accessors(ca):
+    """kernel_length / spatial_dims / spatial_size (src/array.jl:31-33) and
+    size (P, P, batch...) of a 2D and a 1D Circulant."""
+    A = circ(ca, 2, 3, 0.0, dims=(4, 3), ws=3)
+    assert (ca.kernel_length(A), ca.spatial_dims(A), ca.spatial_size(A)) == (3, 2, (4, 3))
+    assert A.size() == (12, 12, 2, 3)
+    L = ca.Circulant(torch.zeros(2, 1, 10, 5), 5, (10,))
+    assert (ca.kernel_length(L), ca.spatial_dims(L), ca.spatial_size(L)) == (5, 1, (10,))
+    assert L.size() == (10, 10, 1, 2)
