@@ -233,7 +233,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the (head, batch) units "
-                                   "shard across GPUs without communication, see DESIGN.md"}))
+                                   "would shard across GPUs without communication, one slice of "
+                                   "nheads*B per GPU"}))
         sys.exit(2)
     if args.ops:
         bench_ops(args)

@@ -84,3 +84,17 @@ def test_accessors(ca):
     L = ca.Circulant(torch.zeros(2, 1, 10, 5), 5, (10,))
     assert (ca.kernel_length(L), ca.spatial_dims(L), ca.spatial_size(L)) == (5, 1, (10,))
     assert L.size() == (10, 10, 1, 2)
+
+
+def test_bench_refuses_several_gpus():
+    """bench.py runs on one GPU: --gpus N > 1 exits with status 2 and a JSON
+    error line before touching a device."""
+    import json
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU only" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
