@@ -415,6 +415,31 @@ def test_cat_heads_then_otimes(ca, cuda):
     assert rel_err(host(z), zr) < TOL_FWD
 
 
+def test_cat_carries_gradients(ca, cuda):
+    """cat(A, B; dims=3) ⨷ w equals A ⨷ (first half of w's channels) next to
+    B ⨷ (second half), and gradients reach q, k, v and w through cat as they
+    do through the two separate products."""
+    dims, ws, Cc, Bb, nh = (12, 10), 5, 16, 2, 2
+    shape = shape_of(dims, Cc, Bb)
+    q, k, v, w, g = (seeded(720 + i, shape) for i in range(5))
+    tq, tk, tv, tw = (dev(a, cuda).requires_grad_(True) for a in (q, k, v, w))
+    _, A = ca.circulant_mh_attention(ca.DotSimilarity(), tq, tk, tv, ws, nh)
+    _, Bm = ca.circulant_mh_attention(ca.DotSimilarity(), tv, tq, tk, ws, nh)
+    z = ca.Otimes(ca.cat(A, Bm, dims=3), tw)
+    z2 = torch.cat([ca.Otimes(A, tw[:, :Cc // 2]), ca.Otimes(Bm, tw[:, Cc // 2:])], dim=1)
+    assert rel_err(host(z), host(z2)) < 1e-6
+    tg = dev(g, cuda)
+    grads = []
+    for out in (z, z2):
+        for t in (tq, tk, tv, tw):
+            t.grad = None
+        (out * tg).sum().backward(retain_graph=True)
+        grads.append([host(t.grad) for t in (tq, tk, tv, tw)])
+    for a, b in zip(*grads):
+        assert np.abs(a).max() > 0
+        assert rel_err(a, b) < 1e-6
+
+
 def test_scale_rrule(ca, cuda):
     """test/rrule.jl:22 scale(a, A) with a (1,1,2,2) against A (P,P,1,2):
     broadcast over the batch dims; gradients by the rrule of src/rrules.jl:94-114."""
