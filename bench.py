@@ -215,6 +215,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--math", choices=("split_f16", "f32"), default=None,
+                    help="arithmetic of the fused kernels' matrix products (default: the "
+                         "library's default, split_f16)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed region, run 3 device copies of this many MiB "
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -245,6 +248,9 @@ def main():
     from circulant_attention import _lib as L
     from circulant_attention._functions import ptr
 
+    if args.math is not None:
+        L.check(L.lib.circatt_set_math(L.MATH_F32 if args.math == "f32" else L.MATH_SPLIT_F16))
+    math_mode = {L.MATH_SPLIT_F16: "split_f16", L.MATH_F32: "f32"}[L.lib.circatt_get_math()]
     base = json.load(open(os.path.join(ROOT, "BASELINE.json")))
     dims, C, B, nh, ws, kind, cplx = CONFIGS[args.config]
     nsp = len(dims)
@@ -354,6 +360,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "c32" if cplx else "f32",
+        "math": math_mode,
         "data": "synthetic N(0,1), seeded, resident in HBM",
         "config": {"workload": describe(args.config), "spatial": list(dims), "C": C, "B": B,
                    "nheads": nh, "ws": ws, "similarity": "Distance" if kind else "Dot"},

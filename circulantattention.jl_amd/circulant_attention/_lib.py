@@ -9,6 +9,14 @@ from __future__ import annotations
 import ctypes
 import os
 
+# torch bundles its own HIP runtime under the soname libamdhip64.so.7, the
+# soname libcircatt.so links against.  Loaded after torch, libcircatt binds to
+# that already-loaded runtime, so one HIP runtime serves both; loaded first,
+# it would pull in /opt/rocm's copy and torch would then load a second one,
+# and two runtimes in one process do not share the device (the second reports
+# none).  So torch is imported before the library is opened.
+import torch  # noqa: F401
+
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get(
     "CIRCATT_LIB", os.path.join(os.path.dirname(_HERE), "libcircatt.so"))
@@ -58,6 +66,9 @@ SIGNATURES = {
                                     _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
     "circatt_fused_bwd_dkdv": (_int, [_int, _int, _int, _i64, _i64, _i32, _i64, _i64, _i64, _p,
                                       _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    "circatt_fused_bwd_noalloc_max_rows": (_i64, []),
+    "circatt_fused_bwd_noalloc": (_int, [_int, _int, _int, _i64, _i64, _i32, _i64, _i64, _i64,
+                                         _p, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
     "circatt_malloc": (_int, [ctypes.POINTER(_p), _i64]),
     "circatt_free": (_int, [_p]),
     "circatt_memcpy": (_int, [_p, _p, _i64, _int]),
