@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "circatt.h"
@@ -408,6 +409,81 @@ int circatt_fused_bwd_dkdv(int kind, int dtype, int nsp, int64_t n1, int64_t n2,
     return fused_bwd_impl(BWD_DKDV, kind, dtype, nsp, n1, n2, ws, C, nheads, B, q, k, v,
                           nullptr, dy, lse, nullptr, dk, dv, workspace, workspace_bytes, stream,
                           "circatt_fused_bwd_dkdv");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Fused backward without a workspace argument: the per-row D = <dy, y> lives
+// in `scratch`, a file-scope device array of fixed size.  Each GPU the
+// library runs on holds its own copy until the process ends; its device
+// address is looked up once per device (hipGetSymbolAddress) and kept.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kScratchBytes = int64_t(16) << 20;  // 4M rows of D
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this device's `scratch` (looked up on its first use).
+int scratch_address(void **out, const char *name) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_result(e, name);
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(CIRCATT_ERR_UNSUPPORTED, "%s: device %d beyond the %d supported", name, dev,
+                    kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_result(e, name);
+        if (p == nullptr) return fail(CIRCATT_ERR_HIP, "%s: no device address for scratch", name);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return CIRCATT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t circatt_fused_bwd_noalloc_max_rows(void) {
+    return kScratchBytes / (int64_t)sizeof(float);
+}
+
+int circatt_fused_bwd_noalloc(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int32_t ws,
+                              int64_t C, int64_t nheads, int64_t B, const void *q,
+                              const void *k, const void *v, const void *y, const void *dy,
+                              const float *lse, void *dq, void *dk, void *dv, void *stream) {
+    const char *name = "circatt_fused_bwd_noalloc";
+    const int64_t need = circatt_fused_bwd_workspace_bytes(nsp, n1, n2, nheads, B);
+    if (need < 0) return fail(CIRCATT_ERR_INVALID, "%s: invalid shape", name);
+    if (need > kScratchBytes)
+        return fail(CIRCATT_ERR_INVALID,
+                    "%s: %lld rows of D (P*nheads*B) exceed the static scratch of %lld rows; "
+                    "use circatt_fused_bwd with a workspace",
+                    name, (long long)(need / 4), (long long)(kScratchBytes / 4));
+    FusedProblem pr;
+    CIRCATT_TRY(fused_problem(kind, dtype, nsp, n1, n2, ws, C, nheads, B, pr));
+    CIRCATT_NONNULL(q);
+    CIRCATT_NONNULL(k);
+    CIRCATT_NONNULL(v);
+    CIRCATT_NONNULL(y);
+    CIRCATT_NONNULL(dy);
+    CIRCATT_NONNULL(lse);
+    CIRCATT_NONNULL(dq);
+    CIRCATT_NONNULL(dk);
+    CIRCATT_NONNULL(dv);
+    void *work = nullptr;
+    CIRCATT_TRY(scratch_address(&work, name));
+    return fused_bwd_impl(BWD_DQ | BWD_DKDV, kind, dtype, nsp, n1, n2, ws, C, nheads, B, q, k,
+                          v, y, dy, lse, dq, dk, dv, work, need, stream, name);
 }
 
 int circatt_malloc(void **ptr, int64_t bytes) {

@@ -193,6 +193,25 @@ int circatt_fused_bwd_dkdv(int kind, int dtype, int nsp, int64_t n1, int64_t n2,
                            const void *workspace, int64_t workspace_bytes, void *stream);
 
 /*
+ * circatt_fused_bwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * per-row D = <dy, y> lives in a fixed device array inside the library, one
+ * per GPU, held until the process ends: 16 MiB, i.e. at most
+ * circatt_fused_bwd_noalloc_max_rows() = 4194304 rows (P * nheads * B);
+ * larger problems fail with CIRCATT_ERR_INVALID.  The entry point calls no
+ * allocating routine.  Every call on one GPU shares that array: calls that
+ * overlap on one GPU (different streams, or different host threads) race
+ * and must be serialised by the caller.  Nothing in the array needs to start
+ * at zero (the dq pass writes every row's D before the dk/dv pass reads it).
+ */
+int64_t circatt_fused_bwd_noalloc_max_rows(void);
+int circatt_fused_bwd_noalloc(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int32_t ws,
+                              int64_t C, int64_t nheads, int64_t B, const void *q,
+                              const void *k, const void *v, const void *y, const void *dy,
+                              const float *lse, void *dq, void *dk, void *dv, void *stream);
+
+/*
  * Device memory helpers for hosts without a GPU array package (the reference
  * gets these from CUDA.jl).  kind: 0 host->device, 1 device->host,
  * 2 device->device.
