@@ -34,6 +34,9 @@ FLAGS = [
     # MFMA accumulators in VGPRs: the softmax rescale and the B-operand reuse
     # of the accumulator then need no AGPR copies
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # the kernels' LDS atomics are issued by one lane per wave already; the
+    # atomic optimizer would wrap each in a lane-iteration loop
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]

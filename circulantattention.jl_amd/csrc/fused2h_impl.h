@@ -27,9 +27,11 @@
 // 16-byte reads of a slot; apply-type rows (one channel of four elements)
 // come from the same slots through the transposing read ds_read_b64_tr_b16.
 //
-// Operands must stay inside the f16 range, |x| < 65504 (queries after the
-// scale 1/sqrt(dh) * log2(e)); circatt_set_math(CIRCATT_MATH_F32) selects
-// the Float32 kernels, which have no such limit.
+// The halves alone would lose Float32's range (lo turns subnormal below
+// 2^-3, every half overflows at 65520), so each item scales its operands by
+// powers of two before the split and undoes the scale on the Float32 results
+// (see shift_of below); waves whose scores could overflow the halves take a
+// slower walk that unscales every score after its product.
 #pragma once
 #include "fused2d_impl.h"
 
@@ -129,8 +131,52 @@ __device__ __forceinline__ h8 cat(h4 a, h4 b) {
 
 constexpr int KS = 40;  // halves per pixel slot: 16 hi, 16 lo, 8 pad (80 bytes)
 
-// slot store of 16 Float32 values as [16 hi | 16 lo] halves
-__device__ __forceinline__ void store_slot(char *sp, const float (&x)[16]) {
+// ---- power-of-two operand scaling ----
+// f16 halves lose Float32's range: lo turns subnormal (spacing 2^-24) once
+// |x| < 2^-3 and every half overflows at 65520.  Operands are therefore
+// scaled by powers of two (exact) before the split, chosen from the largest
+// magnitude m over what is staged for an item (or over a register pixel),
+// and the scale is undone on the Float32 results.  With b the biased
+// exponent of m (m < 2^(b - 126)), shift_of(b) is 0 when m lies in
+// [2^-2, 2^5) and otherwise the shift that brings m into [4, 8).
+__device__ __forceinline__ int shift_of(unsigned b) {
+    return (b >= 125u && b <= 131u) ? 0 : 129 - (int)b;
+}
+// biased exponent of a non-negative float (its bits >> 23; 255 for inf/NaN)
+__device__ __forceinline__ unsigned bexp(float m) { return __float_as_uint(m) >> 23; }
+// exponent e with |x * 2^shift_of(b)| < 2^e for every x of the set
+__device__ __forceinline__ int scaled_exp(unsigned b) { return (int)b - 126 + shift_of(b); }
+
+template <int N>
+__device__ __forceinline__ float maxabs(const float (&x)[N]) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) m = fmaxf(m, fabsf(x[i]));
+    return m;
+}
+// maximum of a non-negative value (as bits) over the wave, in lane 63
+template <int CTRL, int ROWS>
+__device__ __forceinline__ unsigned dpp_umax(unsigned u) {
+    const unsigned o = (unsigned)__builtin_amdgcn_update_dpp(0, (int)u, CTRL, ROWS, 0xf, false);
+    return u > o ? u : o;
+}
+__device__ __forceinline__ unsigned wave_umax63(unsigned u) {
+    u = dpp_umax<0x111, 0xf>(u);  // row_shr:1
+    u = dpp_umax<0x112, 0xf>(u);  // row_shr:2
+    u = dpp_umax<0x114, 0xf>(u);  // row_shr:4
+    u = dpp_umax<0x118, 0xf>(u);  // row_shr:8  (lane 15 of each row: the row's maximum)
+    u = dpp_umax<0x142, 0xa>(u);  // row_bcast:15 into rows 1, 3
+    u = dpp_umax<0x143, 0xc>(u);  // row_bcast:31 into rows 2, 3
+    return u;
+}
+
+// slot store of 16 Float32 values as [16 hi | 16 lo] halves, each scaled by
+// 2^s first when SC
+template <bool SC = false>
+__device__ __forceinline__ void store_slot(char *sp, const float (&xin)[16], int s = 0) {
+    float x[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) x[c] = SC ? __builtin_amdgcn_ldexpf(xin[c], s) : xin[c];
     h2 hi[8], lo[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) split2(x[2 * c], x[2 * c + 1], hi[c], lo[c]);
@@ -164,7 +210,9 @@ struct LGeo {
     static constexpr int OS0 = 2 * OT1;            // Float32 scalars per slot
     static constexpr int OS1 = OS0 + G::LPX * 4;
     static constexpr int NSCAL = MODE == BWDKV ? 2 : (DIST ? 1 : 0);
-    static constexpr int bytes = OS0 + NSCAL * G::LPX * 4;
+    // per-item exchange of maxima: 4 words of (item << 9 | biased exponent)
+    static constexpr int OX = OS0 + NSCAL * G::LPX * 4;
+    static constexpr int bytes = OX + 16;
 };
 
 template <int P, bool CPLX, bool DIST, int MODE>
@@ -324,8 +372,11 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     int k = 0;
     int item = f2d::item_of(a, 0);
     if (item >= a.nitems) return;
+    unsigned *const xwords = reinterpret_cast<unsigned *>(lds + L::OX);
+    if (threadIdx.x < 4) xwords[threadIdx.x] = 0u;
     load_stage(item);
     load_regs(item);
+    __syncthreads();  // exchange words cleared before any item's maxima
 
     while (true) {
         int unit, h0, w0;
@@ -337,20 +388,55 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         const int64_t soff = (int64_t)unit * a.P;
         const float c2 = a.c2;
 
-        __syncthreads();  // the previous item's LDS reads are done
+        // Largest magnitudes of what this item stages (tensors 0, 1) and, in
+        // the key-centric pass, of the register v (the staged -D carries its
+        // scale): a wave maximum, then one LDS atomic per wave.  Keys
+        // (k << 9 | exponent) rise from item to item, so the words need no
+        // clearing between items.
+        {
+            unsigned u0 = 0u, u1 = 0u, u2 = 0u;
+            if (hslot >= 0) {
+                u0 = __float_as_uint(maxabs(h0v));
+                u1 = __float_as_uint(maxabs(h1v));
+            }
+            if constexpr (KV) u2 = __float_as_uint(maxabs(nh1));
+            u0 = wave_umax63(u0);
+            u1 = wave_umax63(u1);
+            if constexpr (KV) u2 = wave_umax63(u2);
+            if (lane == 63) {
+                const unsigned key = (unsigned)k << 9;
+                __hip_atomic_fetch_max(xwords + 0, key | (u0 >> 23), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_fetch_max(xwords + 1, key | (u1 >> 23), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+                if constexpr (KV)
+                    __hip_atomic_fetch_max(xwords + 2, key | (u2 >> 23), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        }
+        __syncthreads();  // the previous item's LDS reads are done; maxima in
+        const unsigned b0 = __builtin_amdgcn_readfirstlane(xwords[0]) & 255u;
+        const unsigned b1 = __builtin_amdgcn_readfirstlane(xwords[1]) & 255u;
+        const unsigned b2 = KV ? __builtin_amdgcn_readfirstlane(xwords[2]) & 255u : 127u;
+        // shifts of the staged tensors (k or q; v or dy) and of the register v
+        const int s0 = shift_of(b0), s1 = shift_of(b1), s2 = KV ? shift_of(b2) : 0;
         if (hslot >= 0) {
             float n2 = 0.f;
             if constexpr (DIST) {
 #pragma unroll
                 for (int c = 0; c < 16; ++c) n2 += h0v[c] * h0v[c];
             }
-            store_slot(lds + L::OT0 + hslot * KS * 2, h0v);
-            store_slot(lds + L::OT1 + hslot * KS * 2, h1v);
+            char *const sl0 = lds + L::OT0 + hslot * KS * 2;
+            char *const sl1 = lds + L::OT1 + hslot * KS * 2;
+            if (s0 == 0) store_slot(sl0, h0v); else store_slot<true>(sl0, h0v, s0);
+            if (s1 == 0) store_slot(sl1, h1v); else store_slot<true>(sl1, h1v, s1);
             if constexpr (KV) {
-                // staged queries: A_q = -lse log2(e) [- c2 |q|^2 / 2], and -D
+                // staged queries: A_q = -lse log2(e) [- c2 |q|^2 / 2], and
+                // -D in the scale of the dP product
                 reinterpret_cast<float *>(lds + L::OS0)[hslot] =
                     -hs0 * kLog2e - (DIST ? 0.5f * c2 * n2 : 0.f);
-                reinterpret_cast<float *>(lds + L::OS1)[hslot] = -hs1;
+                reinterpret_cast<float *>(lds + L::OS1)[hslot] =
+                    -__builtin_amdgcn_ldexpf(hs1, s1 + s2);
             } else if constexpr (DIST) {
                 reinterpret_cast<float *>(lds + L::OS0)[hslot] = -0.5f * c2 * n2;  // key bias
             }
@@ -369,11 +455,43 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             }
         };
         join(nh0, nr0);
+        // The score product's register operand absorbs the staged tensor's
+        // shift (q' = q c2 2^-s0 against k' = k 2^s0), so scores keep their
+        // scale.  A wave whose |q'| reaches 2^15 (the halves would overflow)
+        // or, in the backward, whose scores could pass 2^20 (where the
+        // recomputed probabilities exp2(s - lse) lose all precision and could
+        // overflow the dS halves) takes the slow walk: q normalised per pixel
+        // and each score unscaled after its product.
+        const float c2s = __builtin_amdgcn_ldexpf(c2, -s0);
+        const float mr0 = maxabs(nr0);
+        const float lim = MODE == FWD ? 32768.f
+                                      : fminf(32768.f, __builtin_amdgcn_ldexpf(1.f, 16 - scaled_exp(b0)));
+        const bool slow = __builtin_amdgcn_ballot_w64(!(mr0 * c2s < lim)) != 0;
+        // slow walk: q c2 shifted per pixel to [4, 8), products scaled by 2^eu
+        int eu = 0;
         h8 r0h, r0l, r1h, r1l;
-        reg_split(nr0, c2, r0h, r0l);
-        if constexpr (MODE != FWD) {
-            join(nh1, nr1);
-            reg_split(nr1, 1.f, r1h, r1l);
+        if (slow) {
+            const int sp = min(120, max(-120, 129 - (int)bexp(gmax(mr0) * c2)));
+            eu = sp + s0;
+            reg_split(nr0, __builtin_amdgcn_ldexpf(c2, sp), r0h, r0l);
+        } else {
+            reg_split(nr0, c2s, r0h, r0l);
+        }
+        // dy (query-centric pass) is shifted per register pixel; v
+        // (key-centric pass) by the block-wide s2
+        int sd = 0;
+        if constexpr (MODE != FWD) join(nh1, nr1);
+        if constexpr (MODE == BWDQ) {
+            sd = shift_of(bexp(gmax(maxabs(nr1))));
+            if (__builtin_amdgcn_ballot_w64(sd != 0) != 0)
+                reg_split(nr1, __builtin_amdgcn_ldexpf(1.f, sd), r1h, r1l);
+            else
+                reg_split(nr1, 1.f, r1h, r1l);
+        } else if constexpr (MODE == BWDKV) {
+            if (s2 != 0)
+                reg_split(nr1, __builtin_amdgcn_ldexpf(1.f, s2), r1h, r1l);
+            else
+                reg_split(nr1, 1.f, r1h, r1l);
         }
         // sums of the loaded halves over the four lane groups count every
         // channel once
@@ -475,19 +593,38 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             // scores of the pair's blocks relative to m, masked to -inf outside
             // the window (dep: a per-walk value for the lane masks, so that
             // walks do not share, and keep live, each other's masks)
-            auto scores_ops = [&](auto PI, auto REL, const POps &o, f4 (&sv)[2], int dep) {
+            // (SLOW: the product of the per-pixel normalised q is unscaled by
+            // 2^-eu and the row terms are added after it)
+            auto scores_ops = [&](auto PI, auto REL, const POps &o, f4 (&sv)[2], int dep,
+                                  auto SLOW) {
                 constexpr int pi = decltype(PI)::value;
                 constexpr bool rel = decltype(REL)::value;
+                constexpr bool slw = decltype(SLOW)::value;
                 constexpr int b0 = 2 * pi;
                 constexpr bool has1 = b0 + 1 < NBLK;
                 auto sc = [&](auto B, int u) {
                     constexpr int b = decltype(B)::value;
                     constexpr int bi = b / NKW, bj = b % NKW;
-                    f4 init = f4{0.f, 0.f, 0.f, 0.f};
-                    if constexpr (DIST) init = o.kb[u];
-                    if constexpr (rel) init = init - f4{m, m, m, m};
-                    init = mfmah(o.a[u], r0h, init);
-                    f4 x = mfmah(o.a[u], r0l, init);
+                    f4 x;
+                    if constexpr (slw) {
+                        // the relative score is the maximised value minus m,
+                        // rounded as in the pass that took the maximum
+                        f4 z = f4{0.f, 0.f, 0.f, 0.f};
+                        z = mfmah(o.a[u], r0h, z);
+                        z = mfmah(o.a[u], r0l, z);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            x[r] = __builtin_amdgcn_ldexpf(z[r], -eu);
+                            if constexpr (DIST) x[r] += o.kb[u][r];
+                            if constexpr (rel) x[r] -= m;
+                        }
+                    } else {
+                        f4 init = f4{0.f, 0.f, 0.f, 0.f};
+                        if constexpr (DIST) init = o.kb[u];
+                        if constexpr (rel) init = init - f4{m, m, m, m};
+                        init = mfmah(o.a[u], r0h, init);
+                        x = mfmah(o.a[u], r0l, init);
+                    }
                     x[0] = mask_sel_d<lane_mask(P, bi, bj, 0)>(x[0], -INFINITY, dep);
                     x[1] = mask_sel_d<lane_mask(P, bi, bj, 1)>(x[1], -INFINITY, dep);
                     x[2] = mask_sel_d<lane_mask(P, bi, bj, 2)>(x[2], -INFINITY, dep);
@@ -526,8 +663,8 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 acc = mfmah(vl, ph, acc);
                 return ps;
             };
-            auto scores = [&](auto PI, auto REL, f4 (&sv)[2], int dep) {
-                scores_ops(PI, REL, load_ops(PI), sv, dep);
+            auto scores = [&](auto PI, auto REL, f4 (&sv)[2], int dep, auto SLOW) {
+                scores_ops(PI, REL, load_ops(PI), sv, dep, SLOW);
             };
             auto apply = [&](auto PI, const f4 (&sv)[2]) { return apply_ops(load_ops(PI), sv); };
             // Scores relative to a reference maximum m, folded into the MFMA's
@@ -541,6 +678,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             constexpr int PC = STREAM ? 4 : 0;
             uint64_t over = 1;
             if constexpr (STREAM) {
+              if (!slow) {
                 // Walk order: PC, then the other pairs.  Skewed by one pair:
                 // an iteration takes the scores of the next pair (MFMA) beside
                 // the softmax of the current one (vector ALU), so that the two
@@ -552,7 +690,8 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 POps ca, cv;  // score rows of the next pair, value rows of the current
                 load_a(std::integral_constant<int, PC>{}, ca);
                 load_v(std::integral_constant<int, PC>{}, cv);
-                scores_ops(std::integral_constant<int, PC>{}, std::false_type{}, ca, sv, k);
+                scores_ops(std::integral_constant<int, PC>{}, std::false_type{}, ca, sv, k,
+                           std::false_type{});
                 m = gmax(pair_max(sv));
                 sv[0] = sv[0] - f4{m, m, m, m};
                 sv[1] = sv[1] - f4{m, m, m, m};
@@ -568,7 +707,8 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     if constexpr (i + 1 < NPAIR) load_v(std::integral_constant<int, ord(i + 1)>{}, nv);
                     f4 svn[2];
                     if constexpr (i + 1 < NPAIR)
-                        scores_ops(std::integral_constant<int, ord(i + 1)>{}, std::true_type{}, ca, svn, k);
+                        scores_ops(std::integral_constant<int, ord(i + 1)>{}, std::true_type{}, ca, svn, k,
+                                   std::false_type{});
                     const float ps = apply_ops(cv, sv);
                     if constexpr (i > 0) over |= __builtin_amdgcn_ballot_w64(!(ps <= 256.f));
                     if constexpr (i + 1 < NPAIR) {
@@ -587,15 +727,19 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     });
 #endif
                 });
+              }
             }
-            if (over != 0) {
-                // exact row maximum, then one walk with every score <= m
+            // exact row maximum, then one walk with every score <= m (the slow
+            // walk always takes this form; the streamed walk skipped, it
+            // issues the next item's loads here)
+            auto twopass = [&](auto SLOW) {
+                constexpr bool slw = decltype(SLOW)::value;
                 float mx = -INFINITY;
                 static_for<0, NPAIR>([&](auto PI) {
                     FWD_FENCE_A();
-                    if constexpr (!STREAM && decltype(PI)::value == PFP) prefetch();
+                    if constexpr ((slw || !STREAM) && decltype(PI)::value == PFP) prefetch();
                     f4 sv[2];
-                    scores(PI, std::false_type{}, sv, k + 1);
+                    scores(PI, std::false_type{}, sv, k + 1, SLOW);
                     mx = fmaxf(mx, pair_max(sv));
                 });
                 m = gmax(mx);
@@ -604,9 +748,14 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 static_for<0, NPAIR>([&](auto PI) {
                     FWD_FENCE_A();
                     f4 sv[2];
-                    scores(PI, std::true_type{}, sv, k + 2);
+                    scores(PI, std::true_type{}, sv, k + 2, SLOW);
                     apply(PI, sv);
                 });
+            };
+            if (slow) {
+                twopass(std::true_type{});
+            } else if (over != 0) {
+                twopass(std::false_type{});
             }
             const float l = gsum(lsum);
             const float inv = 1.f / l;
@@ -614,18 +763,26 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 float *yb = a.yout + uoff;
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    yb[f2d::comp_off<CPLX>(a.P, rpix, 4 * g + r)] = acc[r] * inv;
+                    yb[f2d::comp_off<CPLX>(a.P, rpix, 4 * g + r)] =
+                        __builtin_amdgcn_ldexpf(acc[r] * inv, -s1);
                 if (g == 0)
                     a.lse_out[soff + rpix] =
                         (m + __log2f(l)) * kLn2 - (DIST ? 0.5f * sq * a.scale : 0.f);
             }
         } else {
-            // BWDQ: score row term -lse log2(e) [- c2 |q|^2 / 2], dP row term -D
+            // BWDQ: score row term -lse log2(e) [- c2 |q|^2 / 2], dP row term
+            // -D in the scale of the dP product (2^(sd + s1): dy' against v')
             const float nl = -rowL * kLog2e - (DIST ? 0.5f * c2 * sq : 0.f);
+            const float nD = -__builtin_amdgcn_ldexpf(rowD, sd + s1);
             const float kb = DIST ? -0.5f * c2 * sq : 0.f;  // BWDKV key bias
             f4 acc0 = f4{0.f, 0.f, 0.f, 0.f};  // dQ (BWDQ) or dK (BWDKV)
             f4 acc1 = f4{0.f, 0.f, 0.f, 0.f};  // dV (BWDKV)
             float corr = 0.f;
+            // SLOW: scores of the per-pixel normalised register operand,
+            // unscaled by 2^-eu after the product, the row terms added, and
+            // clamped at 0 (a probability recomputed from lse is at most 1)
+            auto walk = [&](auto SLOW) {
+            constexpr bool slw = decltype(SLOW)::value;
             static_for<0, NPAIR>([&](auto PI) {
                 constexpr int pi = decltype(PI)::value;
                 constexpr int b0 = 2 * pi;
@@ -645,9 +802,16 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     } else {
                         s = f4{nl, nl, nl, nl};
                         if constexpr (DIST) s = s + scal(B, pS0);
-                        dp = f4{-rowD, -rowD, -rowD, -rowD};
+                        dp = f4{nD, nD, nD, nD};
                     }
-                    s = score(B, pA0, r0h, r0l, s);
+                    if constexpr (slw) {
+                        const f4 z = score(B, pA0, r0h, r0l, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            s[r] = fminf(__builtin_amdgcn_ldexpf(z[r], -eu) + s[r], 0.f);
+                    } else {
+                        s = score(B, pA0, r0h, r0l, s);
+                    }
                     dp = score(B, pA1, r1h, r1l, dp);
                     p[u][0] = mask_sel_d<lane_mask(P, bi, bj, 0)>(__builtin_amdgcn_exp2f(s[0]), 0.f, k);
                     p[u][1] = mask_sel_d<lane_mask(P, bi, bj, 1)>(__builtin_amdgcn_exp2f(s[1]), 0.f, k);
@@ -688,14 +852,21 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     acc1 = mfmah(zh, pl, acc1);
                 }
             });
+            };
+            if (slow) {
+                walk(std::true_type{});
+            } else {
+                walk(std::false_type{});
+            }
             const float cs = DIST ? gsum(corr) : 0.f;
             if (rvalid) {
                 if constexpr (!KV) {
                     float *ob = a.dq + uoff;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        float val = acc0[r];
-                        if constexpr (DIST) val -= cs * reg0[r];
+                        // dS' = 2^(sd + s1) dS, k' = 2^s0 k
+                        float val = __builtin_amdgcn_ldexpf(acc0[r], -(sd + s1 + s0));
+                        if constexpr (DIST) val -= __builtin_amdgcn_ldexpf(cs, -(sd + s1)) * reg0[r];
                         ob[f2d::comp_off<CPLX>(a.P, rpix, 4 * g + r)] = val * a.scale;
                     }
                     if (g == 0) a.dbuf[soff + rpix] = rowD;
@@ -705,9 +876,10 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int o = f2d::comp_off<CPLX>(a.P, rpix, 4 * g + r);
-                        vb[o] = acc1[r];
-                        float val = acc0[r];
-                        if constexpr (DIST) val -= cs * reg0[r];
+                        // dy' = 2^s1 dy, dS' = 2^(s2 + s1) dS, q' = 2^s0 q
+                        vb[o] = __builtin_amdgcn_ldexpf(acc1[r], -s1);
+                        float val = __builtin_amdgcn_ldexpf(acc0[r], -(s2 + s1 + s0));
+                        if constexpr (DIST) val -= __builtin_amdgcn_ldexpf(cs, -(s2 + s1)) * reg0[r];
                         kbp[o] = val * a.scale;
                     }
                 }

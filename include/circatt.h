@@ -53,11 +53,18 @@ int circatt_version(void);
  * Arithmetic of the fused kernels' matrix products.  The reference computes
  * in Float32 throughout; it has no counterpart of this switch.
  *   CIRCATT_MATH_SPLIT_F16 (default): each Float32 operand is split into two
- *     halves and a product is taken as hi*hi + lo*hi + hi*lo on the f16
+ *     f16 halves and a product is taken as hi*hi + lo*hi + hi*lo on the f16
  *     matrix cores with Float32 accumulation (relative error near 2^-21 per
- *     operand, the order of Float32 rounding); operands must stay below
- *     65504 in magnitude (queries after scaling by 1/sqrt(dh)*log2(e)).
- *   CIRCATT_MATH_F32: Float32 matrix products (no range restriction).
+ *     operand, the order of Float32 rounding).  Operands are scaled by powers
+ *     of two per work item (16x16 pixels of one head) before the split, so
+ *     the halves keep Float32's range: inputs of any magnitude (1e-7 and 1e4
+ *     are tested) give Float32-class results.  Where q.k scores are so large
+ *     that the halves could overflow, a slower exact-scale walk takes over.
+ *   CIRCATT_MATH_F32: Float32 matrix products.
+ * Like any attention backward that recomputes the probabilities from the
+ * stored log-sum-exp, the fused backward loses precision once scores reach
+ * ~1e3 (Float32 rounding of the score itself); the reference's own Float32
+ * computation misses the gradient tolerance there as well.
  * Process-wide; takes effect for launches after the call.
  */
 #define CIRCATT_MATH_SPLIT_F16 0
