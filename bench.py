@@ -7,10 +7,12 @@ batch of synthetic N(0,1) float32 inputs already resident in HBM, at the
 configuration BASELINE.json's metric is quoted on (cfg3: DotSimilarity,
 256x256x64x4, 4 heads, ws = 15).  Prints one JSON line.
 
-Timing: after W warm-up steps, K steps of eager launches with HIP events
-around every entry point (per-kernel times, `ms_per_step_eager`), then the
-step captured once as a HIP graph and replayed W + K times, K of them timed
-(`ms_per_step` and `value`; `--no-graph` times the eager launches only).
+Timing: the step is captured once as a HIP graph; it is replayed untimed
+back to back for --settle-ms (0.3 s by default: from idle the GPU's clocks
+need ~30 ms of sustained load to reach steady state), then W warm-up
+replays, then K timed replays (`ms_per_step` and `value`; `--no-graph`
+times eager launches instead).  Right after, K eager steps with HIP events
+around every entry point give the per-kernel times (`kernels`, roofline).
 
 Roofline: every kernel of the step is priced at its algorithmic FLOPs
 (U = 2*P*K*dh*nheads*B per window contraction; forward 2U, dq pass 2U for
@@ -208,11 +210,11 @@ def bench_ops(args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # about 35 ms of warm-up: over the first few milliseconds of sustained
-    # work the GPU's clocks are still rising (20 steps after 5 warm-up steps
-    # time 13% slower than steady state on MI355X)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--settle-ms", type=float, default=300.0,
+                    help="untimed back-to-back steps before the warm-up steps, in ms of wall "
+                         "time (the GPU's clocks ramp over the first ~30 ms of sustained load)")
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--math", choices=("split_f16", "f32"), default=None,
@@ -288,32 +290,14 @@ def main():
                                              ptr(work), wbytes, s))
 
     kernels = [("fwd", fwd), ("bwd_dq", bwd_dq), ("bwd_dkdv", bwd_dkdv)]
-    for _ in range(args.warmup):
-        for _, f in kernels:
-            f(sp)
+    for _, f in kernels:  # first launches (code objects, kernel attributes)
+        f(sp)
     torch.cuda.synchronize()
 
-    # eager timed region: K steps of the three entry points, HIP events around
-    # every launch on `stream` (per-kernel times for the roofline)
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in kernels] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for s in range(args.steps):
-        for (_, f), (e0, e1) in zip(kernels, evs[s]):
-            e0.record(stream)
-            f(sp)
-            e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step_eager = wall * 1e3 / args.steps
-    kern_ms = {name: sum(evs[s][i][0].elapsed_time(evs[s][i][1]) for s in range(args.steps)) /
-               args.steps for i, (name, _) in enumerate(kernels)}
-
-    # graph timed region: the step (the same three entry points) captured once
-    # as a HIP graph and replayed K times, as a training loop would launch it;
-    # the entry points allocate nothing and record no memset, so they capture
-    ms_step_graph = None
+    # the step (the same three entry points) captured once as a HIP graph, as a
+    # training loop would launch it; the entry points allocate nothing and
+    # record no memset, so they capture
+    graph = None
     if not args.no_graph:
         cs = torch.cuda.Stream(dev)
         csp = ctypes.c_void_p(cs.cuda_stream)
@@ -323,15 +307,51 @@ def main():
             for _, f in kernels:
                 f(csp)
         torch.cuda.synchronize()
-        for _ in range(args.warmup):
+
+    def step():
+        if graph is not None:
             graph.replay()
+        else:
+            for _, f in kernels:
+                f(sp)
+
+    # Settle: from idle, the GPU's clocks need some 20-30 ms of sustained load
+    # to reach steady state (cfg3 from idle: the first 25 steps take 740 us on
+    # average, steady state 630 us), so before the W warm-up steps the step
+    # runs untimed, back to back, for --settle-ms.
+    settle_steps = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < args.settle_ms / 1e3:
+        for _ in range(10):
+            step()
+        settle_steps += 10
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            graph.replay()
-        torch.cuda.synchronize()
-        ms_step_graph = (time.perf_counter() - t0) * 1e3 / args.steps
-    ms_step = ms_step_graph if ms_step_graph is not None else ms_step_eager
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region: K steps, synchronised on both sides
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # per-kernel times for the roofline, right after (the clocks still at
+    # steady state): K eager steps with HIP events around every launch on the
+    # stream the kernels run on
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in kernels] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        for (_, f), (e0, e1) in zip(kernels, evs[s]):
+            e0.record(stream)
+            f(sp)
+            e1.record(stream)
+    torch.cuda.synchronize()
+    ms_step_eager = (time.perf_counter() - t0) * 1e3 / args.steps
+    kern_ms = {name: sum(evs[s][i][0].elapsed_time(evs[s][i][1]) for s in range(args.steps)) /
+               args.steps for i, (name, _) in enumerate(kernels)}
 
     mpix = B * P / (ms_step / 1e3) / 1e6
     cfac = 2 if cplx else 1
@@ -353,8 +373,10 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
-        "timing": ("HIP graph of the step's three entry points, replayed" if ms_step_graph
+        "timing": ("HIP graph of the step's three entry points, replayed" if graph
                    is not None else "eager launches"),
+        "settle_ms": args.settle_ms,
+        "settle_steps": settle_steps,
         "ms_per_step_eager": round(ms_step_eager, 4),
         "higher_is_better": True,
         "scaling": "weak",
