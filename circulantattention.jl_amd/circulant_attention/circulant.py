@@ -166,9 +166,13 @@ class Circulant:
                        dims=self.size(), nnz=self.nzval.numel())
 
     def __repr__(self):
+        """show (src/array.jl:44-47): the type, kernel length, spatial size,
+        then a summary of the CSR data."""
+        size = "×".join(str(d) for d in self.size())
         return (f"Circulant{{Float32, {self.ndims()}, {self.kernel_length}, {self.nsp}}} with "
-                f"kernel-length {self.kernel_length}, spatial-size {self.spatial_size}, "
-                f"size {self.size()}")
+                f"kernel-length {self.kernel_length}, spatial-size {self.spatial_size}, and data,\n"
+                f"{size} batched CSR with {self.P * self.K * self.nb} stored entries "
+                f"(Float32 nzVal, Int32 rowPtr and colVal) on {self.device}")
 
     # ---- shape utilities (src/array.jl:49-60) ----
     def reshape(self, *dims):
@@ -428,9 +432,17 @@ def circulant_similarity_(A: Circulant, simfun, x, y) -> Circulant:
     if A.nb != x.shape[0]:
         raise AssertionError(f"batchdim of circulant matrix ({A.nb}) must match that of x, y "
                              f"({x.shape[0]}).")
-    with torch.no_grad():
-        nz = SimilarityFn.apply(_kind(simfun), x, y, spatial, A.kernel_length, 1.0)
-        A.nzval.copy_(nz.reshape(A.nzval.shape))
+    if tuple(spatial) != A.spatial_size:
+        raise AssertionError(f"spatial size {tuple(spatial)} of x does not match A's "
+                             f"{A.spatial_size}")
+    if not A.nzval.is_contiguous():
+        raise AssertionError("circulant_similarity! needs A's nzVal contiguous")
+    nsp, n1, n2 = geometry(spatial)
+    x, y = x.contiguous(), y.contiguous()
+    # written in place by the kernel (no temporary)
+    L.check(L.lib.circatt_similarity(_kind(simfun), L.C32 if x.is_complex() else L.F32, nsp, n1,
+                                     n2, A.kernel_length, x.shape[1], A.nb, 1.0, ptr(x), ptr(y),
+                                     ptr(A.nzval), stream_ptr(x.device)), "circatt_similarity")
     return A
 
 
@@ -442,8 +454,13 @@ def softmax(A: Circulant) -> Circulant:
 def softmax_(A: Circulant, B: Circulant = None) -> Circulant:
     """NNlib.softmax!(A, B=A) (src/similarity.jl:113-116), not differentiable."""
     B = A if B is None else B
-    with torch.no_grad():
-        A.nzval.copy_(SoftmaxFn.apply(B.nzval))
+    if not (A.nzval.is_contiguous() and B.nzval.is_contiguous()):
+        raise AssertionError("softmax! needs contiguous nzVal")
+    if A.size() != B.size() or A.kernel_length != B.kernel_length:
+        raise AssertionError("softmax!(A, B): A and B must have the same size and pattern")
+    # in place when B is A (circatt_softmax allows in == out)
+    L.check(L.lib.circatt_softmax(A.K, A.P * A.nb, ptr(B.nzval), ptr(A.nzval),
+                                  stream_ptr(A.nzval.device)), "circatt_softmax")
     return A
 
 

@@ -55,7 +55,9 @@ def shape_of(dims, C, B):
 # ---------------------------------------------------------------------------
 PATTERN_CASES = [((8,), 5), ((8, 8), 5), ((12, 10), 3), ((32, 32), 7), ((4,), 5), ((2,), 5),
                  ((4, 4), 5), ((3, 5), 7), ((1, 6), 3), ((128, 96), 15), ((262144,), 63),
-                 ((17,), 1)]
+                 ((17,), 1),
+                 # windows past 15 in 2D (cfg4a's ws = 31), and past the image
+                 ((70, 40), 31), ((37, 9), 19), ((20, 24), 31)]
 
 
 @pytest.mark.parametrize("dims,ws", PATTERN_CASES)
@@ -68,6 +70,20 @@ def test_pattern_bitexact(ca, cuda, dims, ws):
     colval = torch.empty((nb, P * K), dtype=torch.int32, device=cuda)
     L.check(L.lib.circatt_pattern(nsp, n1, n2, ws, nb, ptr(rowptr), ptr(colval), stream_ptr()))
     rp, cv = O.pattern(dims, ws, nb)
+    assert np.array_equal(rowptr.cpu().numpy(), rp)
+    assert np.array_equal(colval.cpu().numpy(), cv)
+
+
+def test_pattern_bitexact_cfg4a_full_size(ca, cuda):
+    """BASELINE cfg4a's pattern at full size: 512x512, ws = 31 (961 slots per
+    row, 251,920,384 entries), rowPtr and colVal bit-exact."""
+    from circulant_attention import _lib as L
+    from circulant_attention._functions import ptr, stream_ptr
+    P, K = 512 * 512, 31 * 31
+    rowptr = torch.empty((1, P + 1), dtype=torch.int32, device=cuda)
+    colval = torch.empty((1, P * K), dtype=torch.int32, device=cuda)
+    L.check(L.lib.circatt_pattern(2, 512, 512, 31, 1, ptr(rowptr), ptr(colval), stream_ptr()))
+    rp, cv = O.pattern((512, 512), 31, 1)
     assert np.array_equal(rowptr.cpu().numpy(), rp)
     assert np.array_equal(colval.cpu().numpy(), cv)
 
