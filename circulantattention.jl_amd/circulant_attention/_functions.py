@@ -197,12 +197,54 @@ class AxpbyFn(torch.autograd.Function):
         return da, dX, db, dY, None
 
 
+def batch_dot_raw(A, B, nb):
+    """(nb,) per-batch sums of A .* B (B None: of A) over nzval slices, with
+    circatt_batch_dot (double accumulation in a fixed order)."""
+    A = _c(A)
+    B = _c(B) if B is not None else None
+    nnz = A.numel() // nb
+    out = torch.empty((nb,), dtype=torch.float32, device=A.device)
+    wbytes = L.lib.circatt_batch_dot_workspace_bytes(nnz, nb)
+    work = torch.empty(((wbytes + 7) // 8,), dtype=torch.float64, device=A.device)
+    L.check(L.lib.circatt_batch_dot(nnz, nb, ptr(A), ptr(B), ptr(out), ptr(work), wbytes,
+                                    stream_ptr(A.device)), "circatt_batch_dot")
+    return out
+
+
+class BatchDotFn(torch.autograd.Function):
+    """out[b] = sum_i A[b, i] B[b, i] (B None: sum_i A[b, i]) over nb batches
+    of nzval: dot (src/array.jl:83-85), sum(A) and sum(A; dims=(1,2))
+    (src/array.jl:132-177).  Pullback: g_b B and g_b A (circatt_axpby)."""
+
+    @staticmethod
+    def forward(ctx, A, B, nb):
+        A = _c(A)
+        B = _c(B) if B is not None else None
+        ctx.save_for_backward(A, B)
+        ctx.nb = nb
+        return batch_dot_raw(A, B, nb)
+
+    @staticmethod
+    def backward(ctx, g):
+        A, B = ctx.saved_tensors
+        nb = ctx.nb
+        g = _c(g.to(torch.float32))
+        dA = dB = None
+        if B is None:
+            if ctx.needs_input_grad[0]:
+                dA = g.reshape(nb, 1).expand(nb, A.numel() // nb).reshape(A.shape)
+        else:
+            if ctx.needs_input_grad[0]:
+                dA = axpby_raw(g, B, None, None, nb).reshape(A.shape)
+            if ctx.needs_input_grad[1]:
+                dB = axpby_raw(g, A, None, None, nb).reshape(B.shape)
+        return dA, dB, None
+
+
 def batch_dot(A, B, nb):
     """(nb,) per-batch sums of A .* B over nzval slices (the ∂c of the scale
-    rrule, src/rrules.jl:101-104).  Uses circatt_rowsum-free torch reduction of
-    a device product: one elementwise product (circatt_axpby is linear, so the
-    product itself is formed by torch) and a per-batch sum."""
-    return (A.reshape(nb, -1) * B.reshape(nb, -1)).sum(dim=1)
+    rrule, src/rrules.jl:101-104)."""
+    return batch_dot_raw(A, B, nb)
 
 
 class FusedAttentionFn(torch.autograd.Function):

@@ -57,6 +57,8 @@ SIGNATURES = {
     "circatt_rowsum": (_int, [_int, _i64, _i64, _i32, _i64, _p, _p, _p]),
     "circatt_colsum": (_int, [_int, _i64, _i64, _i32, _i64, _p, _p, _p]),
     "circatt_axpby": (_int, [_i64, _i64, _p, _f32, _p, _p, _f32, _p, _p, _p]),
+    "circatt_batch_dot_workspace_bytes": (_i64, [_i64, _i64]),
+    "circatt_batch_dot": (_int, [_i64, _i64, _p, _p, _p, _p, _i64, _p]),
     "circatt_fused_fwd": (_int, [_int, _int, _int, _i64, _i64, _i32, _i64, _i64, _i64, _p, _p,
                                  _p, _p, _p, _p]),
     "circatt_fused_bwd_workspace_bytes": (_i64, [_int, _i64, _i64, _i64, _i64]),

@@ -16,8 +16,8 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib as L
-from ._functions import (AxpbyFn, ApplyFn, FusedAttentionFn, SimilarityFn, SoftmaxFn, geometry,
-                         ptr, require, stream_ptr)
+from ._functions import (AxpbyFn, ApplyFn, BatchDotFn, FusedAttentionFn, SimilarityFn, SoftmaxFn,
+                         geometry, ptr, require, stream_ptr)
 
 
 class AbstractSimilarity:
@@ -268,7 +268,7 @@ class Circulant:
         """dot(X, Y) = dot(X.nzVal, Y.nzVal) (src/array.jl:83-85)."""
         if not self._same(other):
             raise AssertionError("dot needs matching Circulants")
-        return (self.nzval * other.nzval).sum()
+        return BatchDotFn.apply(self.nzval, other.nzval, 1).reshape(())
 
     def sum(self, dims=None):
         """sum(A; dims) (src/array.jl:156-177): dims=None (:) -> scalar,
@@ -277,7 +277,7 @@ class Circulant:
         nsp, n1, n2 = geometry(self.spatial_size)
         rb = tuple(reversed(self.batch))
         if dims is None:
-            return self.sum(2).sum()
+            return BatchDotFn.apply(self.nzval, None, 1).reshape(())
         if isinstance(dims, int):
             dims = (dims,)
         dims = tuple(dims)
@@ -286,7 +286,7 @@ class Circulant:
                                       dims[0] == 1).reshape(
                 *rb, *((self.P, 1) if dims[0] == 1 else (1, self.P)))
         if dims == (1, 2):
-            return self.sum(2).reshape(*rb, -1).sum(dim=-1).reshape(*rb, 1, 1)
+            return BatchDotFn.apply(self.nzval, None, self.nb).reshape(*rb, 1, 1)
         if all(d > 2 for d in dims):
             nz = self.nzval
             axes = tuple(len(rb) - (d - 2) for d in dims)  # Julia dim d -> torch axis

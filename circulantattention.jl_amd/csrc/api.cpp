@@ -270,6 +270,28 @@ int circatt_axpby(int64_t nnz, int64_t nb, const float *alpha, float alpha0, con
                       "circatt_axpby");
 }
 
+int64_t circatt_batch_dot_workspace_bytes(int64_t nnz, int64_t nb) {
+    if (nnz < 0 || nb < 1) return -1;
+    return nb * (int64_t)batch_dot_chunks(nnz) * (int64_t)sizeof(double);
+}
+
+int circatt_batch_dot(int64_t nnz, int64_t nb, const float *X, const float *Y, float *out,
+                      void *workspace, int64_t workspace_bytes, void *stream) {
+    if (nnz < 0 || nb < 1)
+        return fail(CIRCATT_ERR_INVALID, "invalid nnz=%lld / nb=%lld", (long long)nnz, (long long)nb);
+    CIRCATT_NONNULL(X);
+    CIRCATT_NONNULL(out);
+    CIRCATT_NONNULL(workspace);
+    const int64_t need = circatt_batch_dot_workspace_bytes(nnz, nb);
+    if (workspace_bytes < need)
+        return fail(CIRCATT_ERR_INVALID, "workspace of %lld bytes, %lld needed",
+                    (long long)workspace_bytes, (long long)need);
+    if (out == X || out == Y || workspace == X || workspace == Y || workspace == out)
+        return fail(CIRCATT_ERR_INVALID, "out and workspace must not alias X or Y");
+    return hip_result(launch_batch_dot(nnz, nb, X, Y, out, workspace, as_stream(stream)),
+                      "circatt_batch_dot");
+}
+
 static int fused_problem(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int32_t ws,
                          int64_t C, int64_t nheads, int64_t B, FusedProblem &pr) {
     Geom g;

@@ -50,6 +50,11 @@ hipError_t launch_similarity(bool dist, int ncomp, const Geom &g, int C, int64_t
                              const float *x, const float *y, float *nz, hipStream_t s);
 hipError_t launch_sum(bool col, const Geom &g, int64_t nb, const float *nz, float *out,
                       hipStream_t s);
+// out[b] = sum_i X[i, b] * Y[i, b] (Y == nullptr: sum_i X[i, b]); work holds
+// nb * batch_dot_chunks(nnz) doubles
+int batch_dot_chunks(int64_t nnz);
+hipError_t launch_batch_dot(int64_t nnz, int64_t nb, const float *X, const float *Y, float *out,
+                            void *work, hipStream_t s);
 hipError_t launch_axpby(int64_t nnz, int64_t nb, const float *alpha, float alpha0,
                         const float *X, const float *beta, float beta0, const float *Y, float *Z,
                         hipStream_t s);

@@ -450,6 +450,69 @@ __global__ __launch_bounds__(256) void axpby2_kernel(int64_t nnz, const float *_
 }
 
 // ---------------------------------------------------------------------------
+// out[b] = sum_i X[i, b] Y[i, b] (sum_i X[i, b] without Y) over nnz entries per
+// batch, deterministic: workgroup (c, b) reduces chunk c of batch b in double
+// into part[b * nchunk + c], then one workgroup per batch adds its chunks in
+// order.  HBM-bound: each element is read once.
+// ---------------------------------------------------------------------------
+constexpr int kDotThreads = 256;
+
+__device__ __forceinline__ double block_sum_d(double v) {
+    __shared__ double wsum[kDotThreads / 64];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < kDotThreads / 64; ++w) t += wsum[w];
+    return t;
+}
+
+// chunk: entries per workgroup (a multiple of 4 when VEC)
+template <bool VEC, bool HASY>
+__global__ __launch_bounds__(kDotThreads) void batch_dot_part_kernel(int64_t nnz, int64_t chunk,
+                                                                     const float *__restrict__ X,
+                                                                     const float *__restrict__ Y,
+                                                                     double *__restrict__ part) {
+    const int64_t b = blockIdx.y, c = blockIdx.x;
+    const int64_t lo = c * chunk, hi = min(nnz, lo + chunk);
+    const float *x = X + b * nnz;
+    const float *y = HASY ? Y + b * nnz : nullptr;
+    double acc = 0.0;
+    if (VEC) {
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        const f4 *x4 = reinterpret_cast<const f4 *>(x);
+        const f4 *y4 = reinterpret_cast<const f4 *>(y);
+        for (int64_t i = lo / 4 + threadIdx.x; i < hi / 4; i += kDotThreads) {
+            const f4 a = x4[i];
+            if (HASY) {
+                const f4 e = y4[i];
+                acc += ((double)a[0] * e[0] + (double)a[1] * e[1]) +
+                       ((double)a[2] * e[2] + (double)a[3] * e[3]);
+            } else {
+                acc += ((double)a[0] + a[1]) + ((double)a[2] + a[3]);
+            }
+        }
+    } else {
+        for (int64_t i = lo + threadIdx.x; i < hi; i += kDotThreads)
+            acc += HASY ? (double)x[i] * y[i] : (double)x[i];
+    }
+    acc = block_sum_d(acc);
+    if (threadIdx.x == 0) part[b * gridDim.x + c] = acc;
+}
+
+__global__ __launch_bounds__(kDotThreads) void batch_dot_final_kernel(int nchunk,
+                                                                      const double *__restrict__ part,
+                                                                      float *__restrict__ out) {
+    const int64_t b = blockIdx.x;
+    double acc = 0.0;
+    for (int c = threadIdx.x; c < nchunk; c += kDotThreads) acc += part[b * nchunk + c];
+    acc = block_sum_d(acc);
+    if (threadIdx.x == 0) out[b] = (float)acc;
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
 static inline unsigned grid_for(int64_t n, int threads, int64_t cap = 1 << 20) {
@@ -592,6 +655,43 @@ hipError_t launch_axpby(int64_t nnz, int64_t nb, const float *alpha, float alpha
     }
     hipLaunchKernelGGL(axpby_kernel, dim3(grid_for(nnz * nb, 256, 1 << 16)), dim3(256), 0, s,
                        nnz, nb, alpha, alpha0, X, beta, beta0, Y, Z);
+    return hipGetLastError();
+}
+
+int batch_dot_chunks(int64_t nnz) {
+    const int64_t n = (nnz + 65535) / 65536;  // 64 Ki entries per workgroup
+    return (int)std::max<int64_t>(1, std::min<int64_t>(1024, n));
+}
+
+hipError_t launch_batch_dot(int64_t nnz, int64_t nb, const float *X, const float *Y, float *out,
+                            void *work, hipStream_t s) {
+    const int nchunk = batch_dot_chunks(nnz);
+    const bool vec = nnz % 4 == 0 && ((uintptr_t)X | (uintptr_t)Y) % 16 == 0;
+    int64_t chunk = (nnz + nchunk - 1) / nchunk;
+    chunk = (chunk + 3) / 4 * 4;
+    double *part = static_cast<double *>(work);
+    // batches in slices of at most 65535 (grid y)
+    for (int64_t b0 = 0; b0 < nb; b0 += 65535) {
+        const unsigned nbs = (unsigned)std::min<int64_t>(65535, nb - b0);
+        const float *xs = X + b0 * nnz;
+        const float *ys = Y ? Y + b0 * nnz : nullptr;
+        double *ps = part + b0 * nchunk;
+        const dim3 grid((unsigned)nchunk, nbs);
+        if (vec && Y)
+            hipLaunchKernelGGL((batch_dot_part_kernel<true, true>), grid, dim3(kDotThreads), 0, s,
+                               nnz, chunk, xs, ys, ps);
+        else if (vec)
+            hipLaunchKernelGGL((batch_dot_part_kernel<true, false>), grid, dim3(kDotThreads), 0, s,
+                               nnz, chunk, xs, ys, ps);
+        else if (Y)
+            hipLaunchKernelGGL((batch_dot_part_kernel<false, true>), grid, dim3(kDotThreads), 0, s,
+                               nnz, chunk, xs, ys, ps);
+        else
+            hipLaunchKernelGGL((batch_dot_part_kernel<false, false>), grid, dim3(kDotThreads), 0, s,
+                               nnz, chunk, xs, ys, ps);
+        hipLaunchKernelGGL(batch_dot_final_kernel, dim3(nbs), dim3(kDotThreads), 0, s, nchunk, ps,
+                           out + b0);
+    }
     return hipGetLastError();
 }
 

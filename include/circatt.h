@@ -154,6 +154,18 @@ int circatt_axpby(int64_t nnz, int64_t nb, const float *alpha, float alpha0, con
                   const float *beta, float beta0, const float *Y, float *Z, void *stream);
 
 /*
+ * out[b] = sum_i X[i, b] * Y[i, b] over nnz entries per batch (Y == NULL:
+ * sum_i X[i, b]); accumulated in double in a fixed order, so results are
+ * reproducible.  Covers dot(X, Y) (src/array.jl:83-85, nb = 1 over all
+ * batches), sum(A) and sum(A; dims=(1,2)) (src/array.jl:132-177) and the ∂c
+ * of the scale rrule (src/rrules.jl:101-104).  workspace: at least
+ * circatt_batch_dot_workspace_bytes(nnz, nb) bytes of device memory.
+ */
+int64_t circatt_batch_dot_workspace_bytes(int64_t nnz, int64_t nb);
+int circatt_batch_dot(int64_t nnz, int64_t nb, const float *X, const float *Y, float *out,
+                      void *workspace, int64_t workspace_bytes, void *stream);
+
+/*
  * Fused forward of circulant (multi-head) attention without materialising A:
  * for head g of batch b (channels g*dh .. g*dh+dh-1, dh = C/nheads),
  *   y = softmax_rows(scale * sim(q, k)) ⊗ v,   scale = 1/sqrt(dh),

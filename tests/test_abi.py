@@ -121,3 +121,14 @@ def test_math_mode_switch(L):
         expect(L, L.lib.circatt_set_math(-1), L.ERR_INVALID, "math")
     finally:
         L.lib.circatt_set_math(old)
+
+
+def test_batch_dot_validation(L):
+    assert L.lib.circatt_batch_dot_workspace_bytes(1000, 3) == 3 * 8
+    assert L.lib.circatt_batch_dot_workspace_bytes(65536 * 1024 * 4, 2) == 2 * 1024 * 8
+    assert L.lib.circatt_batch_dot_workspace_bytes(-1, 1) == -1
+    rc = L.lib.circatt_batch_dot(100, 2, FAKE, NULL, ctypes.c_void_p(0x2000),
+                                 ctypes.c_void_p(0x3000), 8, NULL)
+    expect(L, rc, L.ERR_INVALID, "workspace")
+    rc = L.lib.circatt_batch_dot(100, 2, NULL, NULL, FAKE, FAKE, 64, NULL)
+    expect(L, rc, L.ERR_INVALID, "X is NULL")

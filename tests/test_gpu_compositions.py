@@ -367,3 +367,52 @@ def test_fused_matches_unfused_full_size(ca, cuda, name):
     assert rel_err(outs[1], outs[0]) < TOL_FWD
     for nm, a, b in zip(("dq", "dk", "dv"), grads[1], grads[0]):
         assert rel_err(a, b) < TOL_GRAD, nm
+
+
+@pytest.mark.parametrize("nnz,nb", [(1, 1), (7, 3), (4096, 2), (65537, 2), (1000003, 1),
+                                    (12_390_400, 1), (300, 70000)])
+@pytest.mark.parametrize("with_y", [False, True])
+def test_batch_dot(cuda, nnz, nb, with_y):
+    """circatt_batch_dot against float64 sums: odd and aligned lengths, more
+    chunks than one workgroup, more batches than one grid row (70000), and
+    operands offset by one float (no 16-byte alignment)."""
+    from circulant_attention import _lib as L
+    from circulant_attention._functions import ptr, stream_ptr
+    if nnz * nb > 30_000_000:
+        pytest.skip("size")
+    g = torch.Generator(device=cuda)
+    g.manual_seed(nnz + nb)
+    X = torch.randn(nnz * nb + 1, device=cuda, generator=g)[1:]  # misaligned by 4 bytes
+    Y = torch.randn(nnz * nb, device=cuda, generator=g) if with_y else None
+    out = torch.empty(nb, device=cuda)
+    wb = L.lib.circatt_batch_dot_workspace_bytes(nnz, nb)
+    work = torch.empty((wb + 7) // 8, dtype=torch.float64, device=cuda)
+    L.check(L.lib.circatt_batch_dot(nnz, nb, ptr(X), ptr(Y), ptr(out), ptr(work), wb,
+                                    stream_ptr()))
+    x = X.cpu().numpy().astype(np.float64).reshape(nb, nnz)
+    ref = (x * Y.cpu().numpy().astype(np.float64).reshape(nb, nnz)).sum(1) if with_y else x.sum(1)
+    scale = (np.abs(x) * (np.abs(Y.cpu().numpy().reshape(nb, nnz)) if with_y else 1)).sum(1)
+    assert np.all(np.abs(out.cpu().numpy() - ref) <= 1e-6 * scale + 1e-30)
+    out2 = torch.empty_like(out)
+    L.check(L.lib.circatt_batch_dot(nnz, nb, ptr(X), ptr(Y), ptr(out2), ptr(work), wb,
+                                    stream_ptr()))
+    assert torch.equal(out, out2)  # fixed summation order
+
+
+def test_dot_and_sums_carry_gradients(ca, cuda):
+    """dot(X, Y), sum(A) and sum(A; dims=(1,2)) are differentiable: d/dX of
+    dot is Y, of the sums a broadcast of the cotangent."""
+    dims, ws, nh, B = (8, 6), 3, 2, 2
+    a, b = seeded(980, (B, nh, 48, 9)), seeded(981, (B, nh, 48, 9))
+    ta = torch.from_numpy(a).to(cuda).requires_grad_(True)
+    tb = torch.from_numpy(b).to(cuda).requires_grad_(True)
+    A, Bm = ca.Circulant(ta, ws, dims), ca.Circulant(tb, ws, dims)
+    A.dot(Bm).backward()
+    assert torch.equal(ta.grad, tb.detach()) and torch.equal(tb.grad, ta.detach())
+    ta.grad = None
+    (A.sum() * 3).backward()
+    assert torch.all(ta.grad == 3)
+    ta.grad = None
+    w = torch.arange(B * nh, dtype=torch.float32, device=cuda).reshape(B, nh, 1, 1)
+    (A.sum((1, 2)) * w).sum().backward()
+    assert torch.equal(ta.grad, w.expand(B, nh, 48, 9))
