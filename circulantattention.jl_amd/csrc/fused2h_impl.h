@@ -90,23 +90,25 @@ __device__ __forceinline__ float opaque_neg_one() {
     return c;
 }
 // hi = f16(x), lo = f16(x - hi): one packed conversion for hi, then
-// v_fma_mixlo_f16 / v_fma_mixhi_f16 take x - hi exactly in Float32 from the
-// packed halves and round it once into each half of lo.  Only empty asm
-// statements steer the instruction selection (the first keeps hi one packed
-// value for both mixes, the second keeps the two halves of lo from being
-// combined into two mix_f32 and a packed conversion), so the mixes are
-// ordinary compiler instructions and the compiler inserts the wait states
+// v_fma_mix_f32 takes x - hi exactly in Float32 from each packed half (the
+// difference is representable), and a second packed conversion rounds the two
+// differences once into lo.  On gfx950 the packed conversions and
+// v_fma_mix_f32 issue at half rate, v_fma_mixlo_f16 / v_fma_mixhi_f16 (which
+// would round into the halves of lo directly) at quarter rate: 8.4 against
+// 10.2 cycles per value of a SIMD shared by four waves, with the same halves.
+// Only empty asm statements steer the instruction selection (the first keeps
+// hi one packed value, the second keeps the Float32 differences), so these
+// are ordinary compiler instructions and the compiler inserts the wait states
 // they need next to matrix-core operations.
 __device__ __forceinline__ void split2(float x0, float x1, h2 &hi, h2 &lo) {
     const float m1 = opaque_neg_one();
     h2 h = h2{(_Float16)x0, (_Float16)x1};
     asm("" : "+v"(h));
-    h2 l;
-    l[0] = (_Float16)__builtin_fmaf((float)h[0], m1, x0);
-    asm("" : "+v"(l));
-    l[1] = (_Float16)__builtin_fmaf((float)h[1], m1, x1);
+    float d0 = __builtin_fmaf((float)h[0], m1, x0);
+    float d1 = __builtin_fmaf((float)h[1], m1, x1);
+    asm("" : "+v"(d0), "+v"(d1));
     hi = h;
-    lo = l;
+    lo = h2{(_Float16)d0, (_Float16)d1};
 }
 // 4 values -> hi, lo as one half of a pair operand
 __device__ __forceinline__ void split4(const float (&x)[4], h4 &hi, h4 &lo) {
@@ -127,6 +129,21 @@ __device__ __forceinline__ h4 ldtr(const char *p) {
 }
 __device__ __forceinline__ h8 cat(h4 a, h4 b) {
     return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Wave priority over the N pair steps of an item's walk: 3 for the first
+// quarter, then 2, 1, 0.  A SIMD's arbiter issues for the oldest of its
+// highest-priority waves; with equal priorities the four waves of a SIMD end
+// an item's walk in age order (forward at cfg3 on gfx950: after 138k, 191k,
+// 241k and 284k cycles of a 336k-cycle launch) and the last runs alone, with
+// no latency hidden, while the others wait at the barrier.  Lowering a wave's
+// priority as it advances lets the waves behind it issue, so the four end
+// close together (forward 348k -> 324k cycles, query-centric pass 437k ->
+// 404k).  The key-centric pass gains 3% in cycles and loses it to a lower
+// clock, and keeps equal priorities.
+template <int I, int N>
+__device__ __forceinline__ void walk_prio() {
+    if constexpr (I * 4 % N < 4) __builtin_amdgcn_s_setprio(3 - I * 4 / N);
 }
 
 constexpr int KS = 40;  // halves per pixel slot: 16 hi, 16 lo, 8 pad (80 bytes)
@@ -701,6 +718,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     constexpr int i = decltype(I)::value;
                     constexpr int pi = ord(i);
                     FWD_FENCE_A();
+                    walk_prio<i, NPAIR>();
                     if constexpr (pi == PFP) prefetch();
                     POps na, nv;
                     if constexpr (i + 2 < NPAIR) load_a(std::integral_constant<int, ord(i + 2)>{}, na);
@@ -789,6 +807,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 constexpr bool has1 = b0 + 1 < NBLK;
                 constexpr int b1 = has1 ? b0 + 1 : b0;
                 if constexpr (pi % CIRCATT_F2H_BWD_FSTEP == 0) BLOCK_FENCE();
+                if constexpr (MODE == BWDQ) walk_prio<pi, NPAIR>();
                 if constexpr (pi == PFP) prefetch();
                 float p[2][4], ds[2][4];
                 auto blk = [&](auto B, int u) {
