@@ -36,6 +36,25 @@ __host__ __device__ __forceinline__ int pmod(int a, int n) {
     return r < 0 ? r + n : r;
 }
 
+// Division by a run-time constant d >= 1 as a multiply-high and a shift (the
+// round-up method of Granlund and Montgomery, "Division by invariant integers
+// using multiplication", PLDI 1994): l = ceil(log2 d),
+// m = floor(2^32 (2^l - d) / d) + 1, and n / d = (mulhi(n, m) + n) >> l for
+// 0 <= n < 2^31 (the sum stays below 2^32).  Kernels divide wave-uniform
+// indices this way in scalar instructions instead of the vector expansion of
+// an integer division.
+struct FastDiv {
+    uint32_t m, l;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    return FastDiv{(uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1), l};
+}
+__device__ __forceinline__ int fdiv(int n, FastDiv d) {
+    return (int)((__umulhi((uint32_t)n, d.m) + (uint32_t)n) >> d.l);
+}
+
 // shift s(j) of one dimension, j is 1-based (src/circulant.jl:10-14, 30-39)
 __host__ __device__ __forceinline__ int slot_shift(int j1, int N, int p) {
     if (j1 <= p) return j1 - p - 1;

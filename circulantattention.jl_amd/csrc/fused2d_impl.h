@@ -222,6 +222,7 @@ struct Args {
     float scale, c2;      // similarity scale, scale * log2(e)
     int nunits;           // (head, batch) units
     int tiles_h, tiles_w, nitems, per_xcd;  // set by launch()
+    FastDiv div_tiles, div_th;  // by tiles_h * tiles_w and by tiles_h (split-half launch)
 };
 
 // Buffer resource over `bytes` bytes at p (loads beyond it return 0).

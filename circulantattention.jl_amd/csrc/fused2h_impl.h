@@ -244,9 +244,10 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     // forward: pair chunks whose scores are held in registers at once
     constexpr int NCH = (MODE == FWD && NPAIR > 6) ? 2 : 1;
     constexpr int CHP = (NPAIR + NCH - 1) / NCH;
-    // pair at which the next item's loads are issued (the forward issues them
-    // in its apply walk; with two chunks, at the last pair of the first, so
-    // that the loads are in flight over the whole second chunk).  Backward:
+    // pair at which the next item's loads are issued (the streamed forward
+    // issues them before its walk; otherwise the forward issues them in its
+    // apply walk, with two chunks at the last pair of the first, so that the
+    // loads are in flight over the whole second chunk).  Backward:
     // pair NPAIR / PFD; measured on gfx950, the query-centric pass is fastest
     // with its loads issued at a quarter of the walk (200 against 205 us at
     // cfg3), the key-centric pass at half of it
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     // forward with a reference maximum from the central block row (rows 8, 9
     // of the key region lie in every query's window when 2P >= 9)
     constexpr bool STREAM = MODE == FWD && NKW == 2 && P >= 5;
-    constexpr int PFP = STREAM                    ? 1
+    constexpr int PFP = STREAM                    ? 0
                         : (MODE == FWD && NCH == 2) ? CHP - 1
                         : MODE == BWDQ              ? NPAIR / CIRCATT_F2H_BWDQ_PFD
                                                     : NPAIR / CIRCATT_F2H_BWD_PFD;
@@ -313,21 +314,23 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         rvalid = rh < a.n1 && rw < a.n2;
         rpix = rvalid ? rh + a.n1 * rw : 0;
     };
+    // item -> (head, batch) unit and tile origin; wave-uniform, so scalar
+    // instructions with the launch's precomputed divisors
     auto decode = [&](int item, int &unit, int &h0, int &w0) {
-        const int ntiles = a.tiles_h * a.tiles_w;
-        unit = item / ntiles;
-        const int tile = item - unit * ntiles;
-        const int th = tile % a.tiles_h;
-        h0 = th * G::TH;
-        w0 = (tile - th) / a.tiles_h * G::TW;
+        unit = fdiv(item, a.div_tiles);
+        const int tile = item - unit * (a.tiles_h * a.tiles_w);
+        const int tw = fdiv(tile, a.div_th);
+        h0 = (tile - tw * a.tiles_h) * G::TH;
+        w0 = tw * G::TW;
     };
     const bool big = a.n1 >= HH && a.n2 >= HWD;
     const int px = threadIdx.x;
     const int kw = px / HH, kh = px - kw * HH;
-    auto load_stage = [&](int item) {
-        int unit, h0, w0;
-        decode(item, unit, h0, w0);
-        const int hsh = pmod(h0 - P, a.n1), wsh = pmod(w0 - P, a.n2);
+    auto load_stage = [&](int unit, int h0, int w0) {
+        // halo origin (h0 - P, w0 - P) mod (n1, n2), uniform
+        int hsh = h0 - P, wsh = w0 - P;
+        while (hsh < 0) hsh += a.n1;
+        while (wsh < 0) wsh += a.n2;
         const int64_t uoff = (int64_t)unit * a.unit_stride;
         const auto r0 = f2d::rsrc((KV ? a.q : a.k) + uoff, ubytes);
         const auto r1 = f2d::rsrc((KV ? a.dy : a.v) + uoff, ubytes);
@@ -364,9 +367,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             hs1 = f2d::bload(f2d::rsrc(a.dbuf + soff, a.P * 4), gp * 4, 0);
         }
     };
-    auto load_regs = [&](int item) {
-        int unit, h0, w0;
-        decode(item, unit, h0, w0);
+    auto load_regs = [&](int unit, int h0, int w0) {
         bool rvalid;
         int rpix;
         regpix(h0, w0, rvalid, rpix);
@@ -391,13 +392,13 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     if (item >= a.nitems) return;
     unsigned *const xwords = reinterpret_cast<unsigned *>(lds + L::OX);
     if (threadIdx.x < 4) xwords[threadIdx.x] = 0u;
-    load_stage(item);
-    load_regs(item);
+    int unit, h0, w0;
+    decode(item, unit, h0, w0);
+    load_stage(unit, h0, w0);
+    load_regs(unit, h0, w0);
     __syncthreads();  // exchange words cleared before any item's maxima
 
     while (true) {
-        int unit, h0, w0;
-        decode(item, unit, h0, w0);
         bool rvalid;
         int rpix;
         regpix(h0, w0, rvalid, rpix);
@@ -541,10 +542,11 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         const bool has_next = nitem < a.nitems;
         // unconditional (the last item loads itself again), so that the
         // prefetch registers are dead between the staging and this point
+        int xunit = unit, xh0 = h0, xw0 = w0;
+        if (has_next) decode(nitem, xunit, xh0, xw0);
         auto prefetch = [&]() {
-            const int li = has_next ? nitem : item;
-            load_stage(li);
-            load_regs(li);
+            load_stage(xunit, xh0, xw0);
+            load_regs(xunit, xh0, xw0);
         };
 
         // score-type product of block b (16 elements x 16 register pixels)
@@ -694,6 +696,10 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             // a scores-only pass.  On typical data the redo never runs.
             constexpr int PC = STREAM ? 4 : 0;
             uint64_t over = 1;
+            // streamed configurations issue the next item's loads before the
+            // walk, on both of its paths alike (loads issued inside each path
+            // make the compiler copy the 36 prefetch registers at the merge)
+            if constexpr (STREAM) prefetch();
             if constexpr (STREAM) {
               if (!slow) {
                 // Walk order: PC, then the other pairs.  Skewed by one pair:
@@ -719,7 +725,6 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     constexpr int pi = ord(i);
                     FWD_FENCE_A();
                     walk_prio<i, NPAIR>();
-                    if constexpr (pi == PFP) prefetch();
                     POps na, nv;
                     if constexpr (i + 2 < NPAIR) load_a(std::integral_constant<int, ord(i + 2)>{}, na);
                     if constexpr (i + 1 < NPAIR) load_v(std::integral_constant<int, ord(i + 1)>{}, nv);
@@ -748,14 +753,13 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
               }
             }
             // exact row maximum, then one walk with every score <= m (the slow
-            // walk always takes this form; the streamed walk skipped, it
-            // issues the next item's loads here)
+            // walk always takes this form)
             auto twopass = [&](auto SLOW) {
                 constexpr bool slw = decltype(SLOW)::value;
                 float mx = -INFINITY;
                 static_for<0, NPAIR>([&](auto PI) {
                     FWD_FENCE_A();
-                    if constexpr ((slw || !STREAM) && decltype(PI)::value == PFP) prefetch();
+                    if constexpr (!STREAM && decltype(PI)::value == PFP) prefetch();
                     f4 sv[2];
                     scores(PI, std::false_type{}, sv, k + 1, SLOW);
                     mx = fmaxf(mx, pair_max(sv));
@@ -775,8 +779,11 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             } else if (over != 0) {
                 twopass(std::false_type{});
             }
+            // l >= 1 (the element at m contributes exp2(0)); v_rcp_f32 is
+            // within 1 ulp, where an IEEE division would add a dozen vector
+            // instructions per item
             const float l = gsum(lsum);
-            const float inv = 1.f / l;
+            const float inv = __builtin_amdgcn_rcpf(l);
             if (rvalid) {
                 float *yb = a.yout + uoff;
 #pragma unroll
@@ -908,6 +915,9 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         if (!has_next) break;
         ++k;
         item = nitem;
+        unit = xunit;
+        h0 = xh0;
+        w0 = xw0;
     }
 }
 
@@ -929,6 +939,8 @@ hipError_t launch(const Args &a0, int cus, hipStream_t s) {
     a.tiles_w = (a.n2 + G::TW - 1) / G::TW;
     const int64_t nitems = (int64_t)a.tiles_h * a.tiles_w * a.nunits;
     if (nitems <= 0 || nitems > INT32_MAX / 2) return hipErrorNotSupported;
+    a.div_tiles = make_fastdiv((uint32_t)(a.tiles_h * a.tiles_w));
+    a.div_th = make_fastdiv((uint32_t)a.tiles_h);
     a.nitems = (int)nitems;
     a.per_xcd = (int)((nitems + 7) / 8);
     int64_t grid = std::min<int64_t>(cus, 8LL * a.per_xcd);
