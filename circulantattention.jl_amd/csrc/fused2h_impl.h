@@ -46,6 +46,21 @@
 #ifndef CIRCATT_F2H_FWD_FENCE
 #define CIRCATT_F2H_FWD_FENCE 2
 #endif
+// Per-wave phase timing, off by default (microbench/phase_timing.py builds a
+// library with it on).  Every wave sums s_memtime spans of four phases over
+// its items: staging (without the barriers), the barrier after the maxima, the
+// barrier after the staging, and the walk with its epilogue.  Wave w of
+// workgroup b < 8 writes the four sums (as 32-bit integers) to floats
+// 4 (16 b + w) .. + 3 past the end of its output (y, dq or dk: offset
+// unit_stride * nunits), which the caller must allocate.
+#ifndef CIRCATT_F2H_PHASE
+#define CIRCATT_F2H_PHASE 0
+#endif
+#if CIRCATT_F2H_PHASE
+#define F2H_PHASE(...) __VA_ARGS__
+#else
+#define F2H_PHASE(...)
+#endif
 // bit 0: between score blocks, bit 1: between apply pairs
 #if CIRCATT_F2H_FWD_FENCE & 1
 #define FWD_FENCE_S() __builtin_amdgcn_sched_barrier(0)
@@ -390,6 +405,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     int k = 0;
     int item = f2d::item_of(a, 0);
     if (item >= a.nitems) return;
+    F2H_PHASE(uint64_t phase[4] = {0, 0, 0, 0};)
     unsigned *const xwords = reinterpret_cast<unsigned *>(lds + L::OX);
     if (threadIdx.x < 4) xwords[threadIdx.x] = 0u;
     int unit, h0, w0;
@@ -399,6 +415,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     __syncthreads();  // exchange words cleared before any item's maxima
 
     while (true) {
+        F2H_PHASE(const uint64_t pt0 = __builtin_readcyclecounter();)
         bool rvalid;
         int rpix;
         regpix(h0, w0, rvalid, rpix);
@@ -432,7 +449,9 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                                            __HIP_MEMORY_SCOPE_WORKGROUP);
             }
         }
+        F2H_PHASE(const uint64_t pta = __builtin_readcyclecounter();)
         __syncthreads();  // the previous item's LDS reads are done; maxima in
+        F2H_PHASE(const uint64_t ptb = __builtin_readcyclecounter(); phase[1] += ptb - pta;)
         const unsigned b0 = __builtin_amdgcn_readfirstlane(xwords[0]) & 255u;
         const unsigned b1 = __builtin_amdgcn_readfirstlane(xwords[1]) & 255u;
         const unsigned b2 = KV ? __builtin_amdgcn_readfirstlane(xwords[2]) & 255u : 127u;
@@ -536,7 +555,10 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) reg0[r] = __shfl((g & 2) ? nr0[4 + r] : nr0[r], srcl);
         }
+        F2H_PHASE(const uint64_t ptc = __builtin_readcyclecounter();)
         __syncthreads();  // halo staged
+        F2H_PHASE(const uint64_t pt1 = __builtin_readcyclecounter(); phase[2] += pt1 - ptc;
+                  phase[0] += (ptc - pt0) - (ptb - pta);)
 
         const int nitem = f2d::item_of(a, k + 1);
         const bool has_next = nitem < a.nitems;
@@ -912,6 +934,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             }
         }
 
+        F2H_PHASE(phase[3] += __builtin_readcyclecounter() - pt1;)
         if (!has_next) break;
         ++k;
         item = nitem;
@@ -919,6 +942,14 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         h0 = xh0;
         w0 = xw0;
     }
+#if CIRCATT_F2H_PHASE
+    if (blockIdx.x < 8 && lane == 0) {
+        float *o = (MODE == FWD ? a.yout : MODE == BWDQ ? a.dq : a.dk) +
+                   (int64_t)a.unit_stride * a.nunits + 4 * (16 * blockIdx.x + wv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = __uint_as_float((unsigned)phase[i]);
+    }
+#endif
 }
 
 template <int P, bool CPLX, bool DIST, int MODE>

@@ -1,0 +1,118 @@
+"""Per-wave phase timing of the split-half fused kernels at cfg3.
+
+A copy of libcircatt built with CIRCATT_F2H_PHASE=1 makes every wave of
+kernel2h sum s_memtime spans of four phases over its items (staging, the two
+barriers, the walk with its epilogue) and lets the waves of workgroups 0..7
+write the sums past the end of their output.  This script builds that copy
+(on a machine with hipcc; the other objects come from the in-tree build) and,
+on an MI355X, runs the three cfg3 kernels with enlarged outputs and prints
+the phases per wave slot.
+
+    python circulantattention.jl_amd/microbench/phase_timing.py --build
+    python circulantattention.jl_amd/microbench/phase_timing.py
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+LIB = os.path.join(HERE, "libcircatt_phase.so")
+F2H = ("fused2h_fwd.hip", "fused2h_bwdq.hip", "fused2h_bwdkv.hip")
+
+
+def build() -> None:
+    sys.path.insert(0, PKG)
+    import build as B
+
+    B.build()  # the in-tree objects the copy links against
+    objs = [os.path.join(B.OBJ, os.path.splitext(s)[0] + ".o") for s in B.SOURCES
+            if s not in F2H]
+    out = []
+    for src in F2H:
+        o = os.path.join(HERE, os.path.splitext(src)[0] + "_phase.o")
+        subprocess.run([B.HIPCC, *B.FLAGS, "-DCIRCATT_F2H_PHASE=1", "-c",
+                        os.path.join(B.CSRC, src), "-o", o], check=True)
+        out.append(o)
+    subprocess.run([B.HIPCC, f"--offload-arch={B.ARCH}", "-shared", "-fPIC", "-o", LIB,
+                    *out, *objs], check=True)
+    for o in out:
+        os.remove(o)
+    print("built", LIB)
+
+
+def run() -> None:
+    import torch  # before the library: the process then uses torch's HIP runtime
+
+    sys.path.insert(0, PKG)
+    from circulant_attention import _lib as L
+    from circulant_attention._functions import ptr
+
+    lib = ctypes.CDLL(LIB)
+    for name, (res, args) in L.SIGNATURES.items():
+        f = getattr(lib, name)
+        f.restype, f.argtypes = res, args
+    n1 = n2 = 256
+    C, B, nh, ws = 64, 4, 4, 15
+    P = n1 * n2
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1003)
+    shape = (B, C, n2, n1)
+    q, k, v, dy = (torch.randn(shape, device=dev, generator=g) for _ in range(4))
+    N, EX = q.numel(), 8 * 16 * 4
+    yb, dqb, dkb = (torch.zeros(N + EX, device=dev) for _ in range(3))
+    dv = torch.empty_like(q)
+    lse = torch.empty((B * nh, P), device=dev)
+    wb = lib.circatt_fused_bwd_workspace_bytes(2, n1, n2, nh, B)
+    work = torch.empty((wb // 4,), device=dev)
+    s = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def fwd():
+        L.check(lib.circatt_fused_fwd(0, L.F32, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k), ptr(v),
+                                      ptr(yb), ptr(lse), s))
+
+    def bwd_dq():
+        L.check(lib.circatt_fused_bwd_dq(0, L.F32, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k), ptr(v),
+                                         ptr(yb), ptr(dy), ptr(lse), ptr(dqb), ptr(work), wb, s))
+
+    def bwd_dkdv():
+        L.check(lib.circatt_fused_bwd_dkdv(0, L.F32, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
+                                           ptr(v), ptr(dy), ptr(lse), ptr(dkb), ptr(dv), ptr(work),
+                                           wb, s))
+
+    for _ in range(400):  # clocks to steady state
+        fwd()
+        bwd_dq()
+        bwd_dkdv()
+    torch.cuda.synchronize()
+    print("cfg3, cycles summed over each wave's items (mean over the 8 sampled workgroups)")
+    for name, f, buf in (("forward", fwd, yb), ("query-centric", bwd_dq, dqb),
+                         ("key-centric", bwd_dkdv, dkb)):
+        for _ in range(50):
+            f()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        f()
+        e1.record()
+        torch.cuda.synchronize()
+        t = buf[N:].view(torch.int32).cpu().numpy().reshape(8, 16, 4).astype("int64")
+        tot = t.sum(axis=2)
+        m = t.mean(axis=(0, 1))
+        print(f"{name}: kernel {e0.elapsed_time(e1) * 1e3:.1f} us, "
+              f"{tot.max() / (e0.elapsed_time(e1) * 1e-3) / 1e9:.2f} GHz (cycles / time)")
+        print("  phases (mean over waves): staging %.0f, barrier after maxima %.0f, "
+              "barrier after staging %.0f, walk+epilogue %.0f" % tuple(m))
+        print("  walk+epilogue per wave slot 0..15 (mean over workgroups):",
+              [int(x) for x in t[:, :, 3].mean(axis=0)])
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--build", action="store_true")
+    args = ap.parse_args()
+    build() if args.build else run()
