@@ -156,9 +156,13 @@ __device__ __forceinline__ h8 cat(h4 a, h4 b) {
 // close together (forward 348k -> 324k cycles, query-centric pass 437k ->
 // 404k).  The key-centric pass gains 3% in cycles and loses it to a lower
 // clock, and keeps equal priorities.
+// (CIRCATT_F2H_PRIO=0 keeps equal priorities, for the comparison)
+#ifndef CIRCATT_F2H_PRIO
+#define CIRCATT_F2H_PRIO 1
+#endif
 template <int I, int N>
 __device__ __forceinline__ void walk_prio() {
-    if constexpr (I * 4 % N < 4) __builtin_amdgcn_s_setprio(3 - I * 4 / N);
+    if constexpr (CIRCATT_F2H_PRIO && I * 4 % N < 4) __builtin_amdgcn_s_setprio(3 - I * 4 / N);
 }
 
 constexpr int KS = 40;  // halves per pixel slot: 16 hi, 16 lo, 8 pad (80 bytes)

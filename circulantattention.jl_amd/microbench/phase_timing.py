@@ -8,8 +8,11 @@ write the sums past the end of their output.  This script builds that copy
 on an MI355X, runs the three cfg3 kernels with enlarged outputs and prints
 the phases per wave slot.
 
-    python circulantattention.jl_amd/microbench/phase_timing.py --build
-    python circulantattention.jl_amd/microbench/phase_timing.py
+    python circulantattention.jl_amd/microbench/phase_timing.py --build [--no-prio]
+    python circulantattention.jl_amd/microbench/phase_timing.py [--no-prio]
+
+--no-prio builds and runs a second copy with CIRCATT_F2H_PRIO=0 (equal wave
+priorities over the walk).
 """
 from __future__ import annotations
 
@@ -21,11 +24,14 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
-LIB = os.path.join(HERE, "libcircatt_phase.so")
 F2H = ("fused2h_fwd.hip", "fused2h_bwdq.hip", "fused2h_bwdkv.hip")
 
 
-def build() -> None:
+def lib_path(no_prio: bool) -> str:
+    return os.path.join(HERE, "libcircatt_phase_noprio.so" if no_prio else "libcircatt_phase.so")
+
+
+def build(no_prio: bool) -> None:
     sys.path.insert(0, PKG)
     import build as B
 
@@ -34,25 +40,27 @@ def build() -> None:
             if s not in F2H]
     out = []
     for src in F2H:
-        o = os.path.join(HERE, os.path.splitext(src)[0] + "_phase.o")
-        subprocess.run([B.HIPCC, *B.FLAGS, "-DCIRCATT_F2H_PHASE=1", "-c",
+        o = os.path.join(HERE, os.path.splitext(src)[0] + ("_np" if no_prio else "") + "_phase.o")
+        defs = ["-DCIRCATT_F2H_PHASE=1"] + (["-DCIRCATT_F2H_PRIO=0"] if no_prio else [])
+        subprocess.run([B.HIPCC, *B.FLAGS, *defs, "-c",
                         os.path.join(B.CSRC, src), "-o", o], check=True)
         out.append(o)
-    subprocess.run([B.HIPCC, f"--offload-arch={B.ARCH}", "-shared", "-fPIC", "-o", LIB,
+    lib = lib_path(no_prio)
+    subprocess.run([B.HIPCC, f"--offload-arch={B.ARCH}", "-shared", "-fPIC", "-o", lib,
                     *out, *objs], check=True)
     for o in out:
         os.remove(o)
-    print("built", LIB)
+    print("built", lib)
 
 
-def run() -> None:
+def run(no_prio: bool) -> None:
     import torch  # before the library: the process then uses torch's HIP runtime
 
     sys.path.insert(0, PKG)
     from circulant_attention import _lib as L
     from circulant_attention._functions import ptr
 
-    lib = ctypes.CDLL(LIB)
+    lib = ctypes.CDLL(lib_path(no_prio))
     for name, (res, args) in L.SIGNATURES.items():
         f = getattr(lib, name)
         f.restype, f.argtypes = res, args
@@ -90,7 +98,8 @@ def run() -> None:
         bwd_dq()
         bwd_dkdv()
     torch.cuda.synchronize()
-    print("cfg3, cycles summed over each wave's items (mean over the 8 sampled workgroups)")
+    print("cfg3, cycles summed over each wave's items (mean over the 8 sampled workgroups)"
+          + (", equal wave priorities" if no_prio else ""))
     for name, f, buf in (("forward", fwd, yb), ("query-centric", bwd_dq, dqb),
                          ("key-centric", bwd_dkdv, dkb)):
         for _ in range(50):
@@ -114,5 +123,6 @@ def run() -> None:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--build", action="store_true")
+    ap.add_argument("--no-prio", action="store_true")
     args = ap.parse_args()
-    build() if args.build else run()
+    build(args.no_prio) if args.build else run(args.no_prio)
