@@ -149,13 +149,14 @@ __device__ __forceinline__ h8 cat(h4 a, h4 b) {
 // Wave priority over the N pair steps of an item's walk: 3 for the first
 // quarter, then 2, 1, 0.  A SIMD's arbiter issues for the oldest of its
 // highest-priority waves; with equal priorities the four waves of a SIMD end
-// an item's walk in age order (forward at cfg3 on gfx950: after 138k, 191k,
-// 241k and 284k cycles of a 336k-cycle launch) and the last runs alone, with
-// no latency hidden, while the others wait at the barrier.  Lowering a wave's
-// priority as it advances lets the waves behind it issue, so the four end
-// close together (forward 348k -> 324k cycles, query-centric pass 437k ->
-// 404k).  The key-centric pass gains 3% in cycles and loses it to a lower
-// clock, and keeps equal priorities.
+// an item's walk in age order (forward at cfg3 on gfx950: the four slot
+// groups after 128k, 184k, 235k and 277k cycles of walk) and the last runs
+// its tail alone, with no latency hidden, while the others wait at the
+// barrier.  Lowering a wave's priority as it advances lets the waves behind
+// it issue (164k .. 260k), which cuts the cycles per launch (forward 331k ->
+// 317k per wave, query-centric pass 346k -> 324k); the clock drops with the
+// higher utilisation, so the gain in time is smaller.  The key-centric pass
+// keeps equal priorities: there the lower clock cancelled the gain.
 // (CIRCATT_F2H_PRIO=0 keeps equal priorities, for the comparison)
 #ifndef CIRCATT_F2H_PRIO
 #define CIRCATT_F2H_PRIO 1
