@@ -18,6 +18,9 @@ Julia name              -> here
                         -> same names
 Gradients flow through torch.autograd with the reference's rrules
 (src/rrules.jl); Zygote.accum's role is played by autograd accumulation.
+
+`layers` holds downstream modules in the manner of GroupCDL (README.md:33-38):
+CircAttBlock and GroupThresholding, on channels-last feature maps.
 """
 from . import _lib
 from .circulant import (AbstractSimilarity, Circulant, DistanceSimilarity, DotSimilarity, Otimes,
@@ -27,6 +30,8 @@ from .circulant import (AbstractSimilarity, Circulant, DistanceSimilarity, DotSi
                         circulant_similarity_, circulant_transposed_attention, otimes, scale,
                         kernel_length, softmax, softmax_, spatial_dims, spatial_size)
 
+from .layers import CircAttBlock, GroupThresholding  # noqa: E402
+
 Circulant.__matmul__ = lambda A, x: otimes(A, x)
 
 __all__ = [
@@ -35,4 +40,5 @@ __all__ = [
     "circulant_mh_adjacency", "circulant_mh_attention", "circulant_mh_transposed_attention",
     "circulant_similarity", "circulant_similarity_", "circulant_transposed_attention", "otimes",
     "kernel_length", "scale", "softmax", "softmax_", "spatial_dims", "spatial_size",
+    "CircAttBlock", "GroupThresholding",
 ]

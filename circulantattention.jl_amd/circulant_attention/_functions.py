@@ -250,35 +250,41 @@ def batch_dot(A, B, nb):
 class FusedAttentionFn(torch.autograd.Function):
     """y = softmax(scale*sim(q,k)) ⊗ v without materialising A
     (circatt_fused_fwd / circatt_fused_bwd).  Same value and gradients as the
-    composition circulant_adjacency -> ⊗ of src/attention.jl:19-42."""
+    composition circulant_adjacency -> ⊗ of src/attention.jl:19-42.
+
+    Planar tensors are (B, C, *reversed(spatial)) (the reference's Julia
+    (spatial..., C, B)); with channels_last they are (B, *reversed(spatial), C)
+    (Julia (C, spatial..., B)) and the kernels read and write that layout."""
 
     @staticmethod
-    def forward(ctx, kind, q, k, v, spatial, ws, nheads):
+    def forward(ctx, kind, q, k, v, spatial, ws, nheads, channels_last=False):
         q, k, v = _c(q), _c(k), _c(v)
         nsp, n1, n2 = geometry(spatial)
-        B, C = q.shape[0], q.shape[1]
+        B = q.shape[0]
+        C = q.shape[-1] if channels_last else q.shape[1]
         P = int(math.prod(spatial))
+        code = dtype_code(q) | (L.CHANNELS_LAST if channels_last else 0)
         y = torch.empty_like(q)
         lse = torch.empty((B * nheads, P), dtype=torch.float32, device=q.device)
-        L.check(L.lib.circatt_fused_fwd(kind, dtype_code(q), nsp, n1, n2, ws, C, nheads, B,
+        L.check(L.lib.circatt_fused_fwd(kind, code, nsp, n1, n2, ws, C, nheads, B,
                                         ptr(q), ptr(k), ptr(v), ptr(y), ptr(lse),
                                         stream_ptr(q.device)), "circatt_fused_fwd")
         ctx.save_for_backward(q, k, v, y, lse)
-        ctx.meta = (kind, spatial, ws, nheads)
+        ctx.meta = (kind, spatial, ws, nheads, C, code)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         q, k, v, y, lse = ctx.saved_tensors
-        kind, spatial, ws, nheads = ctx.meta
+        kind, spatial, ws, nheads, C, code = ctx.meta
         nsp, n1, n2 = geometry(spatial)
-        B, C = q.shape[0], q.shape[1]
+        B = q.shape[0]
         dy = _c(dy)
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         wbytes = L.lib.circatt_fused_bwd_workspace_bytes(nsp, n1, n2, nheads, B)
         ws_buf = torch.empty((wbytes // 4,), dtype=torch.float32, device=q.device)
-        L.check(L.lib.circatt_fused_bwd(kind, dtype_code(q), nsp, n1, n2, ws, C, nheads, B,
+        L.check(L.lib.circatt_fused_bwd(kind, code, nsp, n1, n2, ws, C, nheads, B,
                                         ptr(q), ptr(k), ptr(v), ptr(y), ptr(dy), ptr(lse),
                                         ptr(dq), ptr(dk), ptr(dv), ptr(ws_buf), wbytes,
                                         stream_ptr(q.device)), "circatt_fused_bwd")
-        return None, dq, dk, dv, None, None, None
+        return None, dq, dk, dv, None, None, None, None

@@ -30,6 +30,7 @@ DOT = 0
 DISTANCE = 1
 F32 = 0
 C32 = 1
+CHANNELS_LAST = 16  # OR-ed into dtype of the fused entry points
 
 MATH_SPLIT_F16 = 0
 MATH_F32 = 1

@@ -484,14 +484,16 @@ def _splitheads(x, nheads):
     return x.reshape(B * nheads, C // nheads, *x.shape[2:])
 
 
-def circulant_attention(*args, materialize: bool = True):
+def circulant_attention(*args, materialize: bool = True, channels_last: bool = False):
     """Two forms, as in the reference:
 
     * ``y, A = circulant_attention(simfun, q, k, v, W)`` / ``(q, k, v, W)``
       (src/attention.jl:19-26): q and k are scaled by 1/sqrt(sqrt(C)), A is the
       row-softmax adjacency (Julia size (P, P, 1, B)) and y = A ⊗ v.  With
       ``materialize=False`` the fused kernels compute y without forming A and
-      ``None`` is returned in A's place.
+      ``None`` is returned in A's place.  ``channels_last=True`` (fused only)
+      takes and returns (B, *reversed(spatial), C) tensors, Julia
+      (C, spatial..., B), read and written in place by the kernels.
     * ``y = circulant_attention(A, x)`` = ``A ⊗ x`` (src/attention.jl:53-70).
     """
     if len(args) == 2 and isinstance(args[0], Circulant):
@@ -501,14 +503,24 @@ def circulant_attention(*args, materialize: bool = True):
     if len(args) != 5:
         raise TypeError("circulant_attention(simfun, q, k, v, W), (q, k, v, W) or (A, x)")
     simfun, q, k, v, W = args
-    return _attention(_kind(simfun), q, k, v, W, 1, materialize)
+    return _attention(_kind(simfun), q, k, v, W, 1, materialize, channels_last)
 
 
-def _attention(kind, q, k, v, W, nheads, materialize):
+def _attention(kind, q, k, v, W, nheads, materialize, channels_last=False):
     _check_pair(q, k)
     _check_pair(q, v)
     if W % 2 != 1:
         raise AssertionError(f"filter size M={W} must be odd.")
+    if channels_last:
+        if materialize:
+            raise AssertionError("channels_last needs materialize=False (the fused kernels)")
+        if q.dim() < 3:
+            raise AssertionError("channels_last tensors are (B, *spatial, C)")
+        spatial = tuple(reversed(q.shape[1:-1]))
+        C = q.shape[-1]
+        if C % nheads != 0:
+            raise AssertionError(f"channels ({C}) must be divisible by nheads ({nheads})")
+        return FusedAttentionFn.apply(kind, q, k, v, spatial, W, nheads, True), None
     spatial = _spatial(q)
     if not materialize:
         return FusedAttentionFn.apply(kind, q, k, v, spatial, W, nheads), None
@@ -524,7 +536,8 @@ def _attention(kind, q, k, v, W, nheads, materialize):
     return y.reshape(q.shape), A
 
 
-def circulant_mh_attention(*args, materialize: bool = True, honor_simfun: bool = False):
+def circulant_mh_attention(*args, materialize: bool = True, honor_simfun: bool = False,
+                           channels_last: bool = False):
     """Two forms, as in the reference:
 
     * ``y, A = circulant_mh_attention(simfun, q, k, v, W, nheads)``
@@ -532,7 +545,8 @@ def circulant_mh_attention(*args, materialize: bool = True, honor_simfun: bool =
       Julia size (P, P, nheads, B).  The reference ignores ``simfun`` and
       always uses DotSimilarity (src/attention.jl:40); that is reproduced
       unless ``honor_simfun=True``.  ``materialize=False`` selects the fused
-      kernels (A is not formed, ``None`` is returned in its place).
+      kernels (A is not formed, ``None`` is returned in its place);
+      ``channels_last=True`` with it takes (B, *reversed(spatial), C) tensors.
     * ``y = circulant_mh_attention(A, x)`` = ``A ⨷ x`` (src/attention.jl:89-96).
     """
     if len(args) == 2 and isinstance(args[0], Circulant):
@@ -545,7 +559,7 @@ def circulant_mh_attention(*args, materialize: bool = True, honor_simfun: bool =
         raise TypeError("circulant_mh_attention(simfun, q, k, v, W, nheads) or (A, x)")
     simfun, q, k, v, W, nheads = args
     kind = _kind(simfun) if honor_simfun else L.DOT
-    return _attention(kind, q, k, v, W, int(nheads), materialize)
+    return _attention(kind, q, k, v, W, int(nheads), materialize, channels_last)
 
 
 def circulant_mh_adjacency(simfun, x, y, W: int, nheads: int) -> Circulant:

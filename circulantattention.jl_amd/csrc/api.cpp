@@ -295,6 +295,8 @@ int circatt_batch_dot(int64_t nnz, int64_t nb, const float *X, const float *Y, f
 static int fused_problem(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int32_t ws,
                          int64_t C, int64_t nheads, int64_t B, FusedProblem &pr) {
     Geom g;
+    const int cl = (dtype & CIRCATT_CHANNELS_LAST) ? 1 : 0;
+    dtype &= ~CIRCATT_CHANNELS_LAST;
     CIRCATT_TRY(check_kind(kind));
     CIRCATT_TRY(check_dtype(dtype));
     CIRCATT_TRY(check_geom(nsp, n1, n2, ws, g));
@@ -308,6 +310,12 @@ static int fused_problem(int kind, int dtype, int nsp, int64_t n1, int64_t n2, i
     pr.ncomp = dtype == CIRCATT_C32 ? 2 : 1;
     pr.dh = (int)(C / nheads);
     pr.nunits = nheads * B;
+    pr.cl = cl;
+    pr.nheads = (int)nheads;
+    if (cl && g.P * C * pr.ncomp * 4 >= (int64_t)INT32_MAX)
+        return fail(CIRCATT_ERR_UNSUPPORTED,
+                    "channels-last image of %lld floats exceeds the kernels' 32-bit offsets",
+                    (long long)(g.P * C * pr.ncomp));
     // q ./ sqrt(tau), k ./ sqrt(tau), tau = sqrt(channels per head)
     // (src/attention.jl:20-21) scale the similarity by 1/sqrt(dh).
     pr.scale = (float)(1.0 / std::sqrt((double)pr.dh));

@@ -78,6 +78,8 @@ struct FusedProblem {
     int dh;       // channels per head (per unit)
     int64_t nunits;
     float scale;  // similarity scale
+    int cl;       // 1: channels-last tensors (C, spatial..., B)
+    int nheads;   // heads per image (units = nheads * B, head fastest)
     const float *q, *k, *v, *y, *dy, *lse;
     float *yout, *lse_out, *dq, *dk, *dv, *dbuf, *nz;
 };

@@ -38,6 +38,9 @@ Plan make_plan(FusedMode mode, const FusedProblem &pr) {
     a.ncomp = pr.ncomp;
     a.ncr = pr.dh * pr.ncomp;
     a.unit_stride = pr.g.P * pr.dh * pr.ncomp;
+    a.cl = pr.cl;
+    a.nheads = pr.nheads;
+    a.ncrall = pr.nheads * pr.dh * pr.ncomp;
     a.scale = pr.scale;
     a.c2 = pr.scale * kLog2e;
     pl.nc = a.ncr <= 16 ? 16 : a.ncr <= 32 ? 32 : a.ncr <= 64 ? 64 : 0;
@@ -93,6 +96,9 @@ hipError_t launch_f2d(FusedMode mode, const FusedProblem &pr, hipStream_t s) {
     a.n2 = pr.g.n2;
     a.P = (int)pr.g.P;
     a.unit_stride = (int)(pr.g.P * ncr);
+    a.cl = pr.cl;
+    a.nheads = pr.nheads;
+    a.ncrall = pr.nheads * ncr;
     a.scale = pr.scale;
     a.c2 = pr.scale * kLog2e;
     a.nunits = (int)pr.nunits;

@@ -223,7 +223,49 @@ struct Args {
     int nunits;           // (head, batch) units
     int tiles_h, tiles_w, nitems, per_xcd;  // set by launch()
     FastDiv div_tiles, div_th;  // by tiles_h * tiles_w and by tiles_h (split-half launch)
+    // channels-last tensors (C, spatial..., B): cl = 1, nheads heads per
+    // image (div_nh divides by it), ncrall = floats per pixel (C *
+    // components); planar when cl = 0.  The kernels take the layout as a
+    // template argument; cl selects the instantiation.
+    int cl, nheads, ncrall;
+    FastDiv div_nh;
 };
+
+// Layout of q, k, v, y, dy and the gradients.  Planar (CL = false, the
+// reference's column-major (spatial..., C, B)): unit u = (batch, head) starts
+// at float u * P * ncr, pixel p sits p floats in (complex: 2p) and real
+// component k P k floats further (complex: 2 P (k >> 1) + (k & 1)).
+// Channels-last (CL = true, (C, spatial..., B)): unit (b, h) starts at
+// b * P * ncrall + h * ncr, pixel p at p * ncrall, component k at k.  Both
+// offsets separate into a pixel part (per lane) and a component part
+// (constant or wave-uniform).
+template <bool CL>
+__device__ __forceinline__ int64_t unit_base(const Args &a, int unit) {
+    if constexpr (CL) {
+        const int b = fdiv(unit, a.div_nh);
+        return (int64_t)b * a.P * a.ncrall + (int64_t)(unit - b * a.nheads) * (a.unit_stride / a.P);
+    }
+    return (int64_t)unit * a.unit_stride;
+}
+// bytes from the unit's base to the end of its data (the buffer range)
+template <bool CL>
+__device__ __forceinline__ int unit_bytes(const Args &a, int unit) {
+    if constexpr (CL) {
+        const int h = unit - fdiv(unit, a.div_nh) * a.nheads;
+        return (a.P * a.ncrall - h * (a.unit_stride / a.P)) * 4;
+    }
+    return a.unit_stride * 4;
+}
+template <bool CPLX, bool CL>
+__device__ __forceinline__ int pix_off(const Args &a, int pix) {
+    if constexpr (CL) return pix * a.ncrall;
+    return CPLX ? 2 * pix : pix;
+}
+template <bool CPLX, bool CL>
+__device__ __forceinline__ int comp_soff(const Args &a, int comp) {
+    if constexpr (CL) return comp;
+    return CPLX ? 2 * a.P * (comp >> 1) + (comp & 1) : a.P * comp;
+}
 
 // Buffer resource over `bytes` bytes at p (loads beyond it return 0).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const float *p, int bytes) {
@@ -236,11 +278,11 @@ __device__ __forceinline__ f2 bload2(__amdgpu_buffer_rsrc_t r, int voff, int sof
     return __builtin_bit_cast(f2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
 }
 
-// Real component `comp` of pixel `pix` in a unit (float index).
-template <bool CPLX>
-__device__ __forceinline__ int comp_off(int P, int pix, int comp) {
-    if constexpr (CPLX) return 2 * (pix + P * (comp >> 1)) + (comp & 1);
-    return pix + P * comp;
+// Real component `comp` of pixel `pix` in a unit (float index from the
+// unit's base).
+template <bool CPLX, bool CL>
+__device__ __forceinline__ int comp_off(const Args &a, int pix, int comp) {
+    return pix_off<CPLX, CL>(a, pix) + comp_soff<CPLX, CL>(a, comp);
 }
 
 // Work item k of this workgroup: XCD x = blockIdx % 8 owns items
@@ -251,7 +293,7 @@ __device__ __forceinline__ int item_of(const Args &a, int k) {
     return it < min(a.nitems, (xcd + 1) * a.per_xcd) ? it : a.nitems;
 }
 
-template <int P, int NT, bool CPLX, bool DIST, int MODE>
+template <int P, int NT, bool CPLX, bool DIST, int MODE, bool CL>
 __global__ __launch_bounds__((Grid<P, NT, DIST, MODE>::THREADS), (Grid<P, NT, DIST, MODE>::MINWG))
 void kernel2d(Args a) {
     constexpr int WH = Grid<P, NT, DIST, MODE>::WH, WW = Grid<P, NT, DIST, MODE>::WW;
@@ -298,8 +340,6 @@ void kernel2d(Args a) {
     const float *const pS0 = lds + opaque(OS0 + slotE);      // scalars 0 of element 4g
     const float *const pS1 = lds + opaque(OS1 + slotE);      // scalars 1 of element 4g
 
-    const int ubytes = a.unit_stride * 4;
-
     // ---- prefetch registers ----
     float hv[PPT][2][NC];
     float hs[PPT][2];
@@ -321,7 +361,8 @@ void kernel2d(Args a) {
         int unit, h0, w0;
         decode(item, unit, h0, w0);
         const int hs0 = pmod(h0 - P, a.n1), ws0 = pmod(w0 - P, a.n2);  // uniform
-        const int64_t uoff = (int64_t)unit * a.unit_stride;
+        const int64_t uoff = unit_base<CL>(a, unit);
+        const int ubytes = unit_bytes<CL>(a, unit);
         const auto r0 = rsrc((MODE == BWDKV ? a.q : a.k) + uoff, ubytes);
         const auto r1 = rsrc((MODE == BWDKV ? a.dy : a.v) + uoff, ubytes);
 #pragma unroll
@@ -345,8 +386,8 @@ void kernel2d(Args a) {
             if constexpr (CPLX) {
 #pragma unroll
                 for (int c = 0; c < NC / 2; ++c) {
-                    const f2 x0 = bload2(r0, gp * 8, c * a.P * 8);
-                    const f2 x1 = bload2(r1, gp * 8, c * a.P * 8);
+                    const f2 x0 = bload2(r0, pix_off<true, CL>(a, gp) * 4, comp_soff<true, CL>(a, 2 * c) * 4);
+                    const f2 x1 = bload2(r1, pix_off<true, CL>(a, gp) * 4, comp_soff<true, CL>(a, 2 * c) * 4);
                     hv[pp][0][2 * c] = x0[0];
                     hv[pp][0][2 * c + 1] = x0[1];
                     hv[pp][1][2 * c] = x1[0];
@@ -355,8 +396,8 @@ void kernel2d(Args a) {
             } else {
 #pragma unroll
                 for (int c = 0; c < NC; ++c) {
-                    hv[pp][0][c] = bload(r0, gp * 4, c * a.P * 4);
-                    hv[pp][1][c] = bload(r1, gp * 4, c * a.P * 4);
+                    hv[pp][0][c] = bload(r0, pix_off<false, CL>(a, gp) * 4, comp_soff<false, CL>(a, c) * 4);
+                    hv[pp][1][c] = bload(r1, pix_off<false, CL>(a, gp) * 4, comp_soff<false, CL>(a, c) * 4);
                 }
             }
             if constexpr (MODE == BWDKV) {
@@ -375,16 +416,17 @@ void kernel2d(Args a) {
         const int rh = h0 + 8 * wh + jh, rw = w0 + 2 * ww + jw;
         const bool rvalid = rh < a.n1 && rw < a.n2;
         const int rpix = rvalid ? rh + a.n1 * rw : 0;
-        const int64_t uoff = (int64_t)unit * a.unit_stride;
+        const int64_t uoff = unit_base<CL>(a, unit);
+        const int ubytes = unit_bytes<CL>(a, unit);
         const auto r0 = rsrc((MODE == BWDKV ? a.k : a.q) + uoff, ubytes);
         const auto r1 = rsrc((MODE == BWDKV ? a.v : a.dy) + uoff, ubytes);
         // component 16 t + 4 g + c of the lane's pixel: lane part 4 g,
         // scalar part 16 t + c
-        const int vo = comp_off<CPLX>(a.P, rpix, 4 * g) * 4;
+        const int vo = comp_off<CPLX, CL>(a, rpix, 4 * g) * 4;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const int sc = 16 * (s >> 2) + (s & 3);
-            const int so = (CPLX ? 2 * a.P * (sc >> 1) + (sc & 1) : a.P * sc) * 4;
+            const int so = comp_soff<CPLX, CL>(a, sc) * 4;
             nr0[s] = bload(r0, vo, so);
             if constexpr (MODE != FWD) nr1[s] = bload(r1, vo, so);
             if constexpr (MODE == BWDQ) nry[s] = bload(rsrc(a.y + uoff, ubytes), vo, so);
@@ -404,7 +446,7 @@ void kernel2d(Args a) {
         const int rh = h0 + 8 * wh + jh, rw = w0 + 2 * ww + jw;
         const bool rvalid = rh < a.n1 && rw < a.n2;
         const int rpix = rvalid ? rh + a.n1 * rw : 0;
-        const int64_t uoff = (int64_t)unit * a.unit_stride;
+        const int64_t uoff = unit_base<CL>(a, unit);
         const int64_t soff = (int64_t)unit * a.P;
         const float c2 = a.c2;
 
@@ -557,7 +599,7 @@ void kernel2d(Args a) {
                 for (int t = 0; t < NT; ++t)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        yb[comp_off<CPLX>(a.P, rpix, 16 * t + 4 * g + r)] =
+                        yb[comp_off<CPLX, CL>(a, rpix, 16 * t + 4 * g + r)] =
                             (acc[0][t][r] + acc[1][t][r]) * inv;
                 if (g == 0)
                     a.lse_out[soff + rpix] =
@@ -625,7 +667,7 @@ void kernel2d(Args a) {
                     for (int r = 0; r < 4; ++r) {
                         float val = acc[0][t][r] + acc[1][t][r];
                         if constexpr (DIST) val -= rs * reg0[4 * t + r] * invc2;
-                        ob[comp_off<CPLX>(a.P, rpix, 16 * t + 4 * g + r)] = val * a.scale;
+                        ob[comp_off<CPLX, CL>(a, rpix, 16 * t + 4 * g + r)] = val * a.scale;
                     }
                 if (g == 0) a.dbuf[soff + rpix] = rowD;
             }
@@ -696,7 +738,7 @@ void kernel2d(Args a) {
                 for (int t = 0; t < NT; ++t)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int o = comp_off<CPLX>(a.P, rpix, 16 * t + 4 * g + r);
+                        const int o = comp_off<CPLX, CL>(a, rpix, 16 * t + 4 * g + r);
                         vb[o] = accv[0][t][r] + accv[1][t][r];
                         float val = acck[0][t][r] + acck[1][t][r];
                         if constexpr (DIST) val -= cs * reg0[4 * t + r] * invc2;
@@ -714,12 +756,12 @@ void kernel2d(Args a) {
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-template <int P, int NT, bool CPLX, bool DIST, int MODE>
+template <int P, int NT, bool CPLX, bool DIST, int MODE, bool CL>
 hipError_t launch(const Args &a0, int cus, hipStream_t s) {
     using GR = Grid<P, NT, DIST, MODE>;
     using G = Geo<P, NT, GR::WH, GR::WW>;
     static_assert(GR::bytes <= kLdsCap, "halo does not fit LDS");
-    auto kern = kernel2d<P, NT, CPLX, DIST, MODE>;
+    auto kern = kernel2d<P, NT, CPLX, DIST, MODE, CL>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -735,6 +777,7 @@ hipError_t launch(const Args &a0, int cus, hipStream_t s) {
     if (nitems <= 0 || nitems > INT32_MAX / 2) return hipErrorNotSupported;
     a.nitems = (int)nitems;
     a.per_xcd = (int)((nitems + 7) / 8);
+    if (CL) a.div_nh = make_fastdiv((uint32_t)a.nheads);
     int64_t grid = (int64_t)cus * GR::MINWG;
     grid = std::min<int64_t>(grid, 8LL * a.per_xcd);
     grid = std::max<int64_t>(8, grid / 8 * 8);
@@ -748,12 +791,17 @@ hipError_t launch(const Args &a0, int cus, hipStream_t s) {
 // without launching.
 template <int MODE>
 hipError_t dispatch(int p, int nt, bool cplx, bool dist, const Args &a, int cus, hipStream_t s) {
+#define CIRCATT_F2D_CL(PP, NTT, CLL)                                                   \
+    {                                                                                  \
+        if (cplx) return dist ? launch<PP, NTT, true, true, MODE, CLL>(a, cus, s)      \
+                              : launch<PP, NTT, true, false, MODE, CLL>(a, cus, s);    \
+        return dist ? launch<PP, NTT, false, true, MODE, CLL>(a, cus, s)               \
+                    : launch<PP, NTT, false, false, MODE, CLL>(a, cus, s);             \
+    }
 #define CIRCATT_F2D_CASE(PP, NTT)                                                      \
     if (p == PP && nt == NTT) {                                                        \
-        if (cplx) return dist ? launch<PP, NTT, true, true, MODE>(a, cus, s)           \
-                              : launch<PP, NTT, true, false, MODE>(a, cus, s);         \
-        return dist ? launch<PP, NTT, false, true, MODE>(a, cus, s)                    \
-                    : launch<PP, NTT, false, false, MODE>(a, cus, s);                  \
+        if (a.cl) CIRCATT_F2D_CL(PP, NTT, true)                                        \
+        CIRCATT_F2D_CL(PP, NTT, false)                                                 \
     }
     CIRCATT_F2D_CASE(1, 1)
     CIRCATT_F2D_CASE(2, 1)
@@ -766,6 +814,7 @@ hipError_t dispatch(int p, int nt, bool cplx, bool dist, const Args &a, int cus,
     CIRCATT_F2D_CASE(5, 2)
     CIRCATT_F2D_CASE(7, 2)
 #undef CIRCATT_F2D_CASE
+#undef CIRCATT_F2D_CL
     return hipErrorNotSupported;
 }
 

@@ -252,7 +252,7 @@ struct LGeo {
     static constexpr int bytes = OX + 16;
 };
 
-template <int P, bool CPLX, bool DIST, int MODE>
+template <int P, bool CPLX, bool DIST, int MODE, bool CL>
 __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     using G = f2d::Geo<P, 1, 2, 8>;
     using L = LGeo<P, MODE, DIST>;
@@ -317,8 +317,6 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     const float *const pS0 = reinterpret_cast<const float *>(lds + opaque(L::OS0 + slotE * 4));
     const float *const pS1 = reinterpret_cast<const float *>(lds + opaque(L::OS1 + slotE * 4));
 
-    const int ubytes = a.unit_stride * 4;
-
     // ---- prefetch registers ----
     float h0v[16], h1v[16], hs0 = 0.f, hs1 = 0.f;
     int hslot;
@@ -351,7 +349,8 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         int hsh = h0 - P, wsh = w0 - P;
         while (hsh < 0) hsh += a.n1;
         while (wsh < 0) wsh += a.n2;
-        const int64_t uoff = (int64_t)unit * a.unit_stride;
+        const int64_t uoff = f2d::unit_base<CL>(a, unit);
+        const int ubytes = f2d::unit_bytes<CL>(a, unit);
         const auto r0 = f2d::rsrc((KV ? a.q : a.k) + uoff, ubytes);
         const auto r1 = f2d::rsrc((KV ? a.dy : a.v) + uoff, ubytes);
         hslot = px < NPX ? kh + CR * kw : -1;
@@ -367,8 +366,9 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         if constexpr (CPLX) {
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                const f2d::f2 x0 = f2d::bload2(r0, gp * 8, c * a.P * 8);
-                const f2d::f2 x1 = f2d::bload2(r1, gp * 8, c * a.P * 8);
+                const int vo = f2d::pix_off<true, CL>(a, gp) * 4, so = f2d::comp_soff<true, CL>(a, 2 * c) * 4;
+                const f2d::f2 x0 = f2d::bload2(r0, vo, so);
+                const f2d::f2 x1 = f2d::bload2(r1, vo, so);
                 h0v[2 * c] = x0[0];
                 h0v[2 * c + 1] = x0[1];
                 h1v[2 * c] = x1[0];
@@ -377,8 +377,9 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         } else {
 #pragma unroll
             for (int c = 0; c < 16; ++c) {
-                h0v[c] = f2d::bload(r0, gp * 4, c * a.P * 4);
-                h1v[c] = f2d::bload(r1, gp * 4, c * a.P * 4);
+                const int vo = f2d::pix_off<false, CL>(a, gp) * 4, so = f2d::comp_soff<false, CL>(a, c) * 4;
+                h0v[c] = f2d::bload(r0, vo, so);
+                h1v[c] = f2d::bload(r1, vo, so);
             }
         }
         if constexpr (KV) {
@@ -391,13 +392,14 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         bool rvalid;
         int rpix;
         regpix(h0, w0, rvalid, rpix);
-        const int64_t uoff = (int64_t)unit * a.unit_stride;
+        const int64_t uoff = f2d::unit_base<CL>(a, unit);
+        const int ubytes = f2d::unit_bytes<CL>(a, unit);
         const auto r0 = f2d::rsrc((KV ? a.k : a.q) + uoff, ubytes);
         const auto r1 = f2d::rsrc((KV ? a.v : a.dy) + uoff, ubytes);
-        const int vo = f2d::comp_off<CPLX>(a.P, rpix, 8 * (g & 1) + 4 * (g >> 1)) * 4;
+        const int vo = f2d::comp_off<CPLX, CL>(a, rpix, 8 * (g & 1) + 4 * (g >> 1)) * 4;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const int so = (CPLX ? 2 * a.P * (t >> 1) + (t & 1) : a.P * t) * 4;
+            const int so = f2d::comp_soff<CPLX, CL>(a, t) * 4;
             nh0[t] = f2d::bload(r0, vo, so);
             if constexpr (MODE != FWD) nh1[t] = f2d::bload(r1, vo, so);
             // y beside dy, for D = <dy, y>
@@ -424,7 +426,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         bool rvalid;
         int rpix;
         regpix(h0, w0, rvalid, rpix);
-        const int64_t uoff = (int64_t)unit * a.unit_stride;
+        const int64_t uoff = f2d::unit_base<CL>(a, unit);
         const int64_t soff = (int64_t)unit * a.P;
         const float c2 = a.c2;
 
@@ -815,7 +817,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 float *yb = a.yout + uoff;
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    yb[f2d::comp_off<CPLX>(a.P, rpix, 4 * g + r)] =
+                    yb[f2d::comp_off<CPLX, CL>(a, rpix, 4 * g + r)] =
                         __builtin_amdgcn_ldexpf(acc[r] * inv, -s1);
                 if (g == 0)
                     a.lse_out[soff + rpix] =
@@ -920,7 +922,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                         // dS' = 2^(sd + s1) dS, k' = 2^s0 k
                         float val = __builtin_amdgcn_ldexpf(acc0[r], -(sd + s1 + s0));
                         if constexpr (DIST) val -= __builtin_amdgcn_ldexpf(cs, -(sd + s1)) * reg0[r];
-                        ob[f2d::comp_off<CPLX>(a.P, rpix, 4 * g + r)] = val * a.scale;
+                        ob[f2d::comp_off<CPLX, CL>(a, rpix, 4 * g + r)] = val * a.scale;
                     }
                     if (g == 0) a.dbuf[soff + rpix] = rowD;
                 } else {
@@ -928,7 +930,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     float *kbp = a.dk + uoff;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int o = f2d::comp_off<CPLX>(a.P, rpix, 4 * g + r);
+                        const int o = f2d::comp_off<CPLX, CL>(a, rpix, 4 * g + r);
                         // dy' = 2^s1 dy, dS' = 2^(s2 + s1) dS, q' = 2^s0 q
                         vb[o] = __builtin_amdgcn_ldexpf(acc1[r], -s1);
                         float val = __builtin_amdgcn_ldexpf(acc0[r], -(s2 + s1 + s0));
@@ -957,12 +959,12 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
 #endif
 }
 
-template <int P, bool CPLX, bool DIST, int MODE>
+template <int P, bool CPLX, bool DIST, int MODE, bool CL>
 hipError_t launch(const Args &a0, int cus, hipStream_t s) {
     using G = f2d::Geo<P, 1, 2, 8>;
     constexpr int bytes = LGeo<P, MODE, DIST>::bytes;
     static_assert(bytes <= (int)f2d::kLdsCap, "halo does not fit LDS");
-    auto kern = kernel2h<P, CPLX, DIST, MODE>;
+    auto kern = kernel2h<P, CPLX, DIST, MODE, CL>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -977,6 +979,7 @@ hipError_t launch(const Args &a0, int cus, hipStream_t s) {
     if (nitems <= 0 || nitems > INT32_MAX / 2) return hipErrorNotSupported;
     a.div_tiles = make_fastdiv((uint32_t)(a.tiles_h * a.tiles_w));
     a.div_th = make_fastdiv((uint32_t)a.tiles_h);
+    if (CL) a.div_nh = make_fastdiv((uint32_t)a.nheads);
     a.nitems = (int)nitems;
     a.per_xcd = (int)((nitems + 7) / 8);
     int64_t grid = std::min<int64_t>(cus, 8LL * a.per_xcd);
@@ -987,12 +990,17 @@ hipError_t launch(const Args &a0, int cus, hipStream_t s) {
 
 template <int MODE>
 hipError_t dispatch(int p, bool cplx, bool dist, const Args &a, int cus, hipStream_t s) {
+#define CIRCATT_F2H_CL(PP, CLL)                                                          \
+    {                                                                                    \
+        if (cplx) return dist ? launch<PP, true, true, MODE, CLL>(a, cus, s)             \
+                              : launch<PP, true, false, MODE, CLL>(a, cus, s);           \
+        return dist ? launch<PP, false, true, MODE, CLL>(a, cus, s)                      \
+                    : launch<PP, false, false, MODE, CLL>(a, cus, s);                    \
+    }
 #define CIRCATT_F2H_CASE(PP)                                                             \
     if (p == PP) {                                                                       \
-        if (cplx) return dist ? launch<PP, true, true, MODE>(a, cus, s)                  \
-                              : launch<PP, true, false, MODE>(a, cus, s);                \
-        return dist ? launch<PP, false, true, MODE>(a, cus, s)                           \
-                    : launch<PP, false, false, MODE>(a, cus, s);                         \
+        if (a.cl) CIRCATT_F2H_CL(PP, true)                                               \
+        CIRCATT_F2H_CL(PP, false)                                                        \
     }
     CIRCATT_F2H_CASE(1)
     CIRCATT_F2H_CASE(2)
@@ -1000,6 +1008,7 @@ hipError_t dispatch(int p, bool cplx, bool dist, const Args &a, int cus, hipStre
     CIRCATT_F2H_CASE(5)
     CIRCATT_F2H_CASE(7)
 #undef CIRCATT_F2H_CASE
+#undef CIRCATT_F2H_CL
     return hipErrorNotSupported;
 }
 

@@ -149,6 +149,9 @@ struct FArgs {
     int tiles_h, tiles_w;
     int nitems;           // tiles * units
     int per_xcd;          // items per XCD run
+    // channels-last tensors (C, spatial..., B): cl = 1, nheads heads per
+    // image, ncrall = floats per pixel (C * components); planar when cl = 0
+    int cl, nheads, ncrall;
 };
 
 template <int NC, int MODE, bool DIST>
@@ -163,7 +166,21 @@ struct Cfg {
     static constexpr int PPT = NC * NTEN <= 32 ? 2 : 1;        // halo pixels per thread
 };
 
+// Layout of q, k, v, y, dy and the gradients.  Planar (the reference's
+// column-major (spatial..., C, B)): unit u = (batch, head) starts at float
+// u * P * ncr and real component comp of pixel pix sits at pix + P comp
+// (complex: 2 (pix + P (comp >> 1)) + (comp & 1)).  Channels-last
+// ((C, spatial..., B)): unit (b, h) starts at b * P * ncrall + h * ncr, and
+// the component at pix * ncrall + comp.
+__device__ __forceinline__ int64_t unit_base(const FArgs &a, int unit) {
+    if (a.cl) {
+        const int b = unit / a.nheads;
+        return (int64_t)b * a.g.P * a.ncrall + (int64_t)(unit - b * a.nheads) * a.ncr;
+    }
+    return (int64_t)unit * a.unit_stride;
+}
 __device__ __forceinline__ int64_t comp_index(const FArgs &a, int64_t pix, int comp) {
+    if (a.cl) return pix * a.ncrall + comp;
     if (a.ncomp == 1) return pix + a.g.P * comp;
     return 2 * (pix + a.g.P * (comp >> 1)) + (comp & 1);
 }
@@ -175,7 +192,11 @@ __device__ __forceinline__ void load_pixel(float (&v)[NC], const float *base, co
                                            int64_t gp) {
     const int64_t P = a.g.P;
     const bool full = a.ncr == NC;
-    if (a.ncomp == 1) {
+    if (a.cl) {
+        const float *src = base + gp * a.ncrall;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) v[c] = src[full ? c : min(c, a.ncr - 1)];
+    } else if (a.ncomp == 1) {
         const float *src = base + gp;
 #pragma unroll
         for (int c = 0; c < NC; ++c) v[c] = src[(int64_t)(full ? c : min(c, a.dh - 1)) * P];
@@ -335,7 +356,7 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
         const int cr0 = chunk * chunk_rows;
         const int crn = min(chunk_rows, halo_h - cr0);
         const int npx = crn * halo_w;
-        const int64_t uoff = (int64_t)unit * a.unit_stride;
+        const int64_t uoff = unit_base(a, unit);
         const int64_t soff = (int64_t)unit * a.g.P;
         const float *src0 = (MODE == MODE_BWDKV ? a.q : a.k) + uoff;
         const float *src1 = (MODE == MODE_BWDKV ? a.dy : a.v) + uoff;
@@ -363,7 +384,7 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
         const int rh = h0 + wh + jh, rw = w0 + ww + jw;
         const bool rvalid = rh < a.g.n1 && rw < a.g.n2;
         const int64_t rpix = rvalid ? (int64_t)rh + (int64_t)a.g.n1 * rw : 0;
-        const int64_t uoff = (int64_t)unit * a.unit_stride;
+        const int64_t uoff = unit_base(a, unit);
         const float *b0 = (MODE == MODE_BWDKV ? a.k : a.q) + uoff;
         const float *b1 = (MODE == MODE_BWDKV ? a.v : a.dy) + uoff;
 #pragma unroll
@@ -398,7 +419,7 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
         const int rh = h0 + wh + jh, rw = w0 + ww + jw;
         const bool rvalid = rh < a.g.n1 && rw < a.g.n2;
         const int64_t rpix = rvalid ? (int64_t)rh + (int64_t)a.g.n1 * rw : 0;
-        const int64_t uoff = (int64_t)unit * a.unit_stride;
+        const int64_t uoff = unit_base(a, unit);
         const int64_t soff = (int64_t)unit * a.g.P;
         const int cr0 = chunk * chunk_rows;
         const int crn = min(chunk_rows, halo_h - cr0);

@@ -13,9 +13,11 @@ at (linearly indexed) pixels `i`, `j` (``S_{ij} = \mathrm{simfun}(q_i, k_j)``).
 Note: q and k are internally scaled by `sqrt(sqrt(channels))`.  With `materialize=false`
 the fused kernels compute `y` without forming `A` (returned as `nothing`).
 """
-function circulant_attention(simfun::AbstractSimilarity, q::T, k::T, v::T, W::Int; materialize::Bool=true) where {Tv, N, T<: AbstractArray{Tv,N}}
-    if !materialize
-        return (fused_attention(simfun, q, k, v, W, 1), nothing)
+function circulant_attention(simfun::AbstractSimilarity, q::T, k::T, v::T, W::Int; materialize::Bool=true,
+                             channels_last::Bool=false) where {Tv, N, T<: AbstractArray{Tv,N}}
+    if !materialize || channels_last
+        @assert !materialize "channels_last needs materialize=false (the fused kernels)"
+        return (fused_attention(simfun, q, k, v, W, 1, channels_last), nothing)
     end
     τ = sqrt(real(Tv)(size(k, N-1)))
     # q ./ sqrt(τ), k ./ sqrt(τ) (src/attention.jl:20-21) scale the similarity by 1/τ
@@ -38,11 +40,14 @@ As in the reference (src/attention.jl:40), `simfun` is ignored and the dot
 similarity is used unless `honor_simfun=true`.
 """
 function circulant_mh_attention(simfun::AbstractSimilarity, q::T, k::T, v::T, W::Int, nheads::Int;
-                                materialize::Bool=true, honor_simfun::Bool=false) where {Tv, N, T<: AbstractArray{Tv,N}}
+                                materialize::Bool=true, honor_simfun::Bool=false,
+                                channels_last::Bool=false) where {Tv, N, T<: AbstractArray{Tv,N}}
     sim = honor_simfun ? simfun : DotSimilarity()
-    @assert size(q, N-1) % nheads == 0 "channels ($(size(q, N-1))) must be divisible by nheads ($nheads)"
-    if !materialize
-        return (fused_attention(sim, q, k, v, W, nheads), nothing)
+    Cax = channels_last ? 1 : N-1
+    @assert size(q, Cax) % nheads == 0 "channels ($(size(q, Cax))) must be divisible by nheads ($nheads)"
+    if !materialize || channels_last
+        @assert !materialize "channels_last needs materialize=false (the fused kernels)"
+        return (fused_attention(sim, q, k, v, W, nheads, channels_last), nothing)
     end
     qr, kr, vr = splitheads.((q, k, v), nheads)
     yr, A = circulant_attention(sim, qr, kr, vr, W)
@@ -120,29 +125,33 @@ end
 # ---- fused path (no A) -----------------------------------------------------
 
 """y of circulant (multi-head) attention from the fused kernels, without
-forming A; the per-row log-sum-exp is kept for the pullback."""
-function fused_forward(simfun::AbstractSimilarity, q::AbstractArray{T,N}, k, v, W::Int, nheads::Int) where {T,N}
-    spat = size(q)[1:N-2]
+forming A; the per-row log-sum-exp is kept for the pullback.  Planar arrays
+are (spatial..., C, B); with `cl = true` they are channels-last
+(C, spatial..., B), read and written in place (CIRCATT_CHANNELS_LAST)."""
+function fused_forward(simfun::AbstractSimilarity, q::AbstractArray{T,N}, k, v, W::Int, nheads::Int, cl::Bool=false) where {T,N}
+    spat = cl ? size(q)[2:N-1] : size(q)[1:N-2]
     nsp, n1, n2 = geom(spat)
-    C, B = size(q, N-1), size(q, N)
+    C, B = (cl ? size(q, 1) : size(q, N-1)), size(q, N)
     y = similar(q)
     lse = ROCArray{Float32}(undef, prod(spat), nheads * B)
-    check(circatt_fused_fwd(simkind(simfun), dtype_code(T), nsp, n1, n2, Int32(W), Int64(C),
+    code = dtype_code(T) | (cl ? CIRCATT_CHANNELS_LAST : Cint(0))
+    check(circatt_fused_fwd(simkind(simfun), code, nsp, n1, n2, Int32(W), Int64(C),
                             Int64(nheads), Int64(B), cvoid_ptr(q), cvoid_ptr(k), cvoid_ptr(v),
                             cvoid_ptr(y), cfloat_ptr(lse), stream_ptr()), "circatt_fused_fwd")
     return y, lse
 end
 
-fused_attention(simfun, q, k, v, W::Int, nheads::Int) = first(fused_forward(simfun, q, k, v, W, nheads))
+fused_attention(simfun, q, k, v, W::Int, nheads::Int, cl::Bool=false) = first(fused_forward(simfun, q, k, v, W, nheads, cl))
 
-function fused_backward(simfun, q::AbstractArray{T,N}, k, v, y, dy, lse, W::Int, nheads::Int) where {T,N}
-    spat = size(q)[1:N-2]
+function fused_backward(simfun, q::AbstractArray{T,N}, k, v, y, dy, lse, W::Int, nheads::Int, cl::Bool=false) where {T,N}
+    spat = cl ? size(q)[2:N-1] : size(q)[1:N-2]
     nsp, n1, n2 = geom(spat)
-    C, B = size(q, N-1), size(q, N)
+    C, B = (cl ? size(q, 1) : size(q, N-1)), size(q, N)
     dq, dk, dv = similar(q), similar(k), similar(v)
     wb = circatt_fused_bwd_workspace_bytes(nsp, n1, n2, Int64(nheads), Int64(B))
     work = ROCArray{Float32}(undef, cld(wb, 4))
-    check(circatt_fused_bwd(simkind(simfun), dtype_code(T), nsp, n1, n2, Int32(W), Int64(C),
+    code = dtype_code(T) | (cl ? CIRCATT_CHANNELS_LAST : Cint(0))
+    check(circatt_fused_bwd(simkind(simfun), code, nsp, n1, n2, Int32(W), Int64(C),
                             Int64(nheads), Int64(B), cvoid_ptr(q), cvoid_ptr(k), cvoid_ptr(v),
                             cvoid_ptr(y), cvoid_ptr(dy), cfloat_ptr(lse), cvoid_ptr(dq),
                             cvoid_ptr(dk), cvoid_ptr(dv), cvoid_ptr(work), Int64(wb),

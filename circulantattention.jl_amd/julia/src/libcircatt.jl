@@ -16,6 +16,8 @@ const CIRCATT_DOT = Cint(0)
 const CIRCATT_DISTANCE = Cint(1)
 const CIRCATT_F32 = Cint(0)
 const CIRCATT_C32 = Cint(1)
+# OR-ed into dtype of the fused entry points: (C, spatial..., B) tensors
+const CIRCATT_CHANNELS_LAST = Cint(16)
 const CIRCATT_MATH_SPLIT_F16 = Cint(0)
 const CIRCATT_MATH_F32 = Cint(1)
 

@@ -144,12 +144,12 @@ end
 # fused attention (no A): circatt_fused_bwd recomputes the probabilities from
 # the forward's log-sum-exp; the result equals the composition of the rules
 # above for y
-function CRC.rrule(::typeof(fused_attention), simfun::AbstractSimilarity, q::AbstractArray{T,N}, k, v, W::Int, nheads::Int) where {T,N}
-    y, lse = fused_forward(simfun, q, k, v, W, nheads)
+function CRC.rrule(::typeof(fused_attention), simfun::AbstractSimilarity, q::AbstractArray{T,N}, k, v, W::Int, nheads::Int, cl::Bool=false) where {T,N}
+    y, lse = fused_forward(simfun, q, k, v, W, nheads, cl)
     function fused_attention_pullback(Δy)
         dy = as_device(CRC.unthunk(Δy), y)
-        dq, dk, dv = fused_backward(simfun, q, k, v, y, dy, lse, W, nheads)
-        return (CRC.NoTangent(), CRC.NoTangent(), dq, dk, dv, CRC.NoTangent(), CRC.NoTangent())
+        dq, dk, dv = fused_backward(simfun, q, k, v, y, dy, lse, W, nheads, cl)
+        return (CRC.NoTangent(), CRC.NoTangent(), dq, dk, dv, CRC.NoTangent(), CRC.NoTangent(), CRC.NoTangent())
     end
     return y, fused_attention_pullback
 end

@@ -46,6 +46,18 @@ extern "C" {
 #define CIRCATT_F32 0
 #define CIRCATT_C32 1
 
+/*
+ * Layout flag, OR-ed into dtype of the fused entry points (circatt_fused_*):
+ * q, k, v, y, dy and the gradients are channels-last, Julia size
+ * (C, N1[,N2], B): (channel c, pixel r, batch b) at c + C*(r + P*b)
+ * (ComplexF32: interleaved (re, im) elements in that order).  The kernels
+ * read and write this layout directly, so a model that keeps its features
+ * channels-last (the layout convolutions favour) needs no transposes around
+ * the attention.  lse and the workspace keep their layout.  No counterpart in
+ * the reference (which is planar only); other entry points reject the flag.
+ */
+#define CIRCATT_CHANNELS_LAST 16
+
 /* Library version (major*10000 + minor*100 + patch). */
 int circatt_version(void);
 

@@ -77,6 +77,23 @@ def test_unsupported_dtype_and_kind(L):
     expect(L, rc, L.ERR_INVALID, "kind")
 
 
+def test_channels_last_flag_only_on_fused_entry_points(L):
+    # the unfused entry points take planar signals only
+    rc = L.lib.circatt_similarity(0, L.F32 | L.CHANNELS_LAST, 2, 8, 8, 3, 4, 1, 1.0, FAKE, FAKE,
+                                  FAKE, NULL)
+    expect(L, rc, L.ERR_UNSUPPORTED, "dtype")
+    rc = L.lib.circatt_apply(0, L.C32 | L.CHANNELS_LAST, 2, 8, 8, 3, 2, 1, FAKE, FAKE,
+                             ctypes.c_void_p(0x2000), NULL)
+    expect(L, rc, L.ERR_UNSUPPORTED, "dtype")
+    # the fused ones validate the rest as before
+    rc = L.lib.circatt_fused_fwd(0, L.F32 | L.CHANNELS_LAST, 2, 8, 8, 3, 6, 4, 1, FAKE, FAKE,
+                                 FAKE, FAKE, FAKE, NULL)
+    expect(L, rc, L.ERR_INVALID, "divisible by nheads")
+    rc = L.lib.circatt_fused_fwd(0, 7 | L.CHANNELS_LAST, 2, 8, 8, 3, 4, 1, 1, FAKE, FAKE, FAKE,
+                                 FAKE, FAKE, NULL)
+    expect(L, rc, L.ERR_UNSUPPORTED, "dtype")
+
+
 def test_heads_must_divide_channels(L):
     rc = L.lib.circatt_fused_fwd(0, 0, 2, 8, 8, 3, 6, 4, 1, FAKE, FAKE, FAKE, FAKE, FAKE, NULL)
     expect(L, rc, L.ERR_INVALID, "divisible by nheads")
