@@ -22,7 +22,8 @@ HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 SOURCES = ["api.cpp", "unfused.hip", "apply_rb.hip", "fused.hip", "fused_fwd.hip", "fused_sim.hip",
            "fused_bwdq.hip", "fused_bwdkv.hip", "fused2d_fwd.hip", "fused2d_bwdq.hip",
-           "fused2d_bwdkv.hip", "fused2h_fwd.hip", "fused2h_bwdq.hip", "fused2h_bwdkv.hip"]
+           "fused2d_bwdkv.hip", "fused2h_fwd.hip", "fused2h_bwdq.hip", "fused2h_bwdkv.hip",
+           "fused_wide.hip"]
 FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",

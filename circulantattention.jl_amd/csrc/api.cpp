@@ -340,8 +340,8 @@ int circatt_fused_fwd(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int3
     pr.lse_out = lse;
     if (!fused_supported(MODE_FWD, pr))
         return fail(CIRCATT_ERR_UNSUPPORTED,
-                    "circatt_fused_fwd: %d real components per head exceed the fused kernels' 64",
-                    pr.dh * pr.ncomp);
+                    "circatt_fused_fwd: window ws=%d with %d real components per head is outside "
+                    "the fused kernels' range", pr.g.ws, pr.dh * pr.ncomp);
     return hip_result(launch_fused(MODE_FWD, pr, as_stream(stream)), "circatt_fused_fwd");
 }
 
@@ -398,8 +398,8 @@ int fused_bwd_impl(int parts, int kind, int dtype, int nsp, int64_t n1, int64_t 
     pr.dbuf = static_cast<float *>(const_cast<void *>(workspace));
     if (!fused_supported(MODE_BWDQ, pr) || !fused_supported(MODE_BWDKV, pr))
         return fail(CIRCATT_ERR_UNSUPPORTED,
-                    "%s: %d real components per head exceed the fused kernels' 64", name,
-                    pr.dh * pr.ncomp);
+                    "%s: window ws=%d with %d real components per head is outside the fused "
+                    "kernels' range", name, pr.g.ws, pr.dh * pr.ncomp);
     if (parts & BWD_DQ) {
         hipError_t e = launch_fused(MODE_BWDQ, pr, as_stream(stream));
         if (e != hipSuccess) return hip_result(e, name);

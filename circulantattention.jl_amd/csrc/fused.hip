@@ -3,6 +3,7 @@
 #include "fused2d_impl.h"
 #include "fused2h_impl.h"
 #include "fused_impl.h"
+#include "fused_wide_impl.h"
 
 namespace circatt {
 
@@ -74,11 +75,68 @@ Plan make_plan(FusedMode mode, const FusedProblem &pr) {
     return pl;
 }
 
+// Channel-chunked kernels (fused_wide_impl.h) for heads wider than 64 real
+// components.
+struct WidePlan {
+    FArgs a;
+    size_t lds_bytes;
+    dim3 grid;
+    bool ok;
+};
+
+WidePlan make_wide_plan(FusedMode mode, const FusedProblem &pr) {
+    WidePlan wp{};
+    if (mode == MODE_SIM) return wp;
+    const bool dist = pr.kind == 1;
+    const int ntensor = mode == MODE_FWD ? 1 : 2;
+    const int nscal = mode == MODE_BWDKV ? 2 : (dist ? 1 : 0);
+    const wide::Plan w = wide::plan(pr.g.nsp, pr.g.p, ntensor, nscal);
+    if (!w.ok) return wp;
+    FArgs &a = wp.a;
+    a.q = pr.q; a.k = pr.k; a.v = pr.v; a.y = pr.y; a.dy = pr.dy; a.lse = pr.lse;
+    a.yout = pr.yout; a.lse_out = pr.lse_out; a.dq = pr.dq; a.dk = pr.dk; a.dv = pr.dv;
+    a.dbuf = pr.dbuf;
+    a.g = pr.g;
+    a.hg = w.hg;
+    a.dh = pr.dh;
+    a.ncomp = pr.ncomp;
+    a.ncr = pr.dh * pr.ncomp;
+    a.unit_stride = pr.g.P * pr.dh * pr.ncomp;
+    a.cl = pr.cl;
+    a.nheads = pr.nheads;
+    a.ncrall = pr.nheads * pr.dh * pr.ncomp;
+    a.scale = pr.scale;
+    a.c2 = pr.scale * kLog2e;
+    a.rb = w.rb;
+    a.cr = w.cr;
+    a.nst = w.nst;
+    a.ncc = (a.ncr + wide::CC - 1) / wide::CC;
+    a.noc = (a.ncr + wide::OC - 1) / wide::OC;
+    if (pr.g.nsp == 2) {
+        a.tiles_h = (pr.g.n1 + 7) / 8;
+        a.tiles_w = (pr.g.n2 + 7) / 8;
+    } else {
+        a.tiles_h = (pr.g.n1 + 63) / 64;
+        a.tiles_w = 1;
+    }
+    const int64_t nitems = (int64_t)a.tiles_h * a.tiles_w * pr.nunits;
+    if (nitems <= 0 || nitems > INT32_MAX / 2) return wp;
+    a.nitems = (int)nitems;
+    a.per_xcd = (int)((nitems + 7) / 8);
+    int64_t grid = (int64_t)device_cus() * 2;
+    grid = std::min<int64_t>(grid, 8LL * a.per_xcd);
+    grid = std::max<int64_t>(8, grid / 8 * 8);
+    wp.grid = dim3((unsigned)grid);
+    wp.lds_bytes = (size_t)w.lds_floats * sizeof(float);
+    wp.ok = true;
+    return wp;
+}
+
 }  // namespace
 
 bool fused_supported(FusedMode mode, const FusedProblem &pr) {
     Plan pl = make_plan(mode, pr);
-    return pl.ok;
+    return pl.ok || make_wide_plan(mode, pr).ok;
 }
 
 // Compile-time-window 2D kernels (fused2d_impl.h) for the shapes they cover;
@@ -126,7 +184,11 @@ hipError_t launch_fused(FusedMode mode, const FusedProblem &pr, hipStream_t s) {
         if (e != hipErrorNotSupported) return e;
     }
     Plan pl = make_plan(mode, pr);
-    if (!pl.ok) return hipErrorNotSupported;
+    if (!pl.ok) {
+        const WidePlan wp = make_wide_plan(mode, pr);
+        if (!wp.ok) return hipErrorNotSupported;
+        return launch_wide(mode, pr.g.nsp, pr.kind == 1, wp.a, wp.lds_bytes, wp.grid, s);
+    }
     const bool dist = pr.kind == 1;
     switch (mode) {
     case MODE_FWD: return launch_fused_fwd(pl, pr.g.nsp, dist, s);

@@ -152,6 +152,9 @@ struct FArgs {
     // channels-last tensors (C, spatial..., B): cl = 1, nheads heads per
     // image, ncrall = floats per pixel (C * components); planar when cl = 0
     int cl, nheads, ncrall;
+    // channel-chunked kernels (fused_wide_impl.h): block rows per stage, LDS
+    // column stride, stages per pass, score chunks, output passes
+    int rb, cr, nst, ncc, noc;
 };
 
 template <int NC, int MODE, bool DIST>

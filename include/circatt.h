@@ -185,6 +185,12 @@ int circatt_batch_dot(int64_t nnz, int64_t nb, const float *X, const float *Y, f
  * Equals circulant_attention (src/attention.jl:19-26, nheads = 1) and
  * circulant_mh_attention (src/attention.jl:38-42) for the returned y.
  * q, k, v, y: (P, C, B) of dtype; lse: (P, nheads*B) Float32.
+ * Any number of channels per head (the reference's similarity loops over
+ * any C, src/similarity.jl:97-99): heads of up to 64 real components run on
+ * kernels that hold a pixel's components at once, wider heads on kernels
+ * that sum the score products over 32-component chunks and form the outputs
+ * in 64-component passes.  Windows whose 2D block columns exceed the LDS
+ * budget (ws beyond 63) return CIRCATT_ERR_UNSUPPORTED.
  */
 int circatt_fused_fwd(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int32_t ws,
                       int64_t C, int64_t nheads, int64_t B, const void *q, const void *k,
