@@ -205,6 +205,24 @@ def bench_ops(args):
                              "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}}), flush=True)
         del x, y, z, dx, dy, A, B, Z, rowptr, colval
         torch.cuda.empty_cache()
+    if args.calib_copy_mib > 0:
+        calib_copy(args.calib_copy_mib)
+
+
+def calib_copy(mib):
+    """torch's device copy of `mib` MiB, three times: a kernel of known HBM
+    traffic that scales the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.randn(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    return n * 4
 
 
 def main():
@@ -397,15 +415,7 @@ def main():
         "kernels": {n: {kk: round(vv, 4) for kk, vv in d.items()} for n, d in kern.items()},
     }
     if args.calib_copy_mib > 0:
-        n = args.calib_copy_mib * (1 << 20) // 4
-        src = torch.randn(n, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        out["calib_copy_bytes"] = n * 4
-        del src, dst
+        out["calib_copy_bytes"] = calib_copy(args.calib_copy_mib)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.config)
     print(json.dumps(out), flush=True)

@@ -56,6 +56,7 @@ struct ApplyArgs {
     int fa, fb;      // tile columns [fa, fb) are interior
     int gchunk;      // chunk groups on the grid
     int ichunk;      // chunks per wavefront
+    int nrg, brg;    // band kernel: row groups of all units, row groups per XCD band
     float scale;
     const float *nz, *x, *z;
     float *y;
@@ -1710,6 +1711,512 @@ hipError_t launch_wide(ApplyArgs a, int64_t nb, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Wide windows in 2D, workgroup form (apply_band_kernel).  Four wavefronts
+// own four consecutive image rows c2 = kBR c2g + w of the same 64 columns and
+// component pass, with the per-wavefront arithmetic of apply_wide_kernel
+// (sub-rows of kJC window columns, lane groups splitting the components).
+// The workgroup walks the kBR + 2p source rows its windows cover once: per
+// source row the x row's columns for every component of the pass are staged
+// by the four wavefronts together into a shared buffer (kBX columns, the
+// union of every sub-row's runs), and each wavefront whose window covers that
+// row runs its window row against its own staged coefficient chunks.  x thus
+// crosses the vector memory path (kBR + 2p) / kBR times per output row
+// instead of once per sub-row and component step, and the per-step staging
+// arithmetic disappears; one barrier per source row hands the x buffers over.
+//   forward:    source row u (0 .. kBR + 2p - 1) = kBR c2g - p + u serves
+//               window row dd = u - w of wavefront w
+//   transposed: the same source row serves window row dd = w + 2p - u (the
+//               coefficients are the source row's pixels')
+// ---------------------------------------------------------------------------
+constexpr int kBR = 4;   // image rows (wavefronts) per workgroup
+constexpr int kBX = 96;  // staged x columns per source row (16 NJC + 63 <= 96 for NJC <= 2)
+
+template <int NCOMP, bool TRANS>
+struct AB {
+    using W = AW<NCOMP, TRANS>;
+    static constexpr int XROW = NCOMP * kBX;            // floats per channel row
+    static constexpr int XF = kCPass / NCOMP * XROW;    // floats per source row
+    static constexpr int XP = XF / 4 / (64 * kBR);      // 16-byte loads per lane and wavefront
+    static constexpr int X1 = XF / (64 * kBR);          // 4-byte loads per lane and wavefront
+    // one chunk buffer per wavefront: a sub-row's coefficients are read into
+    // registers before the next sub-row's chunk is staged over them
+    static constexpr int LDS = 2 * XF + kBR * W::NZB;
+    static_assert(XF % (256 * kBR) == 0, "x pieces split evenly over the wavefronts");
+};
+
+// first staged x column of a source row (the reads of every sub-row start at
+// a multiple of 4 floats from it)
+__host__ __device__ __forceinline__ int band_x0(bool trans, int f1, int p, int njc) {
+    return trans ? f1 + p - kJC * (njc - 1) - (kJC - 1) : f1 - p;
+}
+
+template <int NCOMP, bool TRANS, bool FAST>
+__device__ __forceinline__ void apply_band_body(const ApplyArgs &a, int pass, int t1, int c2g,
+                                                int b) {
+    using S = AW<NCOMP, TRANS>;
+    using BB = AB<NCOMP, TRANS>;
+    constexpr int KW4 = (NCOMP * (kR + kJC - 1) + 3) / 4;
+    // chunk loads: NZ4 in the interior, NZ4 .. 4 NZ4 at the border (the
+    // waits below allow NZ4 of them in flight, which waits for more than
+    // needed when there are more)
+    constexpr int ZI = S::NZ4;
+    constexpr int XI = FAST ? BB::XP : BB::X1;
+    static_assert(4 * ZI < 64 && XI < 64, "waits exceed vmcnt");
+    typedef __attribute__((address_space(3))) void *lptr;
+    const Geom &g = a.g;
+    const int WS = g.ws, P = g.p, K = g.K;
+    const int n1 = g.n1, n2 = g.n2;
+    const int NJC = (WS + kJC - 1) / kJC;
+    const int NSR = WS * NJC;           // own sub-rows
+    const int NU = kBR + 2 * P;         // source rows of the workgroup
+    const int64_t Pp = g.P;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int l16 = lane & 15, grp = lane >> 4;
+    const int f1 = t1 * 64;
+    const int c2 = c2g * kBR + w;
+    const bool live = c2 < n2;
+    float *lxs = circatt_lds_apply;                        // 2 shared x buffers
+    float *lz = lxs + 2 * BB::XF + w * S::NZB;             // own chunk buffer
+    const auto rs = rsrc(a.nz + (int64_t)b * Pp * K, Pp * K * 4);
+    const int ubytes = (int)(Pp * NCOMP * a.C * 4);
+    const auto rx = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, ubytes);
+    const int plane = (int)(NCOMP * Pp * 4);
+    const int s2own = slot_shift(c2 + 1, n2, P);
+    const int r0 = kBR * c2g - P;   // source row of u = 0 (before wrapping)
+    const int ch0 = pass * (kCPass / NCOMP);
+    const int X0 = band_x0(TRANS, f1, P, NJC);
+
+    // ---- coefficient chunks (as apply_wide_body) ----
+    auto h0_of = [&](int jc) { return kJC * jc - P; };
+    auto col0 = [&](int jc) { return TRANS ? f1 - h0_of(jc) - (kJC - 1) : f1; };
+    // own sub-row s -> window row (in processing order: source rows ascend)
+    auto dd_of = [&](int s) {
+        const int q = s / NJC;
+        return TRANS ? WS - 1 - q : q;
+    };
+    auto zrow = [&](int dd, int &r2, int &mm) {
+        if (TRANS) {
+            r2 = pmod(c2 - (dd - P), n2);
+            mm = pmod(dd + slot_shift(r2 + 1, n2, P), WS);
+        } else {
+            r2 = c2;
+            mm = pmod(dd + s2own, WS);
+        }
+    };
+    int zo[FAST ? ZI : 1];
+    if (FAST) {
+#pragma unroll
+        for (int m = 0; m < ZI; ++m) {
+            const int f = lane + 64 * m;
+            const int kb = f / S::BLK, r = f - kb * S::BLK;
+            const int rq = r < 4 * S::Q ? r : 0;
+            const int wc = min(4 * kb + rq / S::Q, S::NSRC - 1), q = rq - (rq / S::Q) * S::Q;
+            zo[m] = (wc * K + 4 * q) * 4;
+        }
+    }
+    // Border body.  Chunk pixels may wrap along dim 1 and, within p of the
+    // image border, carry the reference's rotated slot order.  The chunk
+    // keeps the interior body's LDS layout: a DMA instruction's 64 16-byte
+    // slots whose pixels all have unrotated slots load as 16-byte pieces from
+    // their (wrapped) pixels; an instruction with a rotated pixel is issued
+    // as four 4-byte DMAs that place each slot.  Offsets are formed per
+    // sub-row (held across the walk they would not fit the register budget).
+    // The columns of a chunk or of a staged x row lie within [-n1, 2 n1)
+    // when n1 >= 2p + 80: one conditional step wraps them, except in narrow
+    // images.
+    const bool narrow = n1 < 2 * P + 80;
+    auto wrapc = [&](int x) {
+        return narrow ? pmod(x, n1) : (x < 0 ? x + n1 : (x >= n1 ? x - n1 : x));
+    };
+    // chunk pixel wc and piece q of LDS 16-byte slot f
+    auto slot_of = [&](int f, int &wc, int &q) {
+        const int kb = f / S::BLK, r = f - kb * S::BLK;
+        const int rq = r < 4 * S::Q ? r : 0;
+        wc = min(4 * kb + rq / S::Q, S::NSRC - 1);
+        q = rq - (rq / S::Q) * S::Q;
+    };
+    auto stage_z = [&](int s) {
+        const int dd = dd_of(s), jc = s - (s / NJC) * NJC;
+        int r2, mm;
+        zrow(dd, r2, mm);
+        float *dst = lz;
+        if (FAST) {
+            const int so = __builtin_amdgcn_readfirstlane(
+                ((n1 * r2 + col0(jc)) * K + mm * WS + kJC * jc) * 4);
+#pragma unroll
+            for (int m = 0; m < ZI; ++m) {
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(dst + 256 * m), 16, zo[m] + so,
+                                                        0, 0, 0);
+            }
+        } else {
+            // (loops kept rolled: the border code stays small in the
+            // instruction cache next to the interior body)
+            const int so = __builtin_amdgcn_readfirstlane((n1 * r2 * K + mm * WS) * 4);
+            const int c0 = col0(jc);
+#pragma unroll 1
+            for (int m = 0; m < S::NZ4; ++m) {
+                int wc, q;
+                slot_of(lane + 64 * m, wc, q);
+                const int col = wrapc(c0 + wc);
+                if (__builtin_amdgcn_ballot_w64(shift0(col, n1, P) != 0) == 0) {
+                    const int vo = (col * K + kJC * jc + 4 * q) * 4 + so;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(dst + 256 * m), 16, vo, 0,
+                                                            0, 0);
+                } else {
+#pragma unroll 1
+                    for (int t = 0; t < 4; ++t) {
+                        int wt, qt;
+                        slot_of(64 * m + 16 * t + (lane >> 2), wt, qt);
+                        const int ct = wrapc(c0 + wt);
+                        const int j = kJC * jc + 4 * qt + (lane & 3);
+                        const int e = j < WS ? fold(j + shift0(ct, n1, P), WS) : 0;
+                        const int vo = (ct * K + e) * 4 + so;
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(dst + 256 * m + 64 * t),
+                                                                4, vo, 0, 0, 0);
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // ---- shared x rows: this wavefront's share of source row u ----
+    // interior: 16-byte piece pc = (w XP + m) 64 + lane of the buffer, i.e.
+    // channel pc / (XROW / 4), floats 4 (pc % (XROW / 4)) ..; border: float
+    // f = (w X1 + m) 64 + lane at its wrapped column.  Channels past C lie
+    // past the unit's bytes and read as zeros.
+    int xo[FAST ? XI : 1];
+    if (FAST) {
+#pragma unroll
+        for (int m = 0; m < XI; ++m) {
+            const int pc = (w * XI + m) * 64 + lane;
+            const int c = pc / (BB::XROW / 4), q = pc - c * (BB::XROW / 4);
+            xo[m] = (ch0 + c) * plane + (NCOMP * X0 + 4 * q) * 4;
+        }
+    }
+    // border float f's offset, formed per source row (12 offsets held across
+    // the walk would not fit the register budget)
+    auto xo_border = [&](int m) {
+        const int f = (w * XI + m) * 64 + lane;
+        const int c = f / BB::XROW, e = f - c * BB::XROW;
+        const int u = e / NCOMP, comp = e - u * NCOMP;
+        return (ch0 + c) * plane + (NCOMP * wrapc(X0 + u) + comp) * 4;
+    };
+    auto stage_x = [&](int u, int buf) {
+        const int so = __builtin_amdgcn_readfirstlane(NCOMP * n1 * pmod(r0 + u, n2) * 4);
+        float *dst = lxs + buf * BB::XF + (w * XI) * (FAST ? 256 : 64);
+        if (FAST) {
+#pragma unroll
+            for (int m = 0; m < XI; ++m) {
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lptr)(dst + 256 * m), 16, xo[m] + so,
+                                                        0, 0, 0);
+            }
+        } else {
+#pragma unroll 1
+            for (int m = 0; m < XI; ++m)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lptr)(dst + 64 * m), 4,
+                                                        xo_border(m) + so, 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    float acc[kR][kCG];
+    float asum[kR];
+#pragma unroll
+    for (int i = 0; i < kR; ++i) {
+        asum[i] = 0.f;
+#pragma unroll
+        for (int k = 0; k < kCG; ++k) acc[i][k] = 0.f;
+    }
+    auto read_av = [&](float (&av)[kR][kJC], int jc) {
+        const int jn = WS - kJC * jc;
+        const float *src = lz;
+#pragma unroll
+        for (int i = 0; i < kR; ++i)
+#pragma unroll
+            for (int j = 0; j < kJC; ++j) {
+                const int c = TRANS ? i - j + kJC - 1 : i;
+                const float v = src[(4 * l16 + c) * kJC + 4 * (l16 + c / 4) + j];
+                av[i][j] = j < jn ? v : 0.f;
+            }
+    };
+
+    // Issue order per source row u: x(u + 1), then one chunk ahead per own
+    // sub-row.  The first chunk is staged before the walk (a wavefront whose
+    // window starts at a later source row waits with it in LDS).
+    stage_x(0, 0);
+    if (live) stage_z(0);
+    wait_vm<0>();
+    __syncthreads();
+    int s = 0;   // next own sub-row
+    float av[kR][kJC];
+#pragma unroll 1
+    for (int u = 0; u < NU; ++u) {
+        const bool more = u + 1 < NU;
+        if (more) stage_x(u + 1, (u + 1) & 1);
+        const int dd = TRANS ? w + 2 * P - u : u - w;
+        const bool act = live && dd >= 0 && dd < WS;
+        if (act) {
+            const float *xbase = lxs + (u & 1) * BB::XF + grp * S::CHS * BB::XROW;
+#pragma unroll 1
+            for (int jc = 0; jc < NJC; ++jc, ++s) {
+                // chunk s was issued before x(u + 1) (jc == 0) or last (jc > 0)
+                if (jc == 0 && more)
+                    wait_vm<XI>();
+                else
+                    wait_vm<0>();
+                read_av(av, jc);
+                if (a.corr) {
+#pragma unroll
+                    for (int i = 0; i < kR; ++i)
+#pragma unroll
+                        for (int j = 0; j < kJC; ++j) asum[i] += av[i][j];
+                }
+                // the chunk's reads are complete: stage the next one over it
+                __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+                if (s + 1 < NSR) stage_z(s + 1);
+                // the lane's runs start kJC jc (forward) or kJC (NJC - 1 - jc)
+                // columns into the staged row
+                const float *xr = xbase + NCOMP * (kJC * (TRANS ? NJC - 1 - jc : jc) + 4 * l16);
+                // real components: step cl + 1's runs are read while step
+                // cl's products run (two register sets); complex runs are
+                // twice as long and are read per step
+                constexpr bool PIPE = NCOMP == 1;
+                f4 xq[PIPE ? 2 : 1][KW4];
+                if (PIPE) {
+#pragma unroll
+                    for (int h = 0; h < KW4; ++h) xq[0][h] = *(const f4 *)(xr + 4 * h);
+                }
+#pragma unroll
+                for (int cl = 0; cl < S::CHS; ++cl) {
+                    const int cur = PIPE ? cl & 1 : 0;
+                    if (PIPE && cl + 1 < S::CHS) {
+#pragma unroll
+                        for (int h = 0; h < KW4; ++h)
+                            xq[(cl + 1) & 1][h] = *(const f4 *)(xr + (cl + 1) * BB::XROW + 4 * h);
+                    } else if (!PIPE) {
+#pragma unroll
+                        for (int h = 0; h < KW4; ++h)
+                            xq[0][h] = *(const f4 *)(xr + cl * BB::XROW + 4 * h);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    float xw[4 * KW4];
+#pragma unroll
+                    for (int h = 0; h < KW4; ++h) {
+                        xw[4 * h] = xq[cur][h][0];
+                        xw[4 * h + 1] = xq[cur][h][1];
+                        xw[4 * h + 2] = xq[cur][h][2];
+                        xw[4 * h + 3] = xq[cur][h][3];
+                    }
+#pragma unroll
+                    for (int i = 0; i < kR; ++i)
+#pragma unroll
+                        for (int j = 0; j < kJC; ++j)
+#pragma unroll
+                            for (int e = 0; e < NCOMP; ++e)
+                                acc[i][NCOMP * cl + e] = __builtin_fmaf(
+                                    av[i][j], xw[NCOMP * (TRANS ? i - j + kJC - 1 : i + j) + e],
+                                    acc[i][NCOMP * cl + e]);
+#pragma unroll
+                    for (int i = 0; i < kR; ++i)
+#pragma unroll
+                        for (int e = 0; e < NCOMP; ++e)
+                            asm volatile("" : "+v"(acc[i][NCOMP * cl + e]));
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+        if (more) {
+            // x(u + 1) landed; only the chunk issued last (if any) may remain
+            if (act && s < NSR)
+                wait_vm<ZI>();
+            else
+                wait_vm<0>();
+            __syncthreads();
+        }
+    }
+    if (!live) return;
+    float *yb = a.y + (int64_t)b * Pp * NCOMP * a.C;
+    const float *zb = a.z ? a.z + (int64_t)b * Pp * NCOMP * a.C : nullptr;
+    const int colf = f1 + 4 * l16;
+    const int64_t pix0 = colf + (int64_t)n1 * c2;
+#pragma unroll
+    for (int cl = 0; cl < S::CHS; ++cl) {
+        const int ch = ch0 + grp * S::CHS + cl;
+        if (ch >= a.C) break;
+        float v[kR * NCOMP];
+#pragma unroll
+        for (int i = 0; i < kR; ++i)
+#pragma unroll
+            for (int e = 0; e < NCOMP; ++e) v[NCOMP * i + e] = acc[i][NCOMP * cl + e];
+        float *dst = yb + NCOMP * (pix0 + Pp * ch);
+        const float *zs = a.corr ? zb + NCOMP * (pix0 + Pp * ch) : nullptr;
+        if (colf + kR <= n1) {
+#pragma unroll
+            for (int h = 0; h < NCOMP; ++h) {
+                f4 r = f4{v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
+                if (a.corr) {
+                    const f4u z = *(const f4u *)(zs + 4 * h);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) r[q] -= asum[(4 * h + q) / NCOMP] * z[q];
+                }
+                *(f4u *)(dst + 4 * h) = r * a.scale;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kR; ++i) {
+                if (colf + i >= n1) break;
+#pragma unroll
+                for (int e = 0; e < NCOMP; ++e) {
+                    float r = v[NCOMP * i + e];
+                    if (a.corr) r -= asum[i] * zs[NCOMP * i + e];
+                    dst[NCOMP * i + e] = r * a.scale;
+                }
+            }
+        }
+    }
+}
+
+// Work items of one product: XCD band `band` holds row groups [band brg,
+// (band + 1) brg) of all units, every tile column and pass; within a band the
+// border segments come first, so that the slower border workgroups start in
+// the first round rather than in the grid's tail.  idx < brg tiles1 gchunk;
+// returns false past the last row group.
+__device__ __forceinline__ bool band_item(const ApplyArgs &a, int band, int idx, int &pass,
+                                          int &t1, int &c2g, int &b) {
+    const int ngr = (a.g.n2 + kBR - 1) / kBR;
+    const int nit = a.fb - a.fa, nbt = a.tiles1 - nit;
+    const int nborder = a.brg * nbt * a.gchunk;
+    const bool border = idx < nborder;
+    const int per = (border ? nbt : nit) * a.gchunk;  // items per row group
+    if (!border) idx -= nborder;
+    const int rgl = idx / per, rem = idx - rgl * per;
+    const int k = rem / a.gchunk;
+    pass = rem - k * a.gchunk;
+    t1 = border ? (k < a.fa ? k : a.fb + (k - a.fa)) : a.fa + k;
+    const int rg = band * a.brg + rgl;
+    c2g = rg % ngr;
+    b = rg / ngr;
+    return rg < a.nrg;
+}
+template <int NCOMP, bool TRANS>
+__device__ __forceinline__ void apply_band_tile(const ApplyArgs &a, int pass, int t1, int c2g,
+                                                int b) {
+    if (t1 >= a.fa && t1 < a.fb)
+        apply_band_body<NCOMP, TRANS, true>(a, pass, t1, c2g, b);
+    else
+        apply_band_body<NCOMP, TRANS, false>(a, pass, t1, c2g, b);
+}
+// One workgroup of kBR wavefronts per (64 columns of kBR image rows,
+// component pass, unit); work items in XCD bands.
+// (the grid is 8 x brg x tiles1 x gchunk workgroups; blockIdx & 7 is the
+// XCD the dispatcher deals the workgroup to)
+template <int NCOMP, bool TRANS>
+__global__ __launch_bounds__(64 * kBR, 3) void apply_band_kernel(ApplyArgs a) {
+    int pass, t1, c2g, b;
+    const int band = (int)(blockIdx.x & 7), idx = (int)(blockIdx.x >> 3);
+    if (!band_item(a, band, idx, pass, t1, c2g, b)) return;
+    apply_band_tile<NCOMP, TRANS>(a, pass, t1, c2g, b);
+}
+// the similarity pullback's two products in one grid: per band, the border
+// items of both products, then the interior ones
+template <int NCOMP>
+__global__ __launch_bounds__(64 * kBR, 3) void apply_band_pair_kernel(ApplyArgs af, ApplyArgs at) {
+    const int band = (int)(blockIdx.x & 7);
+    int idx = (int)(blockIdx.x >> 3);
+    const int per = af.brg * af.tiles1 * af.gchunk;            // items per band and product
+    const int bf = af.brg * (af.tiles1 - (af.fb - af.fa)) * af.gchunk;  // border items
+    const int bt = at.brg * (at.tiles1 - (at.fb - at.fa)) * at.gchunk;
+    bool trans;
+    if (idx < bf) {
+        trans = false;
+    } else if (idx < bf + bt) {
+        trans = true;
+        idx -= bf;
+    } else {
+        idx -= bf + bt;
+        trans = idx >= per - bf;
+        idx = trans ? bt + idx - (per - bf) : bf + idx;
+    }
+    int pass, t1, c2g, b;
+    if (!band_item(trans ? at : af, band, idx, pass, t1, c2g, b)) return;
+    if (trans)
+        apply_band_tile<NCOMP, true>(at, pass, t1, c2g, b);
+    else
+        apply_band_tile<NCOMP, false>(af, pass, t1, c2g, b);
+}
+
+// geometry fields of the band kernel: segments, passes, and the interior
+// segments [fa, fb), whose staged x columns, chunk pixels and coefficient
+// slots need no wrapping and no slot shift
+template <bool TRANS>
+void set_band(ApplyArgs &a, int ncomp, int64_t nb) {
+    const Geom &g = a.g;
+    const int n1 = g.n1, p = g.p, njc = (g.ws + kJC - 1) / kJC;
+    a.tiles1 = (n1 + 63) / 64;
+    a.gchunk = (ncomp * a.C + kCPass - 1) / kCPass;
+    a.nrg = (int)(((g.n2 + kBR - 1) / kBR) * nb);
+    a.brg = (a.nrg + 7) / 8;
+    auto interior = [&](int t1) {
+        const int f1 = 64 * t1, x0 = band_x0(TRANS, f1, p, njc);
+        if (x0 < 0 || x0 + kBX > n1) return false;
+        // chunk pixels: own 64 (forward) or the sub-rows' sources (transposed)
+        const int lo = TRANS ? f1 + p - kJC * (njc - 1) - (kJC - 1) : f1;
+        const int hi = TRANS ? f1 + p + 64 : f1 + 64;  // exclusive
+        return lo >= p && hi <= n1 - p;
+    };
+    a.fa = a.tiles1;
+    a.fb = a.tiles1;
+    for (int t = 0; t < a.tiles1; ++t)
+        if (interior(t)) {
+            if (a.fa == a.tiles1) a.fa = t;
+            a.fb = t + 1;
+        }
+    if (a.fa == a.tiles1) a.fa = a.fb = 0;
+}
+
+bool band_supported(const Geom &g) { return g.nsp == 2 && g.ws > 15 && (g.ws + kJC - 1) / kJC <= 2; }
+
+// the band kernels' LDS passes 64 KiB: raise the kernel's dynamic limit once
+template <typename Kern>
+hipError_t band_lds_attr(Kern kern, size_t bytes, bool &done) {
+    if (done) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess) done = true;
+    return e;
+}
+template <int NCOMP, bool TRANS>
+hipError_t launch_band(ApplyArgs a, int64_t nb, hipStream_t s) {
+    static bool attr = false;
+    set_band<TRANS>(a, NCOMP, nb);
+    const int64_t grid = 8LL * a.brg * a.tiles1 * a.gchunk;
+    const size_t lds = (size_t)AB<NCOMP, TRANS>::LDS * sizeof(float);
+    hipError_t e = band_lds_attr(apply_band_kernel<NCOMP, TRANS>, lds, attr);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((apply_band_kernel<NCOMP, TRANS>), dim3((unsigned)grid), dim3(64 * kBR), lds,
+                       s, a);
+    return hipGetLastError();
+}
+template <int NCOMP>
+hipError_t launch_band_pair(ApplyArgs af, ApplyArgs at, int64_t nb, hipStream_t s) {
+    static bool attr = false;
+    set_band<false>(af, NCOMP, nb);
+    set_band<true>(at, NCOMP, nb);
+    const int64_t grid = 16LL * af.brg * af.tiles1 * af.gchunk;
+    const size_t lds =
+        (size_t)std::max(AB<NCOMP, false>::LDS, AB<NCOMP, true>::LDS) * sizeof(float);
+    hipError_t e = band_lds_attr(apply_band_pair_kernel<NCOMP>, lds, attr);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((apply_band_pair_kernel<NCOMP>), dim3((unsigned)grid), dim3(64 * kBR), lds,
+                       s, af, at);
+    return hipGetLastError();
+}
+
 // Interior tile columns [fa, fb): every lane row 2p or more inside dim 1.
 inline void interior_cols(const Geom &g, int &fa, int &fb) {
     const int tw = tile_w(g.nsp), tiles1 = (g.n1 + tw - 1) / tw;
@@ -1975,6 +2482,11 @@ hipError_t launch_apply_wide(bool trans, bool corr, int ncomp, const Geom &g, in
     a.x = x;
     a.z = z;
     a.y = y;
+    if (band_supported(g)) {
+        if (ncomp == 1)
+            return trans ? launch_band<1, true>(a, nb, s) : launch_band<1, false>(a, nb, s);
+        return trans ? launch_band<2, true>(a, nb, s) : launch_band<2, false>(a, nb, s);
+    }
     if (ncomp == 1)
         return trans ? launch_wide<1, true, false>(a, nb, s) : launch_wide<1, false, false>(a, nb, s);
     return trans ? launch_wide<2, true, false>(a, nb, s) : launch_wide<2, false, false>(a, nb, s);
@@ -2013,6 +2525,8 @@ hipError_t launch_apply_pair(bool corr, int ncomp, const Geom &g, int C, int64_t
     t.y = dy;
     if (pair_rows(g, C, ncomp, nb))
         return ncomp == 1 ? dispatch_pair<1>(f, t, nb, s) : dispatch_pair<2>(f, t, nb, s);
+    if (band_supported(g))
+        return ncomp == 1 ? launch_band_pair<1>(f, t, nb, s) : launch_band_pair<2>(f, t, nb, s);
     return ncomp == 1 ? launch_wide_pair<1>(f, t, nb, s) : launch_wide_pair<2>(f, t, nb, s);
 }
 

@@ -168,7 +168,10 @@ APPLY_CASES = [((8,), 5, 4), ((8, 8), 5, 4), ((12, 10), 3, 8), ((4, 4), 5, 3), (
                ((70, 40), 31, 8), ((400, 3), 17, 4), ((300,), 63, 8), ((1000,), 63, 4),
                ((37, 9), 19, 3),
                # window wider than the image along dim 1 (columns wrap more than once)
-               ((10, 40), 17, 3), ((40,), 63, 2)]
+               ((10, 40), 17, 3), ((40,), 63, 2),
+               # 2D windows 17 .. 31 (workgroup kernel over 4 image rows): interior
+               # segments, a partial last segment and a partial last row group
+               ((300, 22), 31, 8), ((150, 10), 21, 5)]
 
 
 @pytest.mark.parametrize("dims,ws,C", APPLY_CASES)
@@ -186,6 +189,42 @@ def test_apply(ca, cuda, dims, ws, C, cplx, trans):
     rs, cs = O.rowsum(nz.reshape(B, -1), P, K), O.colsum(nz.reshape(B, -1), dims, ws)
     assert rel_err(host(A.sum(2)).reshape(B, P), rs) < TOL_FWD
     assert rel_err(host(A.sum(1)).reshape(B, P), cs) < TOL_FWD
+
+
+SIM_BWD_CASES = [((20, 13), 15, 8), ((70, 40), 31, 8), ((300, 22), 31, 8), ((150, 10), 21, 5),
+                 ((400, 3), 17, 4), ((10, 40), 17, 3), ((300,), 63, 4)]
+
+
+@pytest.mark.parametrize("dims,ws,C", SIM_BWD_CASES)
+@pytest.mark.parametrize("cplx", [False, True])
+@pytest.mark.parametrize("kind", [0, 1])
+def test_similarity_bwd(ca, cuda, dims, ws, C, cplx, kind):
+    """circatt_similarity_bwd (both products in one grid) against the
+    oracle's composition of the similarity rrules (src/rrules.jl:1-32):
+    dx = s (dS ⊠ y - [Distance] rowsum(dS) .* x), dy = s (dSᵀ ⊠ x -
+    [Distance] colsum(dS) .* y)."""
+    from circulant_attention import _lib as L
+    from circulant_attention._functions import ptr, stream_ptr, geometry
+    B, P, K = 2, int(np.prod(dims)), ws ** len(dims)
+    nsp, n1, n2 = geometry(dims)
+    dS = seeded(41, (B, P, K))
+    x = seeded(42, shape_of(dims, C, B), cplx)
+    y = seeded(43, shape_of(dims, C, B), cplx)
+    scale = 0.37
+    tx, ty, tS = dev(x, cuda), dev(y, cuda), dev(dS, cuda)
+    dx, dy = torch.empty_like(tx), torch.empty_like(ty)
+    L.check(L.lib.circatt_similarity_bwd(kind, L.C32 if cplx else L.F32, nsp, n1, n2, ws, C, B,
+                                         scale, ptr(tS), ptr(tx), ptr(ty), ptr(dx), ptr(dy),
+                                         stream_ptr()))
+    torch.cuda.synchronize()
+    nzf, xf, yf = dS.reshape(B, -1), x.reshape(B, C, P), y.reshape(B, C, P)
+    rdx = O.apply(nzf, yf, dims, ws, trans=False)
+    rdy = O.apply(nzf, xf, dims, ws, trans=True)
+    if kind == 1:
+        rdx = rdx - O.rowsum(nzf, P, K)[:, None, :] * xf
+        rdy = rdy - O.colsum(nzf, dims, ws)[:, None, :] * yf
+    assert rel_err(host(dx).reshape(B, C, P), scale * rdx) < TOL_FWD
+    assert rel_err(host(dy).reshape(B, C, P), scale * rdy) < TOL_FWD
 
 
 # ---------------------------------------------------------------------------
