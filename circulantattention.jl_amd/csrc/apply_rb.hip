@@ -1731,18 +1731,26 @@ hipError_t launch_wide(ApplyArgs a, int64_t nb, hipStream_t s) {
 // ---------------------------------------------------------------------------
 constexpr int kBR = 4;   // image rows (wavefronts) per workgroup
 constexpr int kBX = 96;  // staged x columns per source row (16 NJC + 63 <= 96 for NJC <= 2)
+constexpr int kBG = 8;   // real components per lane group and pass
+constexpr int kBPass = 4 * kBG;
+constexpr int kBZ = 1;   // chunk buffers per wavefront (chunks staged kBZ sub-rows ahead;
+                         // two halve the workgroups per CU, which costs more)
 
 template <int NCOMP, bool TRANS>
 struct AB {
     using W = AW<NCOMP, TRANS>;
     static constexpr int XROW = NCOMP * kBX;            // floats per channel row
-    static constexpr int XF = kCPass / NCOMP * XROW;    // floats per source row
-    static constexpr int XP = XF / 4 / (64 * kBR);      // 16-byte loads per lane and wavefront
+    static constexpr int CHS = kBG / NCOMP;             // channels per lane group and pass
+    static constexpr int XF = kBPass / NCOMP * XROW;    // floats per source row
+    static constexpr int PPW = XF / 4 / kBR;            // 16-byte pieces per wavefront
+    static constexpr int XP = (PPW + 63) / 64;          // 16-byte loads per lane and wavefront
+    static constexpr int XPL = PPW - 64 * (XP - 1);     // lanes of the last one
     static constexpr int X1 = XF / (64 * kBR);          // 4-byte loads per lane and wavefront
-    // one chunk buffer per wavefront: a sub-row's coefficients are read into
-    // registers before the next sub-row's chunk is staged over them
-    static constexpr int LDS = 2 * XF + kBR * W::NZB;
-    static_assert(XF % (256 * kBR) == 0, "x pieces split evenly over the wavefronts");
+    // kBZ chunk buffers per wavefront: sub-row s's chunk goes to buffer
+    // s % kBZ once sub-row s - kBZ's coefficients are in registers
+    static constexpr int LDS = 2 * XF + kBR * kBZ * W::NZB;
+    static_assert(XF % (64 * kBR) == 0 && XF % (16 * kBR) == 0,
+                  "x floats and pieces split evenly over the wavefronts");
 };
 
 // first staged x column of a source row (the reads of every sub-row start at
@@ -1778,14 +1786,14 @@ __device__ __forceinline__ void apply_band_body(const ApplyArgs &a, int pass, in
     const int c2 = c2g * kBR + w;
     const bool live = c2 < n2;
     float *lxs = circatt_lds_apply;                        // 2 shared x buffers
-    float *lz = lxs + 2 * BB::XF + w * S::NZB;             // own chunk buffer
+    float *lz = lxs + 2 * BB::XF + w * kBZ * S::NZB;       // own chunk buffers
     const auto rs = rsrc(a.nz + (int64_t)b * Pp * K, Pp * K * 4);
     const int ubytes = (int)(Pp * NCOMP * a.C * 4);
     const auto rx = rsrc(a.x + (int64_t)b * Pp * NCOMP * a.C, ubytes);
     const int plane = (int)(NCOMP * Pp * 4);
     const int s2own = slot_shift(c2 + 1, n2, P);
     const int r0 = kBR * c2g - P;   // source row of u = 0 (before wrapping)
-    const int ch0 = pass * (kCPass / NCOMP);
+    const int ch0 = pass * (kBPass / NCOMP);
     const int X0 = band_x0(TRANS, f1, P, NJC);
 
     // ---- coefficient chunks (as apply_wide_body) ----
@@ -1841,7 +1849,7 @@ __device__ __forceinline__ void apply_band_body(const ApplyArgs &a, int pass, in
         const int dd = dd_of(s), jc = s - (s / NJC) * NJC;
         int r2, mm;
         zrow(dd, r2, mm);
-        float *dst = lz;
+        float *dst = lz + (s % kBZ) * S::NZB;
         if (FAST) {
             const int so = __builtin_amdgcn_readfirstlane(
                 ((n1 * r2 + col0(jc)) * K + mm * WS + kJC * jc) * 4);
@@ -1892,7 +1900,7 @@ __device__ __forceinline__ void apply_band_body(const ApplyArgs &a, int pass, in
     if (FAST) {
 #pragma unroll
         for (int m = 0; m < XI; ++m) {
-            const int pc = (w * XI + m) * 64 + lane;
+            const int pc = w * BB::PPW + 64 * m + lane;
             const int c = pc / (BB::XROW / 4), q = pc - c * (BB::XROW / 4);
             xo[m] = (ch0 + c) * plane + (NCOMP * X0 + 4 * q) * 4;
         }
@@ -1907,13 +1915,14 @@ __device__ __forceinline__ void apply_band_body(const ApplyArgs &a, int pass, in
     };
     auto stage_x = [&](int u, int buf) {
         const int so = __builtin_amdgcn_readfirstlane(NCOMP * n1 * pmod(r0 + u, n2) * 4);
-        float *dst = lxs + buf * BB::XF + (w * XI) * (FAST ? 256 : 64);
+        float *dst = lxs + buf * BB::XF + (FAST ? 4 * w * BB::PPW : w * XI * 64);
         if (FAST) {
 #pragma unroll
             for (int m = 0; m < XI; ++m) {
                 __builtin_amdgcn_sched_barrier(0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lptr)(dst + 256 * m), 16, xo[m] + so,
-                                                        0, 0, 0);
+                if (m + 1 < XI || BB::XPL == 64 || lane < BB::XPL)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lptr)(dst + 256 * m), 16,
+                                                            xo[m] + so, 0, 0, 0);
             }
         } else {
 #pragma unroll 1
@@ -1924,32 +1933,62 @@ __device__ __forceinline__ void apply_band_body(const ApplyArgs &a, int pass, in
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    float acc[kR][kCG];
+    float acc[kR][kBG];
     float asum[kR];
 #pragma unroll
     for (int i = 0; i < kR; ++i) {
         asum[i] = 0.f;
 #pragma unroll
-        for (int k = 0; k < kCG; ++k) acc[i][k] = 0.f;
+        for (int k = 0; k < kBG; ++k) acc[i][k] = 0.f;
     }
-    auto read_av = [&](float (&av)[kR][kJC], int jc) {
+    // slots jn .. kJC - 1 of a window row's last sub-row lie past the window:
+    // once the chunk has landed they are cleared in LDS, so that the reads
+    // below need no mask (chunk pixel wc, slot j at 16 wc + 4 (wc / 4) + j)
+    auto clear_tail = [&](int jc, float *zb) {
         const int jn = WS - kJC * jc;
-        const float *src = lz;
+#pragma unroll 1
+        for (int j = jn; j < kJC; ++j) {
+#pragma unroll
+            for (int h = 0; h < (S::NSRC + 63) / 64; ++h) {
+                const int wc = lane + 64 * h;
+                if (wc < S::NSRC) zb[16 * wc + 4 * (wc >> 2) + j] = 0.f;
+            }
+        }
+    };
+    auto read_av = [&](float (&av)[kR][kJC], const float *src) {
 #pragma unroll
         for (int i = 0; i < kR; ++i)
 #pragma unroll
             for (int j = 0; j < kJC; ++j) {
                 const int c = TRANS ? i - j + kJC - 1 : i;
-                const float v = src[(4 * l16 + c) * kJC + 4 * (l16 + c / 4) + j];
-                av[i][j] = j < jn ? v : 0.f;
+                av[i][j] = src[(4 * l16 + c) * kJC + 4 * (l16 + c / 4) + j];
             }
     };
 
-    // Issue order per source row u: x(u + 1), then one chunk ahead per own
-    // sub-row.  The first chunk is staged before the walk (a wavefront whose
-    // window starts at a later source row waits with it in LDS).
+    // Issue order per source row u: x(u + 1), then per own sub-row s the
+    // chunk of sub-row s + kBZ.  The first kBZ chunks are staged before the
+    // walk (a wavefront whose window starts at a later source row waits with
+    // them in LDS).  The waits count the loads issued after the ones needed:
+    // chunks s + 1 .. s + kBZ - 1 (ZI each, fewer at the end), and x(u + 1)
+    // when chunk s was issued before source row u began (jc < kBZ).
+    auto wait_after = [&](int nz, bool nx) {
+        if (nx) {
+            if (nz >= 2) wait_vm<2 * ZI + XI>();
+            else if (nz == 1) wait_vm<ZI + XI>();
+            else wait_vm<XI>();
+        } else {
+            if (nz >= 2) wait_vm<2 * ZI>();
+            else if (nz == 1) wait_vm<ZI>();
+            else wait_vm<0>();
+        }
+    };
+    static_assert(kBZ <= 3, "wait_after covers up to two younger chunks");
     stage_x(0, 0);
-    if (live) stage_z(0);
+    if (live) {
+#pragma unroll
+        for (int k = 0; k < kBZ; ++k)
+            if (k < NSR) stage_z(k);
+    }
     wait_vm<0>();
     __syncthreads();
     int s = 0;   // next own sub-row
@@ -1961,24 +2000,19 @@ __device__ __forceinline__ void apply_band_body(const ApplyArgs &a, int pass, in
         const int dd = TRANS ? w + 2 * P - u : u - w;
         const bool act = live && dd >= 0 && dd < WS;
         if (act) {
-            const float *xbase = lxs + (u & 1) * BB::XF + grp * S::CHS * BB::XROW;
+            const float *xbase = lxs + (u & 1) * BB::XF + grp * BB::CHS * BB::XROW;
 #pragma unroll 1
             for (int jc = 0; jc < NJC; ++jc, ++s) {
-                // chunk s was issued before x(u + 1) (jc == 0) or last (jc > 0)
-                if (jc == 0 && more)
-                    wait_vm<XI>();
-                else
-                    wait_vm<0>();
-                read_av(av, jc);
+                wait_after(min(kBZ - 1, NSR - 1 - s), more && jc < kBZ);
+                float *zb = lz + (s % kBZ) * S::NZB;
+                clear_tail(jc, zb);
+                read_av(av, zb);
                 if (a.corr) {
 #pragma unroll
                     for (int i = 0; i < kR; ++i)
 #pragma unroll
                         for (int j = 0; j < kJC; ++j) asum[i] += av[i][j];
                 }
-                // the chunk's reads are complete: stage the next one over it
-                __builtin_amdgcn_s_waitcnt(kWaitLgkm);
-                if (s + 1 < NSR) stage_z(s + 1);
                 // the lane's runs start kJC jc (forward) or kJC (NJC - 1 - jc)
                 // columns into the staged row
                 const float *xr = xbase + NCOMP * (kJC * (TRANS ? NJC - 1 - jc : jc) + 4 * l16);
@@ -1992,9 +2026,9 @@ __device__ __forceinline__ void apply_band_body(const ApplyArgs &a, int pass, in
                     for (int h = 0; h < KW4; ++h) xq[0][h] = *(const f4 *)(xr + 4 * h);
                 }
 #pragma unroll
-                for (int cl = 0; cl < S::CHS; ++cl) {
+                for (int cl = 0; cl < BB::CHS; ++cl) {
                     const int cur = PIPE ? cl & 1 : 0;
-                    if (PIPE && cl + 1 < S::CHS) {
+                    if (PIPE && cl + 1 < BB::CHS) {
 #pragma unroll
                         for (int h = 0; h < KW4; ++h)
                             xq[(cl + 1) & 1][h] = *(const f4 *)(xr + (cl + 1) * BB::XROW + 4 * h);
@@ -2027,15 +2061,20 @@ __device__ __forceinline__ void apply_band_body(const ApplyArgs &a, int pass, in
                         for (int e = 0; e < NCOMP; ++e)
                             asm volatile("" : "+v"(acc[i][NCOMP * cl + e]));
                     __builtin_amdgcn_sched_barrier(0);
+                    if (cl == 0) {
+                        // step 0 has consumed every coefficient, so the
+                        // chunk's reads are complete: stage the next one over
+                        // it (the reads' latency was covered by step 0)
+                        __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+                        if (s + kBZ < NSR) stage_z(s + kBZ);
+                    }
                 }
             }
         }
         if (more) {
-            // x(u + 1) landed; only the chunk issued last (if any) may remain
-            if (act && s < NSR)
-                wait_vm<ZI>();
-            else
-                wait_vm<0>();
+            // x(u + 1) landed; the chunks issued during this source row (if
+            // any) may remain
+            wait_after(act ? min(NJC, max(0, NSR - kBZ - (s - NJC))) : 0, false);
             __syncthreads();
         }
     }
@@ -2045,8 +2084,8 @@ __device__ __forceinline__ void apply_band_body(const ApplyArgs &a, int pass, in
     const int colf = f1 + 4 * l16;
     const int64_t pix0 = colf + (int64_t)n1 * c2;
 #pragma unroll
-    for (int cl = 0; cl < S::CHS; ++cl) {
-        const int ch = ch0 + grp * S::CHS + cl;
+    for (int cl = 0; cl < BB::CHS; ++cl) {
+        const int ch = ch0 + grp * BB::CHS + cl;
         if (ch >= a.C) break;
         float v[kR * NCOMP];
 #pragma unroll
@@ -2158,7 +2197,7 @@ void set_band(ApplyArgs &a, int ncomp, int64_t nb) {
     const Geom &g = a.g;
     const int n1 = g.n1, p = g.p, njc = (g.ws + kJC - 1) / kJC;
     a.tiles1 = (n1 + 63) / 64;
-    a.gchunk = (ncomp * a.C + kCPass - 1) / kCPass;
+    a.gchunk = (ncomp * a.C + kBPass - 1) / kBPass;
     a.nrg = (int)(((g.n2 + kBR - 1) / kBR) * nb);
     a.brg = (a.nrg + 7) / 8;
     auto interior = [&](int t1) {
