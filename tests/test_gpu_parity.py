@@ -171,7 +171,11 @@ APPLY_CASES = [((8,), 5, 4), ((8, 8), 5, 4), ((12, 10), 3, 8), ((4, 4), 5, 3), (
                ((10, 40), 17, 3), ((40,), 63, 2),
                # 2D windows 17 .. 31 (workgroup kernel over 4 image rows): interior
                # segments, a partial last segment and a partial last row group
-               ((300, 22), 31, 8), ((150, 10), 21, 5)]
+               ((300, 22), 31, 8), ((150, 10), 21, 5),
+               # 2D windows 13 and 15 on small grids (the same kernel with the deep
+               # schedule and 16-component passes): interior and border segments,
+               # odd channel counts, rows fewer than the window
+               ((300, 14), 15, 8), ((130, 9), 13, 5), ((70, 6), 15, 20)]
 
 
 @pytest.mark.parametrize("dims,ws,C", APPLY_CASES)
@@ -192,7 +196,8 @@ def test_apply(ca, cuda, dims, ws, C, cplx, trans):
 
 
 SIM_BWD_CASES = [((20, 13), 15, 8), ((70, 40), 31, 8), ((300, 22), 31, 8), ((150, 10), 21, 5),
-                 ((400, 3), 17, 4), ((10, 40), 17, 3), ((300,), 63, 4)]
+                 ((400, 3), 17, 4), ((10, 40), 17, 3), ((300,), 63, 4), ((300, 14), 15, 8),
+                 ((130, 9), 13, 5), ((40, 30), 11, 8)]
 
 
 @pytest.mark.parametrize("dims,ws,C", SIM_BWD_CASES)
