@@ -170,6 +170,13 @@ hipError_t launch_f2d(FusedMode mode, const FusedProblem &pr, hipStream_t s) {
         if (mode == MODE_BWDKV) e = launch_f2h_bwdkv(pr.g.p, cplx, dist, a, cus, s);
         if (e != hipErrorNotSupported) return e;
     }
+    if (nt == 2 && math_mode() == CIRCATT_MATH_SPLIT_F16) {
+        hipError_t e = hipErrorNotSupported;
+        if (mode == MODE_FWD) e = launch_f2h2_fwd(pr.g.p, cplx, dist, a, cus, s);
+        if (mode == MODE_BWDQ) e = launch_f2h2_bwdq(pr.g.p, cplx, dist, a, cus, s);
+        if (mode == MODE_BWDKV) e = launch_f2h2_bwdkv(pr.g.p, cplx, dist, a, cus, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     switch (mode) {
     case MODE_FWD: return launch_f2d_fwd(pr.g.p, nt, cplx, dist, a, cus, s);
     case MODE_BWDQ: return launch_f2d_bwdq(pr.g.p, nt, cplx, dist, a, cus, s);

@@ -1,0 +1,12 @@
+// Instantiations of the split-half kernel for 32 real components per head,
+// forward (fused2h_impl.h).
+#include "fused2h_impl.h"
+
+namespace circatt {
+
+hipError_t launch_f2h2_fwd(int p, bool cplx, bool dist, const f2d::Args &a, int cus,
+                           hipStream_t s) {
+    return f2h::dispatch<f2h::FWD, 2>(p, cplx, dist, a, cus, s);
+}
+
+}  // namespace circatt

@@ -5,7 +5,7 @@ namespace circatt {
 
 hipError_t launch_f2h_bwdq(int p, bool cplx, bool dist, const f2d::Args &a, int cus,
                           hipStream_t s) {
-    return f2h::dispatch<f2h::BWDQ>(p, cplx, dist, a, cus, s);
+    return f2h::dispatch<f2h::BWDQ, 1>(p, cplx, dist, a, cus, s);
 }
 
 }  // namespace circatt

@@ -5,7 +5,7 @@ namespace circatt {
 
 hipError_t launch_f2h_fwd(int p, bool cplx, bool dist, const f2d::Args &a, int cus,
                           hipStream_t s) {
-    return f2h::dispatch<f2h::FWD>(p, cplx, dist, a, cus, s);
+    return f2h::dispatch<f2h::FWD, 1>(p, cplx, dist, a, cus, s);
 }
 
 }  // namespace circatt

@@ -166,7 +166,16 @@ __device__ __forceinline__ void walk_prio() {
     if constexpr (CIRCATT_F2H_PRIO && I * 4 % N < 4) __builtin_amdgcn_s_setprio(3 - I * 4 / N);
 }
 
-constexpr int KS = 40;  // halves per pixel slot: 16 hi, 16 lo, 8 pad (80 bytes)
+// LDS pixel slot: NT sub-pixels of 16 channels, each [16 hi | 16 lo] halves
+// (64 bytes), then 8 halves of pad: 80 bytes for 16 real components, 144 for
+// 32 (both strides keep the 16-byte row reads free of bank conflicts)
+template <int NT>
+constexpr int slot_bytes() { return (32 * NT + 8) * 2; }
+// Workgroup grid: 2 x 8 wavefronts (16x16 tiles) for 16 real components per
+// pixel; 1 x 8 (8x16 tiles) for 32, whose two staged tensors would not fit
+// LDS on the larger tile
+template <int NT>
+constexpr int grid_wh() { return NT == 1 ? 2 : 1; }
 
 // ---- power-of-two operand scaling ----
 // f16 halves lose Float32's range: lo turns subnormal (spacing 2^-24) once
@@ -239,11 +248,12 @@ __device__ __forceinline__ void reg_split(const float (&x)[8], float sc, h8 &hi,
 
 enum { FWD = f2d::FWD, BWDQ = f2d::BWDQ, BWDKV = f2d::BWDKV };
 
-template <int P, int MODE, bool DIST>
+template <int P, int NT, int MODE, bool DIST>
 struct LGeo {
-    using G = f2d::Geo<P, 1, 2, 8>;
+    using G = f2d::Geo<P, 1, grid_wh<NT>(), 8>;
+    static constexpr int SB = slot_bytes<NT>();
     static constexpr int OT0 = 0;                  // tensor 0 slots (K, or Q in BWDKV)
-    static constexpr int OT1 = G::LPX * KS * 2;    // tensor 1 slots (V, or dY in BWDKV)
+    static constexpr int OT1 = G::LPX * SB;        // tensor 1 slots (V, or dY in BWDKV)
     static constexpr int OS0 = 2 * OT1;            // Float32 scalars per slot
     static constexpr int OS1 = OS0 + G::LPX * 4;
     static constexpr int NSCAL = MODE == BWDKV ? 2 : (DIST ? 1 : 0);
@@ -252,13 +262,20 @@ struct LGeo {
     static constexpr int bytes = OX + 16;
 };
 
-template <int P, bool CPLX, bool DIST, int MODE, bool CL>
-__global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
-    using G = f2d::Geo<P, 1, 2, 8>;
-    using L = LGeo<P, MODE, DIST>;
-    constexpr int WH = 2;
+// NT: 16-channel sub-pixels per pixel (1 or 2, i.e. 16 or 32 real components)
+template <int P, int NT, bool CPLX, bool DIST, int MODE, bool CL>
+__global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
+    constexpr int WH = grid_wh<NT>();
+    using G = f2d::Geo<P, 1, WH, 8>;
+    using L = LGeo<P, NT, MODE, DIST>;
+    constexpr int SB = L::SB;
     constexpr int CR = G::CR, HH = G::HH, HWD = G::HWD, NKW = G::NKW, NBLK = G::NBLK;
-    constexpr int NPX = G::NPX;
+    // staged columns: all HWD slot columns on the 16x16 tile; on the 8x16
+    // tile only the TW + 2P that lie in some query's window (the slot columns
+    // past them are read by the last LDS blocks under the window mask and
+    // hold zeros, written once)
+    constexpr int SWC = NT == 1 ? HWD : G::TW + 2 * P;
+    constexpr int NPX = HH * SWC;
     constexpr int NPAIR = (NBLK + 1) / 2;
     constexpr bool KV = MODE == BWDKV;
     // forward: pair chunks whose scores are held in registers at once
@@ -288,7 +305,8 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                         : MODE == BWDQ              ? NPAIR / CIRCATT_F2H_BWDQ_PFD
                                                     : NPAIR / CIRCATT_F2H_BWD_PFD;
     static_assert(PFP >= 0 && PFP < NPAIR, "the next item's loads must be issued in the walk");
-    static_assert(NPX <= 1024, "one staged pixel per thread");
+    static_assert(NPX <= G::THREADS, "one staged pixel per thread");
+    static_assert(NT == 1 || NT == 2, "16 or 32 real components per head");
     static_assert(HH % 2 == 0, "row pairs");
     char *const lds = reinterpret_cast<char *>(circatt_lds2);
 
@@ -303,27 +321,28 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     };
     // score-type rows: element j of a block, halves 8 g .. 8 g + 7 of its slot
     const int slotA = 8 * wh + (j & 1) + CR * (2 * ww + (j >> 1));
-    const char *const pA0 = lds + opaque(L::OT0 + slotA * KS * 2 + 16 * g);
-    const char *const pA1 = lds + opaque(L::OT1 + slotA * KS * 2 + 16 * g);
+    const char *const pA0 = lds + opaque(L::OT0 + slotA * SB + 16 * g);
+    const char *const pA1 = lds + opaque(L::OT1 + slotA * SB + 16 * g);
     // apply-type rows from slots by transposing reads: lane (j, g) receives
     // channel j (hi; lo 16 halves further) of elements 4g + t, t = 0..3, so
     // lane j of group g addresses channels 4 (j & 3) .. + 3 of element
     // 4g + (j >> 2), which sits at row (j >> 2) & 1, column 2g + (j >> 3)
     const int slotE = 8 * wh + CR * (2 * ww + 2 * g);
     const int slotT = slotE + ((j >> 2) & 1) + CR * (j >> 3);
-    const char *const pR0 = lds + opaque(L::OT0 + slotT * KS * 2 + 8 * (j & 3));
-    const char *const pR1 = lds + opaque(L::OT1 + slotT * KS * 2 + 8 * (j & 3));
+    const char *const pR0 = lds + opaque(L::OT0 + slotT * SB + 8 * (j & 3));
+    const char *const pR1 = lds + opaque(L::OT1 + slotT * SB + 8 * (j & 3));
     // per-slot Float32 scalars of elements 4g .. 4g+3
     const float *const pS0 = reinterpret_cast<const float *>(lds + opaque(L::OS0 + slotE * 4));
     const float *const pS1 = reinterpret_cast<const float *>(lds + opaque(L::OS1 + slotE * 4));
 
     // ---- prefetch registers ----
-    float h0v[16], h1v[16], hs0 = 0.f, hs1 = 0.f;
+    float h0v[16 * NT], h1v[16 * NT], hs0 = 0.f, hs1 = 0.f;
     int hslot;
     // register operands: lane groups g and g ^ 2 (lanes l, l ^ 32) share a
-    // pixel and its channels 8 (g & 1) .. + 7; each loads half of them,
-    // components 8 (g & 1) + 4 (g >> 1) + t, and a lane swap joins the halves
-    float nh0[4], nh1[4], nry[4];
+    // pixel and its channels 8 (g & 1) .. + 7 of each sub-pixel h; each loads
+    // half of them, components 16 h + 8 (g & 1) + 4 (g >> 1) + t, and a lane
+    // swap joins the halves
+    float nh0[NT][4], nh1[NT][4], nry[NT][4];
     float nlse = 0.f;
 
     // register pixel of this lane in the tile at (h0, w0)
@@ -365,7 +384,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         const int gp = gh + a.n1 * gw;
         if constexpr (CPLX) {
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
+            for (int c = 0; c < 8 * NT; ++c) {
                 const int vo = f2d::pix_off<true, CL>(a, gp) * 4, so = f2d::comp_soff<true, CL>(a, 2 * c) * 4;
                 const f2d::f2 x0 = f2d::bload2(r0, vo, so);
                 const f2d::f2 x1 = f2d::bload2(r1, vo, so);
@@ -376,7 +395,7 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             }
         } else {
 #pragma unroll
-            for (int c = 0; c < 16; ++c) {
+            for (int c = 0; c < 16 * NT; ++c) {
                 const int vo = f2d::pix_off<false, CL>(a, gp) * 4, so = f2d::comp_soff<false, CL>(a, c) * 4;
                 h0v[c] = f2d::bload(r0, vo, so);
                 h1v[c] = f2d::bload(r1, vo, so);
@@ -396,14 +415,17 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         const int ubytes = f2d::unit_bytes<CL>(a, unit);
         const auto r0 = f2d::rsrc((KV ? a.k : a.q) + uoff, ubytes);
         const auto r1 = f2d::rsrc((KV ? a.v : a.dy) + uoff, ubytes);
-        const int vo = f2d::comp_off<CPLX, CL>(a, rpix, 8 * (g & 1) + 4 * (g >> 1)) * 4;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int so = f2d::comp_soff<CPLX, CL>(a, t) * 4;
-            nh0[t] = f2d::bload(r0, vo, so);
-            if constexpr (MODE != FWD) nh1[t] = f2d::bload(r1, vo, so);
-            // y beside dy, for D = <dy, y>
-            if constexpr (MODE == BWDQ) nry[t] = f2d::bload(f2d::rsrc(a.y + uoff, ubytes), vo, so);
+        for (int h = 0; h < NT; ++h) {
+            const int vo = f2d::comp_off<CPLX, CL>(a, rpix, 16 * h + 8 * (g & 1) + 4 * (g >> 1)) * 4;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int so = f2d::comp_soff<CPLX, CL>(a, t) * 4;
+                nh0[h][t] = f2d::bload(r0, vo, so);
+                if constexpr (MODE != FWD) nh1[h][t] = f2d::bload(r1, vo, so);
+                // y beside dy, for D = <dy, y>
+                if constexpr (MODE == BWDQ) nry[h][t] = f2d::bload(f2d::rsrc(a.y + uoff, ubytes), vo, so);
+            }
         }
         if constexpr (MODE == BWDQ)
             nlse = f2d::bload(f2d::rsrc(a.lse + (int64_t)unit * a.P, a.P * 4), rpix * 4, 0);
@@ -415,6 +437,19 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
     F2H_PHASE(uint64_t phase[4] = {0, 0, 0, 0};)
     unsigned *const xwords = reinterpret_cast<unsigned *>(lds + L::OX);
     if (threadIdx.x < 4) xwords[threadIdx.x] = 0u;
+    if constexpr (SWC < HWD) {
+        // slot columns past the staged ones: zero halves and scalars, so that
+        // the masked products over them stay finite
+        constexpr int Z0 = CR * SWC, ZN = CR * (HWD - SWC);
+        for (int i = threadIdx.x; i < ZN; i += G::THREADS) {
+            f4 *const z0 = reinterpret_cast<f4 *>(lds + L::OT0 + (Z0 + i) * SB);
+            f4 *const z1 = reinterpret_cast<f4 *>(lds + L::OT1 + (Z0 + i) * SB);
+#pragma unroll
+            for (int q = 0; q < SB / 16; ++q) z0[q] = z1[q] = f4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (L::NSCAL >= 1) reinterpret_cast<float *>(lds + L::OS0)[Z0 + i] = 0.f;
+            if constexpr (L::NSCAL >= 2) reinterpret_cast<float *>(lds + L::OS1)[Z0 + i] = 0.f;
+        }
+    }
     int unit, h0, w0;
     decode(item, unit, h0, w0);
     load_stage(unit, h0, w0);
@@ -441,7 +476,11 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 u0 = __float_as_uint(maxabs(h0v));
                 u1 = __float_as_uint(maxabs(h1v));
             }
-            if constexpr (KV) u2 = __float_as_uint(maxabs(nh1));
+            if constexpr (KV) {
+                float m2 = maxabs(nh1[0]);
+                if constexpr (NT == 2) m2 = fmaxf(m2, maxabs(nh1[1]));
+                u2 = __float_as_uint(m2);
+            }
             u0 = wave_umax63(u0);
             u1 = wave_umax63(u1);
             if constexpr (KV) u2 = wave_umax63(u2);
@@ -468,12 +507,27 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             float n2 = 0.f;
             if constexpr (DIST) {
 #pragma unroll
-                for (int c = 0; c < 16; ++c) n2 += h0v[c] * h0v[c];
+                for (int c = 0; c < 16 * NT; ++c) n2 += h0v[c] * h0v[c];
             }
-            char *const sl0 = lds + L::OT0 + hslot * KS * 2;
-            char *const sl1 = lds + L::OT1 + hslot * KS * 2;
-            if (s0 == 0) store_slot(sl0, h0v); else store_slot<true>(sl0, h0v, s0);
-            if (s1 == 0) store_slot(sl1, h1v); else store_slot<true>(sl1, h1v, s1);
+            char *const sl0 = lds + L::OT0 + hslot * SB;
+            char *const sl1 = lds + L::OT1 + hslot * SB;
+            if constexpr (NT == 1) {
+                if (s0 == 0) store_slot(sl0, h0v); else store_slot<true>(sl0, h0v, s0);
+                if (s1 == 0) store_slot(sl1, h1v); else store_slot<true>(sl1, h1v, s1);
+            } else {
+                // sub-pixel h of the slot at byte 64 h
+                float x0[2][16], x1[2][16];
+#pragma unroll
+                for (int c = 0; c < 32; ++c) {
+                    x0[c >> 4][c & 15] = h0v[c];
+                    x1[c >> 4][c & 15] = h1v[c];
+                }
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    if (s0 == 0) store_slot(sl0 + 64 * h, x0[h]); else store_slot<true>(sl0 + 64 * h, x0[h], s0);
+                    if (s1 == 0) store_slot(sl1 + 64 * h, x1[h]); else store_slot<true>(sl1 + 64 * h, x1[h], s1);
+                }
+            }
             if constexpr (KV) {
                 // staged queries: A_q = -lse log2(e) [- c2 |q|^2 / 2], and
                 // -D in the scale of the dP product
@@ -487,8 +541,8 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         }
         // register operands (the score product's side pre-scaled by c2):
         // channels 8 (g & 1) + t from the lower half of the wave, + 4 + t
-        // from the upper half
-        float nr0[8], nr1[8];
+        // from the upper half, for each sub-pixel h
+        float nr0[NT][8], nr1[NT][8];
         auto join = [](const float (&h)[4], float (&x)[8]) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -498,7 +552,8 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 x[4 + t] = __uint_as_float(r[1]);
             }
         };
-        join(nh0, nr0);
+#pragma unroll
+        for (int h = 0; h < NT; ++h) join(nh0[h], nr0[h]);
         // The score product's register operand absorbs the staged tensor's
         // shift (q' = q c2 2^-s0 against k' = k 2^s0), so scores keep their
         // scale.  A wave whose |q'| reaches 2^15 (the halves would overflow)
@@ -507,60 +562,79 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
         // overflow the dS halves) takes the slow walk: q normalised per pixel
         // and each score unscaled after its product.
         const float c2s = __builtin_amdgcn_ldexpf(c2, -s0);
-        const float mr0 = maxabs(nr0);
+        float mr0 = maxabs(nr0[0]);
+        if constexpr (NT == 2) mr0 = fmaxf(mr0, maxabs(nr0[1]));
         const float lim = MODE == FWD ? 32768.f
                                       : fminf(32768.f, __builtin_amdgcn_ldexpf(1.f, 16 - scaled_exp(b0)));
         const bool slow = __builtin_amdgcn_ballot_w64(!(mr0 * c2s < lim)) != 0;
         // slow walk: q c2 shifted per pixel to [4, 8), products scaled by 2^eu
         int eu = 0;
-        h8 r0h, r0l, r1h, r1l;
+        h8 r0h[NT], r0l[NT], r1h[NT], r1l[NT];
         if (slow) {
             const int sp = min(120, max(-120, 129 - (int)bexp(gmax(mr0) * c2)));
             eu = sp + s0;
-            reg_split(nr0, __builtin_amdgcn_ldexpf(c2, sp), r0h, r0l);
+#pragma unroll
+            for (int h = 0; h < NT; ++h) reg_split(nr0[h], __builtin_amdgcn_ldexpf(c2, sp), r0h[h], r0l[h]);
         } else {
-            reg_split(nr0, c2s, r0h, r0l);
+#pragma unroll
+            for (int h = 0; h < NT; ++h) reg_split(nr0[h], c2s, r0h[h], r0l[h]);
         }
         // dy (query-centric pass) is shifted per register pixel; v
         // (key-centric pass) by the block-wide s2
         int sd = 0;
-        if constexpr (MODE != FWD) join(nh1, nr1);
+        if constexpr (MODE != FWD) {
+#pragma unroll
+            for (int h = 0; h < NT; ++h) join(nh1[h], nr1[h]);
+        }
+        auto split_r1 = [&](float sc) {
+#pragma unroll
+            for (int h = 0; h < NT; ++h) reg_split(nr1[h], sc, r1h[h], r1l[h]);
+        };
         if constexpr (MODE == BWDQ) {
-            sd = shift_of(bexp(gmax(maxabs(nr1))));
+            float mr1 = maxabs(nr1[0]);
+            if constexpr (NT == 2) mr1 = fmaxf(mr1, maxabs(nr1[1]));
+            sd = shift_of(bexp(gmax(mr1)));
             if (__builtin_amdgcn_ballot_w64(sd != 0) != 0)
-                reg_split(nr1, __builtin_amdgcn_ldexpf(1.f, sd), r1h, r1l);
+                split_r1(__builtin_amdgcn_ldexpf(1.f, sd));
             else
-                reg_split(nr1, 1.f, r1h, r1l);
+                split_r1(1.f);
         } else if constexpr (MODE == BWDKV) {
             if (s2 != 0)
-                reg_split(nr1, __builtin_amdgcn_ldexpf(1.f, s2), r1h, r1l);
+                split_r1(__builtin_amdgcn_ldexpf(1.f, s2));
             else
-                reg_split(nr1, 1.f, r1h, r1l);
+                split_r1(1.f);
         }
         // sums of the loaded halves over the four lane groups count every
         // channel once
         float raw2 = 0.f, rowD = 0.f, rowL = 0.f;
         if constexpr (DIST) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) raw2 += nh0[t] * nh0[t];
+            for (int h = 0; h < NT; ++h)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) raw2 += nh0[h][t] * nh0[h][t];
         }
         if constexpr (MODE == BWDQ) {
             float dd = 0.f;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) dd += nh1[t] * nry[t];
+            for (int h = 0; h < NT; ++h)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) dd += nh1[h][t] * nry[h][t];
             rowD = gsum(dd);
             rowL = nlse;
         }
         const float sq = DIST ? gsum(raw2) : 0.f;
         // Distance correction of the outputs needs the register pixel's
-        // channels 4 g + r (the output layout): channel 4 g + r sits at
-        // index 4 (g & 1) + r in lane group g' = (g >> 1) + 2 (g & 1), whose
-        // groups >= 2 offer indices 4..7 and groups < 2 indices 0..3.
-        float reg0[4] = {0.f, 0.f, 0.f, 0.f};
+        // channels 16 h + 4 g + r (the output layout): channel 4 g + r of a
+        // sub-pixel sits at index 4 (g & 1) + r in lane group
+        // g' = (g >> 1) + 2 (g & 1), whose groups >= 2 offer indices 4..7 and
+        // groups < 2 indices 0..3.
+        float reg0[NT][4] = {};
         if constexpr (DIST && MODE != FWD) {
             const int srcl = j + 16 * ((g >> 1) | ((g & 1) << 1));
 #pragma unroll
-            for (int r = 0; r < 4; ++r) reg0[r] = __shfl((g & 2) ? nr0[4 + r] : nr0[r], srcl);
+            for (int h = 0; h < NT; ++h)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) reg0[h][r] = __shfl((g & 2) ? nr0[h][4 + r] : nr0[h][r], srcl);
         }
         F2H_PHASE(const uint64_t ptc = __builtin_readcyclecounter();)
         __syncthreads();  // halo staged
@@ -578,20 +652,28 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             load_regs(xunit, xh0, xw0);
         };
 
-        // score-type product of block b (16 elements x 16 register pixels)
-        auto score = [&](auto B, const char *pA, h8 rh, h8 rl, f4 init) {
+        // score-type product of block b (16 elements x 16 register pixels),
+        // summed over the sub-pixels
+        auto score = [&](auto B, const char *pA, const h8 (&rh)[NT], const h8 (&rl)[NT], f4 init) {
             constexpr int b = decltype(B)::value;
-            constexpr int aoff = (2 * (b / NKW) + CR * 8 * (b % NKW)) * KS * 2;
-            const h8 x = *reinterpret_cast<const h8 *>(pA + aoff);
-            init = mfmah(x, rh, init);
-            return mfmah(x, rl, init);
+            constexpr int aoff = (2 * (b / NKW) + CR * 8 * (b % NKW)) * SB;
+#pragma unroll
+            for (int h = 0; h < NT; ++h) {
+                const h8 x = *reinterpret_cast<const h8 *>(pA + aoff + 64 * h);
+                init = mfmah(x, rh[h], init);
+                init = mfmah(x, rl[h], init);
+            }
+            return init;
         };
-        // apply-type rows of block b: channel j of elements 4g + t
-        auto trows = [&](auto B, const char *pR, h4 &hi, h4 &lo) {
+        // apply-type rows of block b: channel 16 h + j of elements 4g + t
+        auto trows = [&](auto B, const char *pR, h4 (&hi)[NT], h4 (&lo)[NT]) {
             constexpr int b = decltype(B)::value;
-            constexpr int boff = (2 * (b / NKW) + CR * 8 * (b % NKW)) * KS * 2;
-            hi = ldtr(pR + boff);
-            lo = ldtr(pR + boff + 32);
+            constexpr int boff = (2 * (b / NKW) + CR * 8 * (b % NKW)) * SB;
+#pragma unroll
+            for (int h = 0; h < NT; ++h) {
+                hi[h] = ldtr(pR + boff + 64 * h);
+                lo[h] = ldtr(pR + boff + 64 * h + 32);
+            }
         };
         // per-slot scalars of elements 4g + r of block b
         auto scal = [&](auto B, const float *pS) {
@@ -604,22 +686,26 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
 
         if constexpr (MODE == FWD) {
             float m = 0.f, lsum = 0.f;
-            f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+            f4 acc[NT];
+#pragma unroll
+            for (int h = 0; h < NT; ++h) acc[h] = f4{0.f, 0.f, 0.f, 0.f};
             // LDS operands of a pair: score rows of its two blocks, apply rows
             // (values), and the Distance key biases
             struct POps {
-                h8 a[2];
-                h4 vh[2], vl[2];
+                h8 a[2][NT];
+                h4 vh[2][NT], vl[2][NT];
                 f4 kb[2];
             };
             auto load_a = [&](auto PI, POps &o) {
                 constexpr int pi = decltype(PI)::value;
                 constexpr int b0 = 2 * pi;
                 constexpr int b1 = b0 + 1 < NBLK ? b0 + 1 : b0;
-                constexpr int a0 = (2 * (b0 / NKW) + CR * 8 * (b0 % NKW)) * KS * 2;
-                constexpr int a1 = (2 * (b1 / NKW) + CR * 8 * (b1 % NKW)) * KS * 2;
-                o.a[0] = *reinterpret_cast<const h8 *>(pA0 + a0);
-                o.a[1] = *reinterpret_cast<const h8 *>(pA0 + a1);
+                constexpr int a0 = (2 * (b0 / NKW) + CR * 8 * (b0 % NKW)) * SB;
+                constexpr int a1 = (2 * (b1 / NKW) + CR * 8 * (b1 % NKW)) * SB;
+#pragma unroll
+                for (int h = 0; h < NT; ++h) o.a[0][h] = *reinterpret_cast<const h8 *>(pA0 + a0 + 64 * h);
+#pragma unroll
+                for (int h = 0; h < NT; ++h) o.a[1][h] = *reinterpret_cast<const h8 *>(pA0 + a1 + 64 * h);
                 if constexpr (DIST) {
                     o.kb[0] = scal(std::integral_constant<int, b0>{}, pS0);
                     o.kb[1] = scal(std::integral_constant<int, b1>{}, pS0);
@@ -658,8 +744,11 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                         // the relative score is the maximised value minus m,
                         // rounded as in the pass that took the maximum
                         f4 z = f4{0.f, 0.f, 0.f, 0.f};
-                        z = mfmah(o.a[u], r0h, z);
-                        z = mfmah(o.a[u], r0l, z);
+#pragma unroll
+                        for (int h = 0; h < NT; ++h) {
+                            z = mfmah(o.a[u][h], r0h[h], z);
+                            z = mfmah(o.a[u][h], r0l[h], z);
+                        }
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             x[r] = __builtin_amdgcn_ldexpf(z[r], -eu);
@@ -670,8 +759,12 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                         f4 init = f4{0.f, 0.f, 0.f, 0.f};
                         if constexpr (DIST) init = o.kb[u];
                         if constexpr (rel) init = init - f4{m, m, m, m};
-                        init = mfmah(o.a[u], r0h, init);
-                        x = mfmah(o.a[u], r0l, init);
+#pragma unroll
+                        for (int h = 0; h < NT; ++h) {
+                            init = mfmah(o.a[u][h], r0h[h], init);
+                            init = mfmah(o.a[u][h], r0l[h], init);
+                        }
+                        x = init;
                     }
                     x[0] = mask_sel_d<lane_mask(P, bi, bj, 0)>(x[0], -INFINITY, dep);
                     x[1] = mask_sel_d<lane_mask(P, bi, bj, 1)>(x[1], -INFINITY, dep);
@@ -704,11 +797,14 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 h4 ph0, pl0, ph1, pl1;
                 split4(p[0], ph0, pl0);
                 split4(p[1], ph1, pl1);
-                const h8 vh = cat(o.vh[0], o.vh[1]), vl = cat(o.vl[0], o.vl[1]);
                 const h8 ph = cat(ph0, ph1), pl = cat(pl0, pl1);
-                acc = mfmah(vh, ph, acc);
-                acc = mfmah(vh, pl, acc);
-                acc = mfmah(vl, ph, acc);
+#pragma unroll
+                for (int h = 0; h < NT; ++h) {
+                    const h8 vh = cat(o.vh[0][h], o.vh[1][h]), vl = cat(o.vl[0][h], o.vl[1][h]);
+                    acc[h] = mfmah(vh, ph, acc[h]);
+                    acc[h] = mfmah(vh, pl, acc[h]);
+                    acc[h] = mfmah(vl, ph, acc[h]);
+                }
                 return ps;
             };
             auto scores = [&](auto PI, auto REL, f4 (&sv)[2], int dep, auto SLOW) {
@@ -795,7 +891,8 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 });
                 m = gmax(mx);
                 lsum = 0.f;
-                acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int h = 0; h < NT; ++h) acc[h] = f4{0.f, 0.f, 0.f, 0.f};
                 static_for<0, NPAIR>([&](auto PI) {
                     FWD_FENCE_A();
                     f4 sv[2];
@@ -816,9 +913,11 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             if (rvalid) {
                 float *yb = a.yout + uoff;
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    yb[f2d::comp_off<CPLX, CL>(a, rpix, 4 * g + r)] =
-                        __builtin_amdgcn_ldexpf(acc[r] * inv, -s1);
+                for (int h = 0; h < NT; ++h)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        yb[f2d::comp_off<CPLX, CL>(a, rpix, 16 * h + 4 * g + r)] =
+                            __builtin_amdgcn_ldexpf(acc[h][r] * inv, -s1);
                 if (g == 0)
                     a.lse_out[soff + rpix] =
                         (m + __log2f(l)) * kLn2 - (DIST ? 0.5f * sq * a.scale : 0.f);
@@ -829,8 +928,9 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
             const float nl = -rowL * kLog2e - (DIST ? 0.5f * c2 * sq : 0.f);
             const float nD = -__builtin_amdgcn_ldexpf(rowD, sd + s1);
             const float kb = DIST ? -0.5f * c2 * sq : 0.f;  // BWDKV key bias
-            f4 acc0 = f4{0.f, 0.f, 0.f, 0.f};  // dQ (BWDQ) or dK (BWDKV)
-            f4 acc1 = f4{0.f, 0.f, 0.f, 0.f};  // dV (BWDKV)
+            f4 acc0[NT], acc1[NT];  // dQ (BWDQ) or dK (BWDKV); dV (BWDKV)
+#pragma unroll
+            for (int h = 0; h < NT; ++h) acc0[h] = acc1[h] = f4{0.f, 0.f, 0.f, 0.f};
             float corr = 0.f;
             // SLOW: scores of the per-pixel normalised register operand,
             // unscaled by 2^-eu after the product, the row terms added, and
@@ -887,13 +987,16 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 split4(ds[0], dh0, dl0);
                 split4(ds[1], dh1, dl1);
                 const h8 dsh = cat(dh0, dh1), dsl = cat(dl0, dl1);
-                h4 t0h, t0l, t1h, t1l;
+                h4 t0h[NT], t0l[NT], t1h[NT], t1l[NT];
                 trows(std::integral_constant<int, b0>{}, pR0, t0h, t0l);
                 trows(std::integral_constant<int, b1>{}, pR0, t1h, t1l);
-                const h8 yh = cat(t0h, t1h), yl = cat(t0l, t1l);
-                acc0 = mfmah(yh, dsh, acc0);
-                acc0 = mfmah(yl, dsh, acc0);
-                acc0 = mfmah(yh, dsl, acc0);
+#pragma unroll
+                for (int h = 0; h < NT; ++h) {
+                    const h8 yh = cat(t0h[h], t1h[h]), yl = cat(t0l[h], t1l[h]);
+                    acc0[h] = mfmah(yh, dsh, acc0[h]);
+                    acc0[h] = mfmah(yl, dsh, acc0[h]);
+                    acc0[h] = mfmah(yh, dsl, acc0[h]);
+                }
                 if constexpr (KV) {
                     h4 ph0, pl0, ph1, pl1;
                     split4(p[0], ph0, pl0);
@@ -901,10 +1004,13 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                     const h8 ph = cat(ph0, ph1), pl = cat(pl0, pl1);
                     trows(std::integral_constant<int, b0>{}, pR1, t0h, t0l);
                     trows(std::integral_constant<int, b1>{}, pR1, t1h, t1l);
-                    const h8 zh = cat(t0h, t1h), zl = cat(t0l, t1l);
-                    acc1 = mfmah(zh, ph, acc1);
-                    acc1 = mfmah(zl, ph, acc1);
-                    acc1 = mfmah(zh, pl, acc1);
+#pragma unroll
+                    for (int h = 0; h < NT; ++h) {
+                        const h8 zh = cat(t0h[h], t1h[h]), zl = cat(t0l[h], t1l[h]);
+                        acc1[h] = mfmah(zh, ph, acc1[h]);
+                        acc1[h] = mfmah(zl, ph, acc1[h]);
+                        acc1[h] = mfmah(zh, pl, acc1[h]);
+                    }
                 }
             });
             };
@@ -918,25 +1024,29 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
                 if constexpr (!KV) {
                     float *ob = a.dq + uoff;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        // dS' = 2^(sd + s1) dS, k' = 2^s0 k
-                        float val = __builtin_amdgcn_ldexpf(acc0[r], -(sd + s1 + s0));
-                        if constexpr (DIST) val -= __builtin_amdgcn_ldexpf(cs, -(sd + s1)) * reg0[r];
-                        ob[f2d::comp_off<CPLX, CL>(a, rpix, 4 * g + r)] = val * a.scale;
-                    }
+                    for (int h = 0; h < NT; ++h)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            // dS' = 2^(sd + s1) dS, k' = 2^s0 k
+                            float val = __builtin_amdgcn_ldexpf(acc0[h][r], -(sd + s1 + s0));
+                            if constexpr (DIST) val -= __builtin_amdgcn_ldexpf(cs, -(sd + s1)) * reg0[h][r];
+                            ob[f2d::comp_off<CPLX, CL>(a, rpix, 16 * h + 4 * g + r)] = val * a.scale;
+                        }
                     if (g == 0) a.dbuf[soff + rpix] = rowD;
                 } else {
                     float *vb = a.dv + uoff;
                     float *kbp = a.dk + uoff;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int o = f2d::comp_off<CPLX, CL>(a, rpix, 4 * g + r);
-                        // dy' = 2^s1 dy, dS' = 2^(s2 + s1) dS, q' = 2^s0 q
-                        vb[o] = __builtin_amdgcn_ldexpf(acc1[r], -s1);
-                        float val = __builtin_amdgcn_ldexpf(acc0[r], -(s2 + s1 + s0));
-                        if constexpr (DIST) val -= __builtin_amdgcn_ldexpf(cs, -(s2 + s1)) * reg0[r];
-                        kbp[o] = val * a.scale;
-                    }
+                    for (int h = 0; h < NT; ++h)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int o = f2d::comp_off<CPLX, CL>(a, rpix, 16 * h + 4 * g + r);
+                            // dy' = 2^s1 dy, dS' = 2^(s2 + s1) dS, q' = 2^s0 q
+                            vb[o] = __builtin_amdgcn_ldexpf(acc1[h][r], -s1);
+                            float val = __builtin_amdgcn_ldexpf(acc0[h][r], -(s2 + s1 + s0));
+                            if constexpr (DIST) val -= __builtin_amdgcn_ldexpf(cs, -(s2 + s1)) * reg0[h][r];
+                            kbp[o] = val * a.scale;
+                        }
                 }
             }
         }
@@ -959,12 +1069,12 @@ __global__ __launch_bounds__(1024, 1) void kernel2h(Args a) {
 #endif
 }
 
-template <int P, bool CPLX, bool DIST, int MODE, bool CL>
-hipError_t launch(const Args &a0, int cus, hipStream_t s) {
-    using G = f2d::Geo<P, 1, 2, 8>;
-    constexpr int bytes = LGeo<P, MODE, DIST>::bytes;
+template <int P, int NT, bool CPLX, bool DIST, int MODE, bool CL>
+hipError_t launch2h(const Args &a0, int cus, hipStream_t s) {
+    using G = f2d::Geo<P, 1, grid_wh<NT>(), 8>;
+    constexpr int bytes = LGeo<P, NT, MODE, DIST>::bytes;
     static_assert(bytes <= (int)f2d::kLdsCap, "halo does not fit LDS");
-    auto kern = kernel2h<P, CPLX, DIST, MODE, CL>;
+    auto kern = kernel2h<P, NT, CPLX, DIST, MODE, CL>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -984,18 +1094,20 @@ hipError_t launch(const Args &a0, int cus, hipStream_t s) {
     a.per_xcd = (int)((nitems + 7) / 8);
     int64_t grid = std::min<int64_t>(cus, 8LL * a.per_xcd);
     grid = std::max<int64_t>(8, grid / 8 * 8);
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(1024), bytes, s, a);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(G::THREADS), bytes, s, a);
     return hipGetLastError();
 }
 
-template <int MODE>
+// NT = 1 covers windows 3, 5, 7, 11 and 15; NT = 2 (32 real components per
+// head) windows up to 11, beyond which its halo would not fit LDS
+template <int MODE, int NT>
 hipError_t dispatch(int p, bool cplx, bool dist, const Args &a, int cus, hipStream_t s) {
 #define CIRCATT_F2H_CL(PP, CLL)                                                          \
     {                                                                                    \
-        if (cplx) return dist ? launch<PP, true, true, MODE, CLL>(a, cus, s)             \
-                              : launch<PP, true, false, MODE, CLL>(a, cus, s);           \
-        return dist ? launch<PP, false, true, MODE, CLL>(a, cus, s)                      \
-                    : launch<PP, false, false, MODE, CLL>(a, cus, s);                    \
+        if (cplx) return dist ? launch2h<PP, NT, true, true, MODE, CLL>(a, cus, s)         \
+                              : launch2h<PP, NT, true, false, MODE, CLL>(a, cus, s);       \
+        return dist ? launch2h<PP, NT, false, true, MODE, CLL>(a, cus, s)                  \
+                    : launch2h<PP, NT, false, false, MODE, CLL>(a, cus, s);                \
     }
 #define CIRCATT_F2H_CASE(PP)                                                             \
     if (p == PP) {                                                                       \
@@ -1006,7 +1118,7 @@ hipError_t dispatch(int p, bool cplx, bool dist, const Args &a, int cus, hipStre
     CIRCATT_F2H_CASE(2)
     CIRCATT_F2H_CASE(3)
     CIRCATT_F2H_CASE(5)
-    CIRCATT_F2H_CASE(7)
+    if constexpr (NT == 1) CIRCATT_F2H_CASE(7)
 #undef CIRCATT_F2H_CASE
 #undef CIRCATT_F2H_CL
     return hipErrorNotSupported;
@@ -1014,8 +1126,12 @@ hipError_t dispatch(int p, bool cplx, bool dist, const Args &a, int cus, hipStre
 
 }  // namespace f2h
 
+// 16 real components per head (fused2h_*.hip) and 32 (fused2h2_*.hip)
 hipError_t launch_f2h_fwd(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
 hipError_t launch_f2h_bwdq(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
 hipError_t launch_f2h_bwdkv(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
+hipError_t launch_f2h2_fwd(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
+hipError_t launch_f2h2_bwdq(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
+hipError_t launch_f2h2_bwdkv(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
 
 }  // namespace circatt

@@ -48,7 +48,7 @@
 #include "circatt_common.h"
 #include "circatt_kernels.h"
 
-extern __shared__ float circatt_lds[];
+extern __shared__ __attribute__((aligned(16))) float circatt_lds[];
 
 namespace circatt {
 

@@ -73,6 +73,9 @@ def fused(ca, cuda, kind, q, k, v, dy, ws, nh):
 # split-half kernels, partial tiles and halos that wrap
 CASES = [((40, 24), 15, 64, 1, 4), ((20, 18), 11, 16, 2, 1), ((17, 13), 7, 32, 1, 2),
          ((12, 10), 5, 16, 2, 1), ((9, 11), 3, 16, 1, 1)]
+# 32 real components per head (the 8x16-tile kernels), every window they cover
+CASES32 = [((20, 18), 11, 32, 2, 1), ((17, 13), 7, 64, 1, 2), ((12, 10), 5, 32, 1, 1),
+           ((9, 11), 3, 64, 1, 2)]
 MAGS = [1e-7, 1e-5, 1e-3, 1e2, 1e4]
 
 
@@ -82,11 +85,24 @@ MAGS = [1e-7, 1e-5, 1e-3, 1e2, 1e4]
 @pytest.mark.parametrize("cplx", [False, True])
 @pytest.mark.parametrize("kind", [0, 1])
 def test_fused_across_magnitudes(ca, cuda, case, which, mag, cplx, kind):
+    _across_magnitudes(ca, cuda, case, which, mag, cplx, kind, 0)
+
+
+@pytest.mark.parametrize("case", CASES32, ids=lambda c: f"{c[0]}-ws{c[1]}")
+@pytest.mark.parametrize("which", ["v_dy", "q_k", "all"])
+@pytest.mark.parametrize("mag", MAGS)
+@pytest.mark.parametrize("cplx", [False, True])
+@pytest.mark.parametrize("kind", [0, 1])
+def test_fused_across_magnitudes_32(ca, cuda, case, which, mag, cplx, kind):
+    _across_magnitudes(ca, cuda, case, which, mag, cplx, kind, 50)
+
+
+def _across_magnitudes(ca, cuda, case, which, mag, cplx, kind, seed0):
     dims, ws, C, B, nh = case
     if cplx:
-        C //= 2  # 16 real components per head either way
+        C //= 2  # the same real components per head either way
     shape = (B, C, *reversed(dims))
-    seed = 3000 + 17 * ws + int(math.log10(mag)) + 7 * kind + (100 if cplx else 0)
+    seed = 3000 + seed0 + 17 * ws + int(math.log10(mag)) + 7 * kind + (100 if cplx else 0)
     q, k, v, dy = (seeded(seed + i, shape, cplx) for i in range(4))
     sv = mag if which in ("v_dy", "all") else 1.0
     sq = mag if which in ("q_k", "all") else 1.0
@@ -132,11 +148,12 @@ def test_fused_at_the_reference_loss_scale(ca, cuda, kind):
         assert rel_err(g, r) < TOL_GRAD, (name, rel_err(g, r))
 
 
-def central_gap(kind, q, k, ws, nh, tile=16):
+def central_gap(kind, q, k, ws, nh, tile_h=16, tile_w=16):
     """Largest (over queries) of max_window(s) - max_central(s) in log2 units,
     where the central keys are the two halo rows the split-half forward takes
     its reference maximum from (tile rows 8 wh + 8 - P, 8 wh + 9 - P of the
-    query's wavefront, halo columns 2 ww .. 2 ww + 15)."""
+    query's wavefront, halo columns 2 ww .. 2 ww + 15), on tiles of
+    tile_h x tile_w pixels (16 x 16, or 8 x 16 for 32 real components)."""
     dims = O.spatial_dims(q)
     n1, n2 = dims
     P = (ws - 1) // 2
@@ -149,7 +166,7 @@ def central_gap(kind, q, k, ws, nh, tile=16):
     best = -np.inf
     for r in range(n1 * n2):
         h, w = r % n1, r // n1
-        th, tw = h % tile, w % tile
+        th, tw = h % tile_h, w % tile_w
         wh, ww = th // 8, tw // 2
         rows = {(h - th + 8 * wh + 8 - P + d) % n1 for d in (0, 1)}
         cset = {(w - tw + 2 * ww - P + d) % n2 for d in range(16)}
@@ -172,6 +189,23 @@ def test_fused_forward_redo_path(ca, cuda, ws, kind):
     q, k, v, dy = (seeded(3600 + i + ws + 5 * kind, shape) for i in range(4))
     q, k = q * np.float32(2.5), k * np.float32(2.5)
     assert central_gap(kind, q, k, ws, nh) > 8.5
+    y, dq, dk, dv = fused(ca, cuda, kind, q, k, v, dy, ws, nh)
+    yr, _ = O.attention_fwd(kind, *(f64(a) for a in (q, k, v)), ws, nh)
+    gr = O.attention_bwd(kind, *(f64(a) for a in (q, k, v, dy)), ws, nh)
+    assert rel_err(y, yr) < TOL_FWD
+    for name, g, r in zip(("dq", "dk", "dv"), (dq, dk, dv), gr):
+        assert rel_err(g, r) < TOL_GRAD, (name, rel_err(g, r))
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_fused_forward_redo_path_32(ca, cuda, kind):
+    """The redo path of the forward for 32 real components per head (8x16
+    tiles, window 11), q and k scaled by 2.5 as above."""
+    dims, C, B, nh, ws = (40, 24), 64, 1, 2, 11
+    shape = (B, C, *reversed(dims))
+    q, k, v, dy = (seeded(3700 + i + 5 * kind, shape) for i in range(4))
+    q, k = q * np.float32(2.5), k * np.float32(2.5)
+    assert central_gap(kind, q, k, ws, nh, tile_h=8) > 8.5
     y, dq, dk, dv = fused(ca, cuda, kind, q, k, v, dy, ws, nh)
     yr, _ = O.attention_fwd(kind, *(f64(a) for a in (q, k, v)), ws, nh)
     gr = O.attention_bwd(kind, *(f64(a) for a in (q, k, v, dy)), ws, nh)
