@@ -1,4 +1,4 @@
-"""Per-wave phase timing of the split-half fused kernels at cfg3.
+"""Per-wave phase timing of the split-half fused kernels at cfg3 (or cfg5).
 
 A copy of libcircatt built with CIRCATT_F2H_PHASE=1 makes every wave of
 kernel2h sum s_memtime spans of four phases over its items (staging, the two
@@ -12,7 +12,8 @@ the phases per wave slot.
     python circulantattention.jl_amd/microbench/phase_timing.py [--no-prio]
 
 --no-prio builds and runs a second copy with CIRCATT_F2H_PRIO=0 (equal wave
-priorities over the walk).
+priorities over the walk).  --config cfg5 does the same for the kernels of 32
+real components per head (8 wavefronts per workgroup) at cfg5's shape.
 """
 from __future__ import annotations
 
@@ -24,11 +25,17 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
-F2H = ("fused2h_fwd.hip", "fused2h_bwdq.hip", "fused2h_bwdkv.hip")
+F2H16 = ("fused2h_fwd.hip", "fused2h_bwdq.hip", "fused2h_bwdkv.hip")
+F2H32 = ("fused2h2_fwd.hip", "fused2h2_bwdq.hip", "fused2h2_bwdkv.hip")
+# name: (spatial n1, n2, channels, batch, heads, window, complex, sources, waves per workgroup)
+CONFIGS = {"cfg3": (256, 256, 64, 4, 4, 15, False, F2H16, 16),
+           "cfg5": (320, 320, 32, 2, 2, 11, True, F2H32, 8)}
+F2H = F2H16
 
 
 def lib_path(no_prio: bool) -> str:
-    return os.path.join(HERE, "libcircatt_phase_noprio.so" if no_prio else "libcircatt_phase.so")
+    tag = "" if F2H is F2H16 else "32"
+    return os.path.join(HERE, f"libcircatt_phase{tag}_noprio.so" if no_prio else f"libcircatt_phase{tag}.so")
 
 
 def build(no_prio: bool) -> None:
@@ -64,15 +71,15 @@ def run(no_prio: bool) -> None:
     for name, (res, args) in L.SIGNATURES.items():
         f = getattr(lib, name)
         f.restype, f.argtypes = res, args
-    n1 = n2 = 256
-    C, B, nh, ws = 64, 4, 4, 15
+    n1, n2, C, B, nh, ws, cplx, _, nw = CONFIGS[CFG]
     P = n1 * n2
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(1003)
     shape = (B, C, n2, n1)
-    q, k, v, dy = (torch.randn(shape, device=dev, generator=g) for _ in range(4))
-    N, EX = q.numel(), 8 * 16 * 4
+    dt, DT = (torch.complex64, L.C32) if cplx else (torch.float32, L.F32)
+    q, k, v, dy = (torch.randn(shape, device=dev, generator=g, dtype=dt) for _ in range(4))
+    N, EX = q.numel() * (2 if cplx else 1), 8 * 16 * 4
     yb, dqb, dkb = (torch.zeros(N + EX, device=dev) for _ in range(3))
     dv = torch.empty_like(q)
     lse = torch.empty((B * nh, P), device=dev)
@@ -81,15 +88,15 @@ def run(no_prio: bool) -> None:
     s = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
     def fwd():
-        L.check(lib.circatt_fused_fwd(0, L.F32, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k), ptr(v),
+        L.check(lib.circatt_fused_fwd(0, DT, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k), ptr(v),
                                       ptr(yb), ptr(lse), s))
 
     def bwd_dq():
-        L.check(lib.circatt_fused_bwd_dq(0, L.F32, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k), ptr(v),
+        L.check(lib.circatt_fused_bwd_dq(0, DT, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k), ptr(v),
                                          ptr(yb), ptr(dy), ptr(lse), ptr(dqb), ptr(work), wb, s))
 
     def bwd_dkdv():
-        L.check(lib.circatt_fused_bwd_dkdv(0, L.F32, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
+        L.check(lib.circatt_fused_bwd_dkdv(0, DT, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
                                            ptr(v), ptr(dy), ptr(lse), ptr(dkb), ptr(dv), ptr(work),
                                            wb, s))
 
@@ -98,7 +105,7 @@ def run(no_prio: bool) -> None:
         bwd_dq()
         bwd_dkdv()
     torch.cuda.synchronize()
-    print("cfg3, cycles summed over each wave's items (mean over the 8 sampled workgroups)"
+    print(f"{CFG}, cycles summed over each wave's items (mean over the 8 sampled workgroups)"
           + (", equal wave priorities" if no_prio else ""))
     for name, f, buf in (("forward", fwd, yb), ("query-centric", bwd_dq, dqb),
                          ("key-centric", bwd_dkdv, dkb)):
@@ -109,14 +116,14 @@ def run(no_prio: bool) -> None:
         f()
         e1.record()
         torch.cuda.synchronize()
-        t = buf[N:].view(torch.int32).cpu().numpy().reshape(8, 16, 4).astype("int64")
+        t = buf[N:].view(torch.int32).cpu().numpy().reshape(8, 16, 4)[:, :nw].astype("int64")
         tot = t.sum(axis=2)
         m = t.mean(axis=(0, 1))
         print(f"{name}: kernel {e0.elapsed_time(e1) * 1e3:.1f} us, "
               f"{tot.max() / (e0.elapsed_time(e1) * 1e-3) / 1e9:.2f} GHz (cycles / time)")
         print("  phases (mean over waves): staging %.0f, barrier after maxima %.0f, "
               "barrier after staging %.0f, walk+epilogue %.0f" % tuple(m))
-        print("  walk+epilogue per wave slot 0..15 (mean over workgroups):",
+        print(f"  walk+epilogue per wave slot 0..{nw - 1} (mean over workgroups):",
               [int(x) for x in t[:, :, 3].mean(axis=0)])
 
 
@@ -124,5 +131,8 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--build", action="store_true")
     ap.add_argument("--no-prio", action="store_true")
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="cfg3")
     args = ap.parse_args()
+    CFG = args.config
+    F2H = CONFIGS[CFG][7]
     build(args.no_prio) if args.build else run(args.no_prio)
