@@ -5,9 +5,9 @@ arithmetic is the planar path's, element for element, so y, lse, dq, dk, dv
 must equal the planar results bit for bit after the layout permutation.  The
 planar path itself is pinned against the oracle in test_gpu_parity.py and
 test_gpu_magnitudes.py.  Cases cover every fused kernel family: split-half
-(2D, 16 real components per head), Float32 matrix cores (2D, 32 components,
-or CIRCATT_MATH_F32), and the run-time-window kernels (1D, 2D windows past 15,
-64 components).
+(2D, 16 real components per head on 16x16 tiles, 32 on 8x16 tiles), Float32
+matrix cores (2D, 32 components at ws 15, or CIRCATT_MATH_F32), and the
+run-time-window kernels (1D, 2D windows past 15, 64 components).
 """
 import ctypes
 
@@ -22,8 +22,11 @@ CASES = [
     ((24, 20), 32, 2, 2, 15, 1, False, "split"),    # split-half, Distance, streamed forward
     ((16, 18), 16, 2, 1, 5, 0, True, "split"),      # split-half, ComplexF32
     ((24, 20), 32, 2, 2, 11, 0, False, "f32"),      # Float32 matrix cores, 16 components
-    ((20, 16), 64, 2, 2, 7, 1, False, "split"),     # Float32 matrix cores, 32 components
-    ((20, 16), 32, 2, 1, 3, 0, True, "split"),      # Float32 matrix cores, ComplexF32 32 components
+    ((20, 16), 64, 2, 2, 7, 1, False, "split"),     # split-half, 32 components (8x16 tiles)
+    ((20, 16), 32, 2, 1, 3, 0, True, "split"),      # split-half, ComplexF32 32 components
+    ((28, 20), 32, 2, 2, 11, 1, True, "split"),     # split-half, ComplexF32 32 components, streamed forward
+    ((20, 16), 64, 2, 2, 15, 0, False, "split"),    # Float32 matrix cores, 32 components at ws 15
+    ((20, 16), 64, 2, 2, 7, 1, False, "f32"),       # Float32 matrix cores, 32 components
     ((150,), 32, 1, 2, 9, 0, False, "split"),       # run-time window, 1D
     ((40, 36), 16, 1, 1, 19, 1, False, "split"),    # run-time window, 2D ws 19
     ((18, 14), 128, 2, 1, 5, 0, False, "split"),    # run-time window, 64 components
