@@ -257,6 +257,12 @@ ATT_CASES = [
     ((8, 8), 15, 32, 1, 2, 110),
     ((17, 26), 11, 64, 1, 4, 111),
     ((24, 16), 7, 32, 2, 1, 112),
+    # 32 real components per head (real C / nheads = 32, complex C / nheads = 16) on the
+    # split-half 8x16 tiles: partial tiles, halos that wrap more than once, ws > N
+    ((9, 7), 5, 32, 2, 1, 113),
+    ((5, 13), 11, 64, 1, 2, 114),
+    ((13, 21), 11, 16, 1, 1, 115),
+    ((30, 17), 3, 32, 1, 1, 116),
 ]
 
 
