@@ -68,7 +68,8 @@ int circatt_version(void);
  *     f16 halves and a product is taken as hi*hi + lo*hi + hi*lo on the f16
  *     matrix cores with Float32 accumulation (relative error near 2^-21 per
  *     operand, the order of Float32 rounding).  Operands are scaled by powers
- *     of two per work item (16x16 pixels of one head) before the split, so
+ *     of two per work item (a 16x16 tile of one head, 8x16 for heads of 32
+ *     real components) before the split, so
  *     the halves keep Float32's range: inputs of any magnitude (1e-7 and 1e4
  *     are tested) give Float32-class results.  Where q.k scores are so large
  *     that the halves could overflow, a slower exact-scale walk takes over.
