@@ -82,7 +82,6 @@ using f2d::gmax;
 using f2d::gsum;
 using f2d::kLn2;
 using f2d::kLog2e;
-using f2d::lane_mask;
 using f2d::mask_sel;
 using f2d::mask_sel_d;
 using f2d::static_for;
@@ -248,9 +247,66 @@ __device__ __forceinline__ void reg_split(const float (&x)[8], float sc, h8 &hi,
 
 enum { FWD = f2d::FWD, BWDQ = f2d::BWDQ, BWDKV = f2d::BWDKV };
 
+// Tile and block geometry.  A wavefront holds an 8x2 block of register
+// pixels (queries in the forward) and walks LDS blocks of 16 pixels covering
+// their (8 + 2P) x (2 + 2P) window region: 2x8 blocks, or for 32 real
+// components at windows 3 and 11 4x4 blocks, which cover that region with
+// fewer pixels (ws 11: 15 blocks, 240 pixels, against 18 blocks, 288).
+// Element 4 g + r of a block (the score accumulator's row) sits at block row
+// r % 2, column 2 g + r / 2 (2x8), or at row r, column g (4x4).  LDS slots
+// are column-major with CR slots per column: CR = 2 mod 4 for 2x8 blocks and
+// CR = 4 mod 16 for 4x4 blocks, which keeps the 16-byte reads of a block's
+// rows (slot stride 144 bytes) free of bank conflicts.  4x4 blocks reach
+// BR * NKH - (8 + 2P) rows past the staged ones, into the pad rows of the
+// column; those rows, and staged-region columns past the last staged one,
+// hold zeros written once per launch and are read only under the mask.
+template <int P, int NT>
+struct HGeo {
+    static constexpr int WH = grid_wh<NT>(), WW = 8;
+    static constexpr int THREADS = 64 * WH * WW;
+    static constexpr int TH = 8 * WH, TW = 2 * WW;
+    static constexpr int BR = (NT == 2 && (P == 1 || P == 5)) ? 4 : 2;  // block rows
+    static constexpr int BC = 16 / BR;                                   // block columns
+    static constexpr int NKH = (8 + 2 * P + BR - 1) / BR;
+    static constexpr int NKW = (2 + 2 * P + BC - 1) / BC;
+    static constexpr int NBLK = NKH * NKW;
+    static constexpr int HH = TH + 2 * P;
+    static constexpr int HWD = 2 * (WW - 1) + BC * NKW;
+    static constexpr int CR = BR == 2 ? HH + ((2 - HH % 4) + 4) % 4     // LDS column stride
+                                      : HH + ((4 - HH % 16) + 16) % 16;
+    static constexpr int LPX = CR * HWD;                    // LDS pixel slots per tensor
+    // slot offset of block b within a wavefront's region
+    static constexpr int bslot(int b) { return BR * (b / NKW) + CR * BC * (b % NKW); }
+    // central pair of the streamed forward: two blocks of the block row that
+    // holds key rows 8, 9 (in every query's window when 2P >= 9)
+    static constexpr int PCENT = (8 / BR) * NKW / 2;
+    static_assert(8 * (WH - 1) + BR * NKH <= CR, "a wavefront's blocks stay within their column's slots");
+    static_assert((8 / BR) * NKW % 2 == 0, "the central pair lies in one block row");
+};
+static_assert(HGeo<5, 2>::LPX == 520 && HGeo<5, 2>::NBLK == 15, "4x4 blocks at ws 11");
+static_assert(HGeo<7, 1>::LPX == f2d::Geo<7, 1, 2, 8>::LPX && HGeo<7, 1>::NBLK == f2d::Geo<7, 1, 2, 8>::NBLK,
+              "2x8 geometry as the Float32 kernels'");
+
+// lane j + 16 g holds query (j % 8, j / 8) and key element 4 g + r of block
+// (bi, bj); bit set where the key lies in the query's window
+template <int BR>
+__host__ __device__ constexpr uint64_t hmask(int P, int bi, int bj, int r) {
+    uint64_t m = 0;
+    for (int lane = 0; lane < 64; ++lane) {
+        const int j = lane & 15, g = lane >> 4;
+        const int kr = BR == 2 ? 2 * bi + (r & 1) : 4 * bi + r;
+        const int kc = BR == 2 ? 8 * bj + 2 * g + (r >> 1) : 4 * bj + g;
+        const int u1 = kr - (j & 7), u2 = kc - (j >> 3);
+        if (u1 >= 0 && u1 <= 2 * P && u2 >= 0 && u2 <= 2 * P) m |= 1ull << lane;
+    }
+    return m;
+}
+static_assert(hmask<2>(7, 3, 1, 2) == f2d::lane_mask(7, 3, 1, 2) && hmask<2>(5, 0, 0, 1) == f2d::lane_mask(5, 0, 0, 1),
+              "2x8 masks as the Float32 kernels'");
+
 template <int P, int NT, int MODE, bool DIST>
 struct LGeo {
-    using G = f2d::Geo<P, 1, grid_wh<NT>(), 8>;
+    using G = HGeo<P, NT>;
     static constexpr int SB = slot_bytes<NT>();
     static constexpr int OT0 = 0;                  // tensor 0 slots (K, or Q in BWDKV)
     static constexpr int OT1 = G::LPX * SB;        // tensor 1 slots (V, or dY in BWDKV)
@@ -266,8 +322,9 @@ struct LGeo {
 template <int P, int NT, bool CPLX, bool DIST, int MODE, bool CL>
 __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
     constexpr int WH = grid_wh<NT>();
-    using G = f2d::Geo<P, 1, WH, 8>;
+    using G = HGeo<P, NT>;
     using L = LGeo<P, NT, MODE, DIST>;
+    constexpr int BR = G::BR;
     constexpr int SB = L::SB;
     constexpr int CR = G::CR, HH = G::HH, HWD = G::HWD, NKW = G::NKW, NBLK = G::NBLK;
     // staged columns: all HWD slot columns on the 16x16 tile; on the 8x16
@@ -299,7 +356,7 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
 #endif
     // forward with a reference maximum from the central block row (rows 8, 9
     // of the key region lie in every query's window when 2P >= 9)
-    constexpr bool STREAM = MODE == FWD && NKW == 2 && P >= 5;
+    constexpr bool STREAM = MODE == FWD && P >= 5 && (BR == 4 || NKW == 2);
     constexpr int PFP = STREAM                    ? 0
                         : (MODE == FWD && NCH == 2) ? CHP - 1
                         : MODE == BWDQ              ? NPAIR / CIRCATT_F2H_BWDQ_PFD
@@ -320,15 +377,16 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         return v;
     };
     // score-type rows: element j of a block, halves 8 g .. 8 g + 7 of its slot
-    const int slotA = 8 * wh + (j & 1) + CR * (2 * ww + (j >> 1));
+    const int slotA = BR == 2 ? 8 * wh + (j & 1) + CR * (2 * ww + (j >> 1))
+                              : 8 * wh + (j & 3) + CR * (2 * ww + (j >> 2));
     const char *const pA0 = lds + opaque(L::OT0 + slotA * SB + 16 * g);
     const char *const pA1 = lds + opaque(L::OT1 + slotA * SB + 16 * g);
     // apply-type rows from slots by transposing reads: lane (j, g) receives
     // channel j (hi; lo 16 halves further) of elements 4g + t, t = 0..3, so
     // lane j of group g addresses channels 4 (j & 3) .. + 3 of element
     // 4g + (j >> 2), which sits at row (j >> 2) & 1, column 2g + (j >> 3)
-    const int slotE = 8 * wh + CR * (2 * ww + 2 * g);
-    const int slotT = slotE + ((j >> 2) & 1) + CR * (j >> 3);
+    const int slotE = 8 * wh + CR * (2 * ww + (BR == 2 ? 2 * g : g));
+    const int slotT = BR == 2 ? slotE + ((j >> 2) & 1) + CR * (j >> 3) : slotE + (j >> 2);
     const char *const pR0 = lds + opaque(L::OT0 + slotT * SB + 8 * (j & 3));
     const char *const pR1 = lds + opaque(L::OT1 + slotT * SB + 8 * (j & 3));
     // per-slot Float32 scalars of elements 4g .. 4g+3
@@ -437,17 +495,18 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
     F2H_PHASE(uint64_t phase[4] = {0, 0, 0, 0};)
     unsigned *const xwords = reinterpret_cast<unsigned *>(lds + L::OX);
     if (threadIdx.x < 4) xwords[threadIdx.x] = 0u;
-    if constexpr (SWC < HWD) {
-        // slot columns past the staged ones: zero halves and scalars, so that
-        // the masked products over them stay finite
-        constexpr int Z0 = CR * SWC, ZN = CR * (HWD - SWC);
-        for (int i = threadIdx.x; i < ZN; i += G::THREADS) {
-            f4 *const z0 = reinterpret_cast<f4 *>(lds + L::OT0 + (Z0 + i) * SB);
-            f4 *const z1 = reinterpret_cast<f4 *>(lds + L::OT1 + (Z0 + i) * SB);
+    if constexpr (NT == 2) {
+        // slots never staged (pad rows, columns past the staged ones): zero
+        // halves and scalars, so that the masked products over them stay
+        // finite
+        for (int i = threadIdx.x; i < G::LPX; i += G::THREADS) {
+            if (i % CR < HH && i / CR < SWC) continue;
+            f4 *const z0 = reinterpret_cast<f4 *>(lds + L::OT0 + i * SB);
+            f4 *const z1 = reinterpret_cast<f4 *>(lds + L::OT1 + i * SB);
 #pragma unroll
             for (int q = 0; q < SB / 16; ++q) z0[q] = z1[q] = f4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (L::NSCAL >= 1) reinterpret_cast<float *>(lds + L::OS0)[Z0 + i] = 0.f;
-            if constexpr (L::NSCAL >= 2) reinterpret_cast<float *>(lds + L::OS1)[Z0 + i] = 0.f;
+            if constexpr (L::NSCAL >= 1) reinterpret_cast<float *>(lds + L::OS0)[i] = 0.f;
+            if constexpr (L::NSCAL >= 2) reinterpret_cast<float *>(lds + L::OS1)[i] = 0.f;
         }
     }
     int unit, h0, w0;
@@ -656,7 +715,7 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         // summed over the sub-pixels
         auto score = [&](auto B, const char *pA, const h8 (&rh)[NT], const h8 (&rl)[NT], f4 init) {
             constexpr int b = decltype(B)::value;
-            constexpr int aoff = (2 * (b / NKW) + CR * 8 * (b % NKW)) * SB;
+            constexpr int aoff = G::bslot(b) * SB;
 #pragma unroll
             for (int h = 0; h < NT; ++h) {
                 const h8 x = *reinterpret_cast<const h8 *>(pA + aoff + 64 * h);
@@ -668,7 +727,7 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         // apply-type rows of block b: channel 16 h + j of elements 4g + t
         auto trows = [&](auto B, const char *pR, h4 (&hi)[NT], h4 (&lo)[NT]) {
             constexpr int b = decltype(B)::value;
-            constexpr int boff = (2 * (b / NKW) + CR * 8 * (b % NKW)) * SB;
+            constexpr int boff = G::bslot(b) * SB;
 #pragma unroll
             for (int h = 0; h < NT; ++h) {
                 hi[h] = ldtr(pR + boff + 64 * h);
@@ -678,9 +737,9 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         // per-slot scalars of elements 4g + r of block b
         auto scal = [&](auto B, const float *pS) {
             constexpr int b = decltype(B)::value;
-            constexpr int boff = 2 * (b / NKW) + CR * 8 * (b % NKW);
+            constexpr int boff = G::bslot(b);
             const f2 lo = *reinterpret_cast<const f2 *>(pS + boff);
-            const f2 hi = *reinterpret_cast<const f2 *>(pS + boff + CR);
+            const f2 hi = *reinterpret_cast<const f2 *>(pS + boff + (BR == 2 ? CR : 2));
             return f4{lo[0], lo[1], hi[0], hi[1]};
         };
 
@@ -700,8 +759,8 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
                 constexpr int pi = decltype(PI)::value;
                 constexpr int b0 = 2 * pi;
                 constexpr int b1 = b0 + 1 < NBLK ? b0 + 1 : b0;
-                constexpr int a0 = (2 * (b0 / NKW) + CR * 8 * (b0 % NKW)) * SB;
-                constexpr int a1 = (2 * (b1 / NKW) + CR * 8 * (b1 % NKW)) * SB;
+                constexpr int a0 = G::bslot(b0) * SB;
+                constexpr int a1 = G::bslot(b1) * SB;
 #pragma unroll
                 for (int h = 0; h < NT; ++h) o.a[0][h] = *reinterpret_cast<const h8 *>(pA0 + a0 + 64 * h);
 #pragma unroll
@@ -766,10 +825,10 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
                         }
                         x = init;
                     }
-                    x[0] = mask_sel_d<lane_mask(P, bi, bj, 0)>(x[0], -INFINITY, dep);
-                    x[1] = mask_sel_d<lane_mask(P, bi, bj, 1)>(x[1], -INFINITY, dep);
-                    x[2] = mask_sel_d<lane_mask(P, bi, bj, 2)>(x[2], -INFINITY, dep);
-                    x[3] = mask_sel_d<lane_mask(P, bi, bj, 3)>(x[3], -INFINITY, dep);
+                    x[0] = mask_sel_d<hmask<BR>(P, bi, bj, 0)>(x[0], -INFINITY, dep);
+                    x[1] = mask_sel_d<hmask<BR>(P, bi, bj, 1)>(x[1], -INFINITY, dep);
+                    x[2] = mask_sel_d<hmask<BR>(P, bi, bj, 2)>(x[2], -INFINITY, dep);
+                    x[3] = mask_sel_d<hmask<BR>(P, bi, bj, 3)>(x[3], -INFINITY, dep);
                     sv[u] = x;
                 };
                 sc(std::integral_constant<int, b0>{}, 0);
@@ -819,7 +878,7 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
             // more than 8 above m, in log2 units, where the halves could
             // overflow), the item is redone with m the exact row maximum from
             // a scores-only pass.  On typical data the redo never runs.
-            constexpr int PC = STREAM ? 4 : 0;
+            constexpr int PC = STREAM ? G::PCENT : 0;
             uint64_t over = 1;
             // streamed configurations issue the next item's loads before the
             // walk, on both of its paths alike (loads issued inside each path
@@ -968,10 +1027,10 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
                         s = score(B, pA0, r0h, r0l, s);
                     }
                     dp = score(B, pA1, r1h, r1l, dp);
-                    p[u][0] = mask_sel_d<lane_mask(P, bi, bj, 0)>(__builtin_amdgcn_exp2f(s[0]), 0.f, k);
-                    p[u][1] = mask_sel_d<lane_mask(P, bi, bj, 1)>(__builtin_amdgcn_exp2f(s[1]), 0.f, k);
-                    p[u][2] = mask_sel_d<lane_mask(P, bi, bj, 2)>(__builtin_amdgcn_exp2f(s[2]), 0.f, k);
-                    p[u][3] = mask_sel_d<lane_mask(P, bi, bj, 3)>(__builtin_amdgcn_exp2f(s[3]), 0.f, k);
+                    p[u][0] = mask_sel_d<hmask<BR>(P, bi, bj, 0)>(__builtin_amdgcn_exp2f(s[0]), 0.f, k);
+                    p[u][1] = mask_sel_d<hmask<BR>(P, bi, bj, 1)>(__builtin_amdgcn_exp2f(s[1]), 0.f, k);
+                    p[u][2] = mask_sel_d<hmask<BR>(P, bi, bj, 2)>(__builtin_amdgcn_exp2f(s[2]), 0.f, k);
+                    p[u][3] = mask_sel_d<hmask<BR>(P, bi, bj, 3)>(__builtin_amdgcn_exp2f(s[3]), 0.f, k);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) ds[u][r] = p[u][r] * dp[r];
                     if constexpr (DIST) corr += (ds[u][0] + ds[u][1]) + (ds[u][2] + ds[u][3]);

@@ -148,12 +148,13 @@ def test_fused_at_the_reference_loss_scale(ca, cuda, kind):
         assert rel_err(g, r) < TOL_GRAD, (name, rel_err(g, r))
 
 
-def central_gap(kind, q, k, ws, nh, tile_h=16, tile_w=16):
+def central_gap(kind, q, k, ws, nh, tile_h=16, tile_w=16, crows=2, ccols=16):
     """Largest (over queries) of max_window(s) - max_central(s) in log2 units,
-    where the central keys are the two halo rows the split-half forward takes
-    its reference maximum from (tile rows 8 wh + 8 - P, 8 wh + 9 - P of the
-    query's wavefront, halo columns 2 ww .. 2 ww + 15), on tiles of
-    tile_h x tile_w pixels (16 x 16, or 8 x 16 for 32 real components)."""
+    where the central keys are the block pair the split-half forward takes its
+    reference maximum from: crows halo rows from tile row 8 wh + 8 - P of the
+    query's wavefront and ccols halo columns from 2 ww - P (2 x 16 for 2x8 LDS
+    blocks; 4 x 8 for the 4x4 blocks of 32 real components at ws 11), on tiles
+    of tile_h x tile_w pixels (16 x 16, or 8 x 16 for 32 real components)."""
     dims = O.spatial_dims(q)
     n1, n2 = dims
     P = (ws - 1) // 2
@@ -168,8 +169,8 @@ def central_gap(kind, q, k, ws, nh, tile_h=16, tile_w=16):
         h, w = r % n1, r // n1
         th, tw = h % tile_h, w % tile_w
         wh, ww = th // 8, tw // 2
-        rows = {(h - th + 8 * wh + 8 - P + d) % n1 for d in (0, 1)}
-        cset = {(w - tw + 2 * ww - P + d) % n2 for d in range(16)}
+        rows = {(h - th + 8 * wh + 8 - P + d) % n1 for d in range(crows)}
+        cset = {(w - tw + 2 * ww - P + d) % n2 for d in range(ccols)}
         central = np.array([(c % n1) in rows and (c // n1) in cset for c in cols[r]])
         gap = S[:, r, :].max(axis=1) - np.where(central, S[:, r, :], -np.inf).max(axis=1)
         best = max(best, float(gap.max()))
@@ -200,12 +201,12 @@ def test_fused_forward_redo_path(ca, cuda, ws, kind):
 @pytest.mark.parametrize("kind", [0, 1])
 def test_fused_forward_redo_path_32(ca, cuda, kind):
     """The redo path of the forward for 32 real components per head (8x16
-    tiles, window 11), q and k scaled by 2.5 as above."""
+    tiles, 4x4 LDS blocks, window 11), q and k scaled by 2.5 as above."""
     dims, C, B, nh, ws = (40, 24), 64, 1, 2, 11
     shape = (B, C, *reversed(dims))
     q, k, v, dy = (seeded(3700 + i + 5 * kind, shape) for i in range(4))
     q, k = q * np.float32(2.5), k * np.float32(2.5)
-    assert central_gap(kind, q, k, ws, nh, tile_h=8) > 8.5
+    assert central_gap(kind, q, k, ws, nh, tile_h=8, crows=4, ccols=8) > 8.5
     y, dq, dk, dv = fused(ca, cuda, kind, q, k, v, dy, ws, nh)
     yr, _ = O.attention_fwd(kind, *(f64(a) for a in (q, k, v)), ws, nh)
     gr = O.attention_bwd(kind, *(f64(a) for a in (q, k, v, dy)), ws, nh)
