@@ -906,7 +906,6 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
                 over = 0;
                 static_for<0, NPAIR>([&](auto I) {
                     constexpr int i = decltype(I)::value;
-                    constexpr int pi = ord(i);
                     FWD_FENCE_A();
                     walk_prio<i, NPAIR>();
                     POps na, nv;
@@ -939,7 +938,6 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
             // exact row maximum, then one walk with every score <= m (the slow
             // walk always takes this form)
             auto twopass = [&](auto SLOW) {
-                constexpr bool slw = decltype(SLOW)::value;
                 float mx = -INFINITY;
                 static_for<0, NPAIR>([&](auto PI) {
                     FWD_FENCE_A();
