@@ -249,9 +249,9 @@ enum { FWD = f2d::FWD, BWDQ = f2d::BWDQ, BWDKV = f2d::BWDKV };
 
 // Tile and block geometry.  A wavefront holds an 8x2 block of register
 // pixels (queries in the forward) and walks LDS blocks of 16 pixels covering
-// their (8 + 2P) x (2 + 2P) window region: 2x8 blocks, or for 32 real
-// components at windows 3 and 11 4x4 blocks, which cover that region with
-// fewer pixels (ws 11: 15 blocks, 240 pixels, against 18 blocks, 288).
+// their (8 + 2P) x (2 + 2P) window region: 2x8 blocks, or at windows 3 and
+// 11 4x4 blocks, which cover that region with fewer pixels (ws 11: 15
+// blocks, 240 pixels, against 18 blocks, 288).
 // Element 4 g + r of a block (the score accumulator's row) sits at block row
 // r % 2, column 2 g + r / 2 (2x8), or at row r, column g (4x4).  LDS slots
 // are column-major with CR slots per column: CR = 2 mod 4 for 2x8 blocks and
@@ -265,7 +265,7 @@ struct HGeo {
     static constexpr int WH = grid_wh<NT>(), WW = 8;
     static constexpr int THREADS = 64 * WH * WW;
     static constexpr int TH = 8 * WH, TW = 2 * WW;
-    static constexpr int BR = (NT == 2 && (P == 1 || P == 5)) ? 4 : 2;  // block rows
+    static constexpr int BR = (P == 1 || P == 5) ? 4 : 2;  // block rows
     static constexpr int BC = 16 / BR;                                   // block columns
     static constexpr int NKH = (8 + 2 * P + BR - 1) / BR;
     static constexpr int NKW = (2 + 2 * P + BC - 1) / BC;
@@ -495,7 +495,7 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
     F2H_PHASE(uint64_t phase[4] = {0, 0, 0, 0};)
     unsigned *const xwords = reinterpret_cast<unsigned *>(lds + L::OX);
     if (threadIdx.x < 4) xwords[threadIdx.x] = 0u;
-    if constexpr (NT == 2) {
+    if constexpr (NT == 2 || BR == 4) {
         // slots never staged (pad rows, columns past the staged ones): zero
         // halves and scalars, so that the masked products over them stay
         // finite
