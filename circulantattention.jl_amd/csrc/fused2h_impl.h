@@ -155,7 +155,7 @@ __device__ __forceinline__ h8 cat(h4 a, h4 b) {
 // it issue (164k .. 260k), which cuts the cycles per launch (forward 331k ->
 // 317k per wave, query-centric pass 346k -> 324k); the clock drops with the
 // higher utilisation, so the gain in time is smaller.  The key-centric pass
-// keeps equal priorities: there the lower clock cancelled the gain.
+// uses walk_prio_tail instead (below).
 // (CIRCATT_F2H_PRIO=0 keeps equal priorities, for the comparison)
 #ifndef CIRCATT_F2H_PRIO
 #define CIRCATT_F2H_PRIO 1
@@ -163,6 +163,17 @@ __device__ __forceinline__ h8 cat(h4 a, h4 b) {
 template <int I, int N>
 __device__ __forceinline__ void walk_prio() {
     if constexpr (CIRCATT_F2H_PRIO && I * 4 % N < 4) __builtin_amdgcn_s_setprio(3 - I * 4 / N);
+}
+// Key-centric pass: priority 1 over the first three quarters of the walk, 0
+// over the last, so that a wave in its last quarter yields to the waves
+// behind it.  Measured at cfg3 on gfx950 (interleaved A/B, two boxes): key-
+// centric pass 233.5 -> 227.6 us; the quarter steps of walk_prio gave 0.7%,
+// two steps (at one half and three quarters) 1%, a single drop at one half
+// was slower (+3%).
+template <int I, int N>
+__device__ __forceinline__ void walk_prio_tail() {
+    if constexpr (CIRCATT_F2H_PRIO && I == 0) __builtin_amdgcn_s_setprio(1);
+    if constexpr (CIRCATT_F2H_PRIO && I == (3 * N) / 4) __builtin_amdgcn_s_setprio(0);
 }
 
 // LDS pixel slot: NT sub-pixels of 16 channels, each [16 hi | 16 lo] halves
@@ -1001,6 +1012,7 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
                 constexpr int b1 = has1 ? b0 + 1 : b0;
                 if constexpr (pi % CIRCATT_F2H_BWD_FSTEP == 0) BLOCK_FENCE();
                 if constexpr (MODE == BWDQ) walk_prio<pi, NPAIR>();
+                if constexpr (MODE == BWDKV) walk_prio_tail<pi, NPAIR>();
                 if constexpr (pi == PFP) prefetch();
                 float p[2][4], ds[2][4];
                 auto blk = [&](auto B, int u) {
