@@ -1,0 +1,87 @@
+"""CPU checks of the split-half kernels' tile geometry (csrc/fused2h_impl.h,
+HGeo and hmask), restated here: for every window the kernels instantiate and
+both head widths, the LDS blocks of a wavefront cover each query's window
+exactly once under the lane masks, the 16-byte row reads of a block fall in
+distinct banks, the reads stay within a slot column, and the staged halo and
+its scalars fit the 160 KiB of LDS.  A wrong block shape, element layout,
+column stride or mask fails one of these.  The GPU parity tests
+(test_gpu_parity.py, test_gpu_magnitudes.py) check the kernels themselves."""
+import pytest
+
+LDS_CAP = 160 * 1024
+
+
+def geo(P, NT):
+    WH = 2 if NT == 1 else 1
+    TH, TW = 8 * WH, 16
+    BR = 4 if P in (1, 5) else 2
+    BC = 16 // BR
+    NKH = (8 + 2 * P + BR - 1) // BR
+    NKW = (2 + 2 * P + BC - 1) // BC
+    HH = TH + 2 * P
+    HWD = 2 * 7 + BC * NKW
+    CR = HH + ((2 - HH % 4) + 4) % 4 if BR == 2 else HH + ((4 - HH % 16) + 16) % 16
+    SB = (32 * NT + 8) * 2
+    SWC = HWD if NT == 1 else TW + 2 * P
+    return dict(WH=WH, TH=TH, TW=TW, BR=BR, BC=BC, NKH=NKH, NKW=NKW, HH=HH, HWD=HWD, CR=CR,
+                SB=SB, SWC=SWC, LPX=CR * HWD, THREADS=64 * 8 * WH)
+
+
+def element(BR, bi, bj, g, r):
+    """Wave-relative key position of element 4 g + r of block (bi, bj)."""
+    if BR == 2:
+        return 2 * bi + (r & 1), 8 * bj + 2 * g + (r >> 1)
+    return 4 * bi + r, 4 * bj + g
+
+
+CASES = [(P, NT) for NT in (1, 2) for P in (1, 2, 3, 5, 7) if not (NT == 2 and P == 7)]
+
+
+@pytest.mark.parametrize("P,NT", CASES)
+def test_blocks_cover_each_window_once(P, NT):
+    G = geo(P, NT)
+    seen = {}
+    for bi in range(G["NKH"]):
+        for bj in range(G["NKW"]):
+            for g in range(4):
+                for r in range(4):
+                    kr, kc = element(G["BR"], bi, bj, g, r)
+                    for j in range(16):
+                        u1, u2 = kr - (j & 7), kc - (j >> 3)
+                        if 0 <= u1 <= 2 * P and 0 <= u2 <= 2 * P:  # the lane's mask bit
+                            key = (j, u1, u2)
+                            assert key not in seen, (key, seen.get(key), (bi, bj, g, r))
+                            seen[key] = (bi, bj, g, r)
+    assert len(seen) == 16 * (2 * P + 1) ** 2
+
+
+@pytest.mark.parametrize("P,NT", CASES)
+def test_block_rows_read_conflict_free(P, NT):
+    """Score-type rows: lanes j = 0..15 of a lane group read 16 bytes at
+    slot(element j) * SB; distinct 16-byte units modulo 256 bytes (64 banks of
+    4 bytes) mean no bank conflict within the group."""
+    G = geo(P, NT)
+    units = set()
+    for j in range(16):
+        row, col = (j & 1, j >> 1) if G["BR"] == 2 else (j & 3, j >> 2)
+        units.add(((row + G["CR"] * col) * G["SB"] // 16) % 16)
+    assert len(units) == 16
+
+
+@pytest.mark.parametrize("P,NT", CASES)
+def test_reads_stay_in_slots_and_halo_fits(P, NT):
+    G = geo(P, NT)
+    # a wavefront's block rows stay within its slot column; its columns within the slots
+    assert 8 * (G["WH"] - 1) + G["BR"] * G["NKH"] <= G["CR"]
+    assert 2 * 7 + G["BC"] * G["NKW"] <= G["HWD"]
+    # every key of a window lies in a staged row and column
+    assert 8 * (G["WH"] - 1) + 7 + 2 * P < G["HH"] and 2 * 7 + 1 + 2 * P < G["SWC"]
+    assert G["HH"] * G["SWC"] <= G["THREADS"]  # one staged pixel per thread
+    for nscal in (0, 1, 2):  # scalars: none, Distance key bias, the key-centric pass's two
+        assert 2 * G["LPX"] * G["SB"] + nscal * G["LPX"] * 4 + 16 <= LDS_CAP
+
+
+def test_4x4_blocks_do_less_work_at_ws_11():
+    two_by_eight = (4 + 5) * ((2 + 10 + 7) // 8) * 16
+    g = geo(5, 2)
+    assert g["BR"] == 4 and g["NKH"] * g["NKW"] * 16 == 240 and two_by_eight == 288
