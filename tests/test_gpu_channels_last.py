@@ -25,6 +25,8 @@ CASES = [
     ((20, 16), 64, 2, 2, 7, 1, False, "split"),     # split-half, 32 components (8x16 tiles)
     ((20, 16), 32, 2, 1, 3, 0, True, "split"),      # split-half, ComplexF32 32 components
     ((28, 20), 32, 2, 2, 11, 1, True, "split"),     # split-half, ComplexF32 32 components, streamed forward
+    ((24, 20), 32, 2, 2, 11, 1, False, "split"),    # split-half, 16 components, 4x4 blocks, streamed forward
+    ((20, 12), 16, 1, 2, 3, 0, False, "split"),     # split-half, 16 components, 4x4 blocks, ws 3
     ((20, 16), 64, 2, 2, 15, 0, False, "split"),    # Float32 matrix cores, 32 components at ws 15
     ((20, 16), 64, 2, 2, 7, 1, False, "f32"),       # Float32 matrix cores, 32 components
     ((150,), 32, 1, 2, 9, 0, False, "split"),       # run-time window, 1D
