@@ -894,7 +894,8 @@ hipError_t launch_sim_wide_t(ApplyArgs a, int64_t nb, hipStream_t s) {
 constexpr int kCG = 8;          // components per lane group and pass
 constexpr int kCPass = 4 * kCG; // components per pass
 
-template <int WS, int NCOMP, bool TRANS>
+// CG: components per lane group and pass (4 CG per pass)
+template <int WS, int NCOMP, bool TRANS, int CG = kCG>
 struct A2 {
     static constexpr int P = (WS - 1) / 2;
     static constexpr int NSRC = TRANS ? 64 + 2 * P : 64;  // staged chunks per row
@@ -913,7 +914,7 @@ struct A2 {
     static constexpr int XF = 4 * RF;
     static constexpr int XL = (XF / 4 + 63) / 64;         // interior: 16-byte DMA loads per lane
     static constexpr int XBF = XL * 256;                  // x buffer floats (border: 4 XL dword loads)
-    static constexpr int CHS = kCG / NCOMP;               // channels per group and pass
+    static constexpr int CHS = CG / NCOMP;                // channels per group and pass
     static constexpr int NZR = 2, NXB = 3;                // ring sizes
     static constexpr int NZR_SUMS = 4;                    // column sums: chunks 3 rows ahead
     // a lane's last x read may pass its row by 3 floats
@@ -928,9 +929,9 @@ struct A2 {
 // 16-byte pieces (interior tiles, and border tiles when n1 is a multiple of
 // the 4 / NCOMP pixels of a piece, so that no piece straddles the wrap);
 // otherwise float by float.
-template <int WS, int NCOMP, bool TRANS, bool FAST, bool SUMS = false, bool XV = FAST>
+template <int WS, int NCOMP, bool TRANS, bool FAST, bool SUMS = false, bool XV = FAST, int CG = kCG>
 __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1, int c2, int b) {
-    using S = A2<WS, NCOMP, TRANS>;
+    using S = A2<WS, NCOMP, TRANS, CG>;
     constexpr int P = S::P;
     constexpr int K = WS * WS;
     constexpr int XW = kR + 2 * P;
@@ -1020,7 +1021,7 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
     // the border body) f of group gs = f / RF.  A group's channels past C lie
     // past the unit's bytes: the range check makes their reads zero (they
     // are never stored).
-    const int ch0 = pass * (kCPass / NCOMP);  // first channel of the pass
+    const int ch0 = pass * (4 * CG / NCOMP);  // first channel of the pass
     int xo[XI];
 #pragma unroll
     for (int m = 0; m < XI; ++m) {
@@ -1059,13 +1060,13 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    float acc[kR][kCG];
+    float acc[kR][CG];
     float asum[kR];
 #pragma unroll
     for (int i = 0; i < kR; ++i) {
         asum[i] = 0.f;
 #pragma unroll
-        for (int k = 0; k < kCG; ++k) acc[i][k] = 0.f;
+        for (int k = 0; k < CG; ++k) acc[i][k] = 0.f;
     }
     // the lane's 4 x ws coefficients of window row dd, from chunk buffer zb
     auto read_av = [&](float (&av)[kR][WS], int zb) {
@@ -1234,19 +1235,19 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
 
 // the body for tile column t1: interior, border with 16-byte x pieces, or
 // border float by float
-template <int WS, int NCOMP, bool TRANS, bool SUMS>
+template <int WS, int NCOMP, bool TRANS, bool SUMS, int CG = kCG>
 __device__ __forceinline__ void apply2_tile(const ApplyArgs &a, int pass, int t1, int c2, int b) {
     if (t1 >= a.fa && t1 < a.fb)
-        apply2_body<WS, NCOMP, TRANS, true, SUMS>(a, pass, t1, c2, b);
+        apply2_body<WS, NCOMP, TRANS, true, SUMS, true, CG>(a, pass, t1, c2, b);
     else if (!SUMS && a.g.n1 % (4 / NCOMP) == 0)
-        apply2_body<WS, NCOMP, TRANS, false, SUMS, true>(a, pass, t1, c2, b);
+        apply2_body<WS, NCOMP, TRANS, false, SUMS, true, CG>(a, pass, t1, c2, b);
     else
-        apply2_body<WS, NCOMP, TRANS, false, SUMS, false>(a, pass, t1, c2, b);
+        apply2_body<WS, NCOMP, TRANS, false, SUMS, false, CG>(a, pass, t1, c2, b);
 }
 
 // One wavefront per (64 output pixels of an image row, component pass, unit);
 // work items in XCD bands as in sim_rows_kernel.
-template <int WS, int NCOMP, bool TRANS, bool SUMS = false>
+template <int WS, int NCOMP, bool TRANS, bool SUMS = false, int CG = kCG>
 __global__ __launch_bounds__(64, 2) void apply2_kernel(ApplyArgs a, int nwork) {
     const int nper = (nwork + 7) >> 3;
     int it = (int)(blockIdx.x & 7) * nper + (int)(blockIdx.x >> 3);
@@ -1257,7 +1258,7 @@ __global__ __launch_bounds__(64, 2) void apply2_kernel(ApplyArgs a, int nwork) {
     it /= a.tiles1;
     const int c2 = __builtin_amdgcn_readfirstlane(it % a.g.n2);
     const int b = __builtin_amdgcn_readfirstlane(it / a.g.n2);
-    apply2_tile<WS, NCOMP, TRANS, SUMS>(a, pass, t1, c2, b);
+    apply2_tile<WS, NCOMP, TRANS, SUMS, CG>(a, pass, t1, c2, b);
 }
 
 // The similarity pullback's two products in one grid: work items
@@ -2277,7 +2278,21 @@ hipError_t launch_rb(ApplyArgs a, int64_t nb, hipStream_t s) {
         if (a.fb > tiles1) a.fb = tiles1;
         if (a.fb < a.fa) a.fb = a.fa;
         a.gchunk = (NCOMP * a.C + kCPass - 1) / kCPass;  // component passes
-        const int64_t nwork = (int64_t)tiles1 * a.g.n2 * nb * a.gchunk;
+        int64_t nwork = (int64_t)tiles1 * a.g.n2 * nb * a.gchunk;
+        // Grids of fewer wavefronts than SIMDs are bound by each wavefront's
+        // chain of component steps: passes of 16 components there (twice the
+        // wavefronts, chains half as long; cfg2 on gfx950: forward 37.9 ->
+        // 34.1 us, transposed 42.9 -> 40.3 us).  Larger grids keep passes of
+        // 32 (cfg5's forward apply took 150 against 126 us with 16).
+        if (nwork < 1024 && NCOMP * a.C > kCPass / 2) {
+            using S4 = A2<WS, NCOMP, TRANS, kCG / 2>;
+            a.gchunk = (NCOMP * a.C + kCPass / 2 - 1) / (kCPass / 2);
+            nwork = (int64_t)tiles1 * a.g.n2 * nb * a.gchunk;
+            const int64_t grid = 8 * ((nwork + 7) / 8);
+            hipLaunchKernelGGL((apply2_kernel<WS, NCOMP, TRANS, false, kCG / 2>), dim3((unsigned)grid),
+                               dim3(64), (size_t)S4::LDS * sizeof(float), s, a, (int)nwork);
+            return hipGetLastError();
+        }
         const int64_t grid = 8 * ((nwork + 7) / 8);
         hipLaunchKernelGGL((apply2_kernel<WS, NCOMP, TRANS>), dim3((unsigned)grid), dim3(64),
                            (size_t)S::LDS * sizeof(float), s, a, (int)nwork);
