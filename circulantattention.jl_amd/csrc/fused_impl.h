@@ -345,12 +345,32 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
     float nr0[NS], nr1[NS], nry[NS];
     float nlse = 0.f;
 
+    // 2D tiles in bands of 8 tile rows, column by column within a band, so
+    // that the items an XCD runs at once (consecutive item numbers) form a
+    // compact block whose halos share that XCD's L2 (a column-major order
+    // puts them in one tall strip, whose halos at large windows overflow it)
     auto decode = [&](int item, int &unit, int &h0, int &w0) {
         const int ntiles = a.tiles_h * a.tiles_w;
         unit = item / ntiles;
         const int tile = item - unit * ntiles;
-        h0 = (tile % a.tiles_h) * G::TH;
-        w0 = (tile / a.tiles_h) * G::TW;
+        if constexpr (NSP == 2) {
+            const int full = (a.tiles_h >> 3) * 8 * a.tiles_w;  // tiles in full bands
+            int th, tw;
+            if (tile < full) {
+                const int band = tile / (8 * a.tiles_w), r = tile - band * 8 * a.tiles_w;
+                th = 8 * band + (r & 7);
+                tw = r >> 3;
+            } else {
+                const int bh = a.tiles_h & 7, r = tile - full;
+                th = (a.tiles_h & ~7) + r % bh;
+                tw = r / bh;
+            }
+            h0 = th * G::TH;
+            w0 = tw * G::TW;
+        } else {
+            h0 = (tile % a.tiles_h) * G::TH;
+            w0 = (tile / a.tiles_h) * G::TW;
+        }
     };
 
     auto load_stage = [&](int item, int chunk) {
