@@ -68,6 +68,23 @@ __host__ __device__ __forceinline__ int offset_to_slot(int d, int s, int M, int 
     return pmod(d + p + s, M);
 }
 
+// Tile (th, tw) of tile number t on a tiles_h x tiles_w grid, in bands of 8
+// tile rows, column by column within a band (the last band may be shorter):
+// consecutive tile numbers form compact 8-row blocks, so the tiles a GPU
+// region runs at once share their halos in its cache.  A bijection.
+__host__ __device__ __forceinline__ void banded_tile(int t, int tiles_h, int tiles_w, int &th, int &tw) {
+    const int full = (tiles_h >> 3) * 8 * tiles_w;  // tiles in full bands
+    if (t < full) {
+        const int band = t / (8 * tiles_w), r = t - band * 8 * tiles_w;
+        th = 8 * band + (r & 7);
+        tw = r >> 3;
+    } else {
+        const int bh = tiles_h & 7, r = t - full;
+        th = (tiles_h & ~7) + r % bh;
+        tw = r / bh;
+    }
+}
+
 // Geometry of one problem: nsp spatial dims, N1 (fastest) and N2 (1 for 1D),
 // window ws along each spatial dim.
 struct Geom {

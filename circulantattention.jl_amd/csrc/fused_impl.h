@@ -354,17 +354,8 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
         unit = item / ntiles;
         const int tile = item - unit * ntiles;
         if constexpr (NSP == 2) {
-            const int full = (a.tiles_h >> 3) * 8 * a.tiles_w;  // tiles in full bands
             int th, tw;
-            if (tile < full) {
-                const int band = tile / (8 * a.tiles_w), r = tile - band * 8 * a.tiles_w;
-                th = 8 * band + (r & 7);
-                tw = r >> 3;
-            } else {
-                const int bh = a.tiles_h & 7, r = tile - full;
-                th = (a.tiles_h & ~7) + r % bh;
-                tw = r / bh;
-            }
+            banded_tile(tile, a.tiles_h, a.tiles_w, th, tw);
             h0 = th * G::TH;
             w0 = tw * G::TW;
         } else {
