@@ -85,3 +85,23 @@ def test_4x4_blocks_do_less_work_at_ws_11():
     two_by_eight = (4 + 5) * ((2 + 10 + 7) // 8) * 16
     g = geo(5, 2)
     assert g["BR"] == 4 and g["NKH"] * g["NKW"] * 16 == 240 and two_by_eight == 288
+
+
+def banded_tile(t, tiles_h, tiles_w):
+    """circatt_common.h banded_tile: bands of 8 tile rows, column by column."""
+    full = (tiles_h >> 3) * 8 * tiles_w
+    if t < full:
+        band, r = divmod(t, 8 * tiles_w)
+        return 8 * band + (r & 7), r >> 3
+    bh, r = tiles_h & 7, t - full
+    return (tiles_h & ~7) + r % bh, r // bh
+
+
+def test_banded_tile_order_is_a_bijection_with_compact_runs():
+    for th_n in range(1, 41):
+        for tw_n in range(1, 23):
+            tiles = [banded_tile(t, th_n, tw_n) for t in range(th_n * tw_n)]
+            assert sorted(tiles) == [(h, w) for h in range(th_n) for w in range(tw_n)], (th_n, tw_n)
+    # 64 consecutive tiles of a full band form an 8 x 8 block
+    tiles = [banded_tile(t, 64, 64) for t in range(64 * 5, 64 * 6)]
+    assert {h for h, _ in tiles} == set(range(8)) and len({w for _, w in tiles}) == 8
