@@ -527,6 +527,16 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
 #pragma unroll UNROLL
         for (int qb = 0; qb < (CT ? GC.nkh * GC.nkw : nblk); qb += 2) {
             if (!ONECHUNK && qb >= nblk) break;
+            // 2D: wave priority 1 over the first three quarters of a chunk's
+            // block walk, 0 over the last, so that a wave near its end yields
+            // to the waves behind it (cfg4a on gfx950, interleaved A/B on two
+            // boxes: step 2838 -> 2702 and 2913 -> 2843 us; drops at two
+            // thirds or seven eighths no better; in 1D, cfg4b, 1.4% slower,
+            // so not there)
+            if constexpr (NSP == 2) {
+                if (qb == 0) __builtin_amdgcn_s_setprio(1);
+                if (qb == ((3 * nblk / 4) & ~1)) __builtin_amdgcn_s_setprio(0);
+            }
             const bool hasb = qb + 1 < nblk;
             int bi2 = bi, bj2 = bj + 1;
             if (bj2 == nkw) {
