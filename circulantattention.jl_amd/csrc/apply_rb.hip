@@ -509,6 +509,10 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
         int cur = 0;
 #pragma unroll 1
         for (int c = 0; c < nst; ++c) {
+            // priority 1 over the first three quarters of the steps, 0 over
+            // the last (cfg5 on gfx950, interleaved A/B: 145.6 -> 143.7 us)
+            if (c == 0) __builtin_amdgcn_s_setprio(1);
+            if (c == (3 * nst) / 4) __builtin_amdgcn_s_setprio(0);
             // loads issued after step c's: step c + 1's
             if (c + 1 < nst)
                 wait_vm<NI>();
@@ -691,6 +695,10 @@ __device__ __forceinline__ void sim_wide_body(const ApplyArgs &a, int t1, int c2
     const int nit = (NT + 3) / 4;
 #pragma unroll 1
     for (int itr = 0; itr < nit; ++itr) {
+        // priority 1 over the first three quarters, 0 over the last (cfg4a on
+        // gfx950, interleaved A/B: 926 -> 909 us)
+        if (itr == 0) __builtin_amdgcn_s_setprio(1);
+        if (itr == (3 * nit) / 4) __builtin_amdgcn_s_setprio(0);
         int ko[NK];
 #pragma unroll
         for (int m = 0; m < NK; ++m) {
