@@ -357,6 +357,19 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// vmcnt(C0 + n XI) for n in 0 .. K (n wave-uniform; constant after unrolling)
+template <int C0, int XI, int K>
+__device__ __forceinline__ void wait_vm_steps(int n) {
+    if constexpr (K == 0) {
+        wait_vm<C0>();
+    } else {
+        if (n >= K)
+            wait_vm<C0 + K * XI>();
+        else
+            wait_vm_steps<C0, XI, K - 1>(n);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // nzVal = scale * similarity(x, y) in 2D (src/similarity.jl:31-103): a
 // wavefront owns 64 consecutive pixels of one image row; lane group r takes
@@ -901,9 +914,19 @@ hipError_t launch_sim_wide_t(ApplyArgs a, int64_t nb, hipStream_t s) {
 // ---------------------------------------------------------------------------
 constexpr int kCG = 8;          // components per lane group and pass
 constexpr int kCPass = 4 * kCG; // components per pass
+// x ring sizes (x loads in flight kNX - 1 steps ahead of a step).  Four
+// buffers against three, interleaved A/B on gfx950 (identical outputs):
+// cfg5 apply 130 -> 125 us, transposed 140 -> 130 us, similarity pullback
+// (pair kernel) 263 -> 233 us; 1D ws = 63 (wide kernel) apply 104 -> 98 us,
+// pullback 198 -> 185 us.  Five were slower than four.  Grids of fewer
+// wavefronts than SIMDs (passes of 16 components) keep three: deeper rings
+// did not help there (cfg2 34.6 -> 36.9 us with five).
+constexpr int kNX = 4;
+constexpr int kNXSmall = 3;
 
-// CG: components per lane group and pass (4 CG per pass)
-template <int WS, int NCOMP, bool TRANS, int CG = kCG>
+// CG: components per lane group and pass (4 CG per pass); NX: x buffers in
+// the ring, so that NX - 1 steps' x loads are in flight ahead of a step
+template <int WS, int NCOMP, bool TRANS, int CG = kCG, int NX = 3>
 struct A2 {
     static constexpr int P = (WS - 1) / 2;
     static constexpr int NSRC = TRANS ? 64 + 2 * P : 64;  // staged chunks per row
@@ -923,13 +946,17 @@ struct A2 {
     static constexpr int XL = (XF / 4 + 63) / 64;         // interior: 16-byte DMA loads per lane
     static constexpr int XBF = XL * 256;                  // x buffer floats (border: 4 XL dword loads)
     static constexpr int CHS = CG / NCOMP;                // channels per group and pass
-    static constexpr int NZR = 2, NXB = 3;                // ring sizes
+    static constexpr int NZR = 2, NXB = NX;               // ring sizes
+    static constexpr int XD = NX - 1;                     // x prefetch distance in steps
     static constexpr int NZR_SUMS = 4;                    // column sums: chunks 3 rows ahead
     // a lane's last x read may pass its row by 3 floats
     static constexpr int LDS = NZR * NZB + NXB * XBF + 4;
     static constexpr int LDS_SUMS = NZR_SUMS * NZB;
     static constexpr int EDGE = kHalo > 2 * P ? kHalo : 2 * P;  // interior margin
     static_assert(CHS >= 2, "the step waits assume two or more steps per window row");
+    // a row's chunks are issued CHS steps ahead, at least as far as x, so the
+    // wait for x(t) also covers the chunks read at step t
+    static_assert(XD >= 2 && XD <= CHS, "x prefetch distance out of range");
 };
 
 // SUMS: column sums only (x = 1, no products): out[o] = sum of the staged
@@ -937,9 +964,10 @@ struct A2 {
 // 16-byte pieces (interior tiles, and border tiles when n1 is a multiple of
 // the 4 / NCOMP pixels of a piece, so that no piece straddles the wrap);
 // otherwise float by float.
-template <int WS, int NCOMP, bool TRANS, bool FAST, bool SUMS = false, bool XV = FAST, int CG = kCG>
+template <int WS, int NCOMP, bool TRANS, bool FAST, bool SUMS = false, bool XV = FAST, int CG = kCG,
+          int NX = 3>
 __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1, int c2, int b) {
-    using S = A2<WS, NCOMP, TRANS, CG>;
+    using S = A2<WS, NCOMP, TRANS, CG, NX>;
     constexpr int P = S::P;
     constexpr int K = WS * WS;
     constexpr int XW = kR + 2 * P;
@@ -951,7 +979,7 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
     // exceed the vmcnt field)
     constexpr int NZR = !SUMS ? S::NZR : ((S::NZR_SUMS - 1) * ZI < 64 ? S::NZR_SUMS : 3);
     constexpr int T = WS * S::CHS;                  // steps
-    static_assert(ZI + XI < 64 && (NZR - 1) * ZI < 64, "waits exceed vmcnt");
+    static_assert(ZI + (S::XD - 1) * XI < 64 && (NZR - 1) * ZI < 64, "waits exceed vmcnt");
     typedef __attribute__((address_space(3))) void *lptr;
     const Geom &g = a.g;
     const int n1 = g.n1, n2 = g.n2;
@@ -1131,12 +1159,16 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
         return;
     }
 
-    // issue order: chunks(0), x(0), x(1); step t issues [chunks(dd + 1) if
-    // cl == 0] then x(t + 2).  Loads issued after x(t): chunks(dd + 1) when
-    // cl == 1, and x(t + 1).
+    // issue order: chunks(0), x(0) .. x(XD - 1); step t issues
+    // [chunks(dd + 1) if cl == 0] then x(t + XD).  Loads issued after x(t):
+    // chunks(dd + 1) when 1 <= cl < XD, and x(t + 1) .. x(t + XD - 1) (those
+    // before T).  chunks(dd), issued CHS >= XD steps before row dd, precede
+    // x(t) at cl == 0.
+    constexpr int XD = S::XD;
     stage_z(0, 0);
-    stage_x(0, 0);
-    if (T > 1) stage_x(1, 1);
+#pragma unroll
+    for (int u = 0; u < XD; ++u)
+        if (u < T) stage_x(u, u);
     int xb = 0;  // x buffer of step t (t % NXB)
     float av[kR][WS];
 #pragma unroll 1
@@ -1150,16 +1182,12 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
         for (int cl = 0; cl < S::CHS; ++cl) {
             const int t = dd * S::CHS + cl;
             __builtin_amdgcn_sched_barrier(0);
-            const bool zy = cl == 1 && dd + 1 < WS;
-            const bool xy = t + 1 < T;
-            if (zy && xy)
-                wait_vm<ZI + XI>();
-            else if (zy)
-                wait_vm<ZI>();
-            else if (xy)
-                wait_vm<XI>();
+            const bool zy = cl >= 1 && cl < XD && dd + 1 < WS;
+            const int nx = min(XD - 1, T - 1 - t);  // x loads issued after x(t)
+            if (zy)
+                wait_vm_steps<ZI, XI, XD - 1>(nx);
             else
-                wait_vm<0>();
+                wait_vm_steps<0, XI, XD - 1>(nx);
             if (cl == 0) {
                 // chunks(dd) arrived before x(t), which was issued after them
                 read_av(av, dd & 1);
@@ -1174,7 +1202,7 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
             // row (chunks) ago; those reads are complete
             __builtin_amdgcn_s_waitcnt(kWaitLgkm);
             if (cl == 0 && dd + 1 < WS) stage_z(dd + 1, (dd + 1) & 1);
-            if (t + 2 < T) stage_x(t + 2, xb == 0 ? 2 : xb - 1);
+            if (t + XD < T) stage_x(t + XD, xb == 0 ? S::NXB - 1 : xb - 1);
             float xw[4 * KW4];
             const float *xr = lx + xb * S::XBF + grp * S::RF + NCOMP * (4 * l16 + kHalo - P) - AL;
 #pragma unroll
@@ -1248,19 +1276,19 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
 
 // the body for tile column t1: interior, border with 16-byte x pieces, or
 // border float by float
-template <int WS, int NCOMP, bool TRANS, bool SUMS, int CG = kCG>
+template <int WS, int NCOMP, bool TRANS, bool SUMS, int CG = kCG, int NX = 3>
 __device__ __forceinline__ void apply2_tile(const ApplyArgs &a, int pass, int t1, int c2, int b) {
     if (t1 >= a.fa && t1 < a.fb)
-        apply2_body<WS, NCOMP, TRANS, true, SUMS, true, CG>(a, pass, t1, c2, b);
+        apply2_body<WS, NCOMP, TRANS, true, SUMS, true, CG, NX>(a, pass, t1, c2, b);
     else if (!SUMS && a.g.n1 % (4 / NCOMP) == 0)
-        apply2_body<WS, NCOMP, TRANS, false, SUMS, true, CG>(a, pass, t1, c2, b);
+        apply2_body<WS, NCOMP, TRANS, false, SUMS, true, CG, NX>(a, pass, t1, c2, b);
     else
-        apply2_body<WS, NCOMP, TRANS, false, SUMS, false, CG>(a, pass, t1, c2, b);
+        apply2_body<WS, NCOMP, TRANS, false, SUMS, false, CG, NX>(a, pass, t1, c2, b);
 }
 
 // One wavefront per (64 output pixels of an image row, component pass, unit);
 // work items in XCD bands as in sim_rows_kernel.
-template <int WS, int NCOMP, bool TRANS, bool SUMS = false, int CG = kCG>
+template <int WS, int NCOMP, bool TRANS, bool SUMS = false, int CG = kCG, int NX = 3>
 __global__ __launch_bounds__(64, 2) void apply2_kernel(ApplyArgs a, int nwork) {
     const int nper = (nwork + 7) >> 3;
     int it = (int)(blockIdx.x & 7) * nper + (int)(blockIdx.x >> 3);
@@ -1271,14 +1299,14 @@ __global__ __launch_bounds__(64, 2) void apply2_kernel(ApplyArgs a, int nwork) {
     it /= a.tiles1;
     const int c2 = __builtin_amdgcn_readfirstlane(it % a.g.n2);
     const int b = __builtin_amdgcn_readfirstlane(it / a.g.n2);
-    apply2_tile<WS, NCOMP, TRANS, SUMS, CG>(a, pass, t1, c2, b);
+    apply2_tile<WS, NCOMP, TRANS, SUMS, CG, NX>(a, pass, t1, c2, b);
 }
 
 // The similarity pullback's two products in one grid: work items
 // [0, nwork) are A ⊗ y (args af), [nwork, 2 nwork) are Aᵀ ⊗ x (args at), each
 // half in XCD bands, so that the two share the GPU instead of running one
 // after the other.
-template <int WS, int NCOMP>
+template <int WS, int NCOMP, int NX = 3>
 __global__ __launch_bounds__(64, 2) void apply2_pair_kernel(ApplyArgs af, ApplyArgs at, int nwork) {
     const int nall = 2 * nwork;
     const int nper = (nall + 7) >> 3;
@@ -1294,9 +1322,9 @@ __global__ __launch_bounds__(64, 2) void apply2_pair_kernel(ApplyArgs af, ApplyA
     const int c2 = __builtin_amdgcn_readfirstlane(it % a.g.n2);
     const int b = __builtin_amdgcn_readfirstlane(it / a.g.n2);
     if (trans)
-        apply2_tile<WS, NCOMP, true, false>(at, pass, t1, c2, b);
+        apply2_tile<WS, NCOMP, true, false, kCG, NX>(at, pass, t1, c2, b);
     else
-        apply2_tile<WS, NCOMP, false, false>(af, pass, t1, c2, b);
+        apply2_tile<WS, NCOMP, false, false, kCG, NX>(af, pass, t1, c2, b);
 }
 
 // ---------------------------------------------------------------------------
@@ -1327,10 +1355,12 @@ struct AW {
     static constexpr int XL = (XF / 4 + 63) / 64;
     static constexpr int XBF = XL * 256;
     static constexpr int CHS = kCG / NCOMP;
-    static constexpr int NZR = 2, NXB = 3;
+    static constexpr int NZR = 2, NXB = kNX;
+    static constexpr int XD = NXB - 1;
     static constexpr int LDS = NZR * NZB + NXB * XBF + 4;
     static constexpr int LDS_SUMS = 4 * NZB;
     static_assert(CHS >= 2, "the step waits assume two or more steps per sub-row");
+    static_assert(XD >= 2 && XD <= CHS, "x prefetch distance out of range");
 };
 
 template <int NCOMP, bool TRANS, bool FAST, bool SUMS>
@@ -1341,7 +1371,7 @@ __device__ __forceinline__ void apply_wide_body(const ApplyArgs &a, int pass, in
     constexpr int ZI = FAST ? S::NZ4 : S::NZ1;
     constexpr int XI = FAST ? S::XL : 4 * S::XL;
     constexpr int NZR = !SUMS ? S::NZR : (3 * ZI < 64 ? 4 : 3);
-    static_assert(ZI + XI < 64 && (NZR - 1) * ZI < 64, "waits exceed vmcnt");
+    static_assert(ZI + (S::XD - 1) * XI < 64 && (NZR - 1) * ZI < 64, "waits exceed vmcnt");
     typedef __attribute__((address_space(3))) void *lptr;
     const Geom &g = a.g;
     const int WS = g.ws, P = g.p, K = g.K;
@@ -1536,9 +1566,11 @@ __device__ __forceinline__ void apply_wide_body(const ApplyArgs &a, int pass, in
 
     // issue order and waits as in apply2_body, over T = NSR x CHS steps
     const int T = NSR * S::CHS;
+    constexpr int XD = S::XD;
     stage_z(0, 0);
-    stage_x(0, 0);
-    if (T > 1) stage_x(1, 1);
+#pragma unroll
+    for (int u = 0; u < XD; ++u)
+        if (u < T) stage_x(u, u);
     int xb = 0;
     float av[kR][kJC];
 #pragma unroll 1
@@ -1547,16 +1579,12 @@ __device__ __forceinline__ void apply_wide_body(const ApplyArgs &a, int pass, in
         for (int cl = 0; cl < S::CHS; ++cl) {
             const int t = sr * S::CHS + cl;
             __builtin_amdgcn_sched_barrier(0);
-            const bool zy = cl == 1 && sr + 1 < NSR;
-            const bool xy = t + 1 < T;
-            if (zy && xy)
-                wait_vm<ZI + XI>();
-            else if (zy)
-                wait_vm<ZI>();
-            else if (xy)
-                wait_vm<XI>();
+            const bool zy = cl >= 1 && cl < XD && sr + 1 < NSR;
+            const int nx = min(XD - 1, T - 1 - t);  // x loads issued after x(t)
+            if (zy)
+                wait_vm_steps<ZI, XI, XD - 1>(nx);
             else
-                wait_vm<0>();
+                wait_vm_steps<0, XI, XD - 1>(nx);
             if (cl == 0) {
                 read_av(av, sr & 1, sr);
                 if (a.corr) {
@@ -1568,7 +1596,7 @@ __device__ __forceinline__ void apply_wide_body(const ApplyArgs &a, int pass, in
             }
             __builtin_amdgcn_s_waitcnt(kWaitLgkm);
             if (cl == 0 && sr + 1 < NSR) stage_z(sr + 1, (sr + 1) & 1);
-            if (t + 2 < T) stage_x(t + 2, xb == 0 ? 2 : xb - 1);
+            if (t + XD < T) stage_x(t + XD, xb == 0 ? S::NXB - 1 : xb - 1);
             float xw[4 * KW4];
             const float *xr = lx + xb * S::XBF + grp * S::RF + NCOMP * 4 * l16;
 #pragma unroll
@@ -2289,7 +2317,9 @@ inline void interior_cols(const Geom &g, int &fa, int &fb) {
 template <int WS, int NCOMP, bool TRANS>
 hipError_t launch_rb(ApplyArgs a, int64_t nb, hipStream_t s) {
     if (a.g.nsp == 2) {
-        using S = A2<WS, NCOMP, TRANS>;
+        constexpr int NXL = kNX;
+        constexpr int NXS = kNXSmall;
+        using S = A2<WS, NCOMP, TRANS, kCG, NXL>;
         const int tiles1 = (a.g.n1 + 63) / 64;
         a.tiles1 = tiles1;
         a.fa = (S::EDGE + 63) / 64;
@@ -2304,16 +2334,16 @@ hipError_t launch_rb(ApplyArgs a, int64_t nb, hipStream_t s) {
         // 34.1 us, transposed 42.9 -> 40.3 us).  Larger grids keep passes of
         // 32 (cfg5's forward apply took 150 against 126 us with 16).
         if (nwork < 1024 && NCOMP * a.C > kCPass / 2) {
-            using S4 = A2<WS, NCOMP, TRANS, kCG / 2>;
+            using S4 = A2<WS, NCOMP, TRANS, kCG / 2, NXS>;
             a.gchunk = (NCOMP * a.C + kCPass / 2 - 1) / (kCPass / 2);
             nwork = (int64_t)tiles1 * a.g.n2 * nb * a.gchunk;
             const int64_t grid = 8 * ((nwork + 7) / 8);
-            hipLaunchKernelGGL((apply2_kernel<WS, NCOMP, TRANS, false, kCG / 2>), dim3((unsigned)grid),
+            hipLaunchKernelGGL((apply2_kernel<WS, NCOMP, TRANS, false, kCG / 2, NXS>), dim3((unsigned)grid),
                                dim3(64), (size_t)S4::LDS * sizeof(float), s, a, (int)nwork);
             return hipGetLastError();
         }
         const int64_t grid = 8 * ((nwork + 7) / 8);
-        hipLaunchKernelGGL((apply2_kernel<WS, NCOMP, TRANS>), dim3((unsigned)grid), dim3(64),
+        hipLaunchKernelGGL((apply2_kernel<WS, NCOMP, TRANS, false, kCG, NXL>), dim3((unsigned)grid), dim3(64),
                            (size_t)S::LDS * sizeof(float), s, a, (int)nwork);
         return hipGetLastError();
     }
@@ -2343,9 +2373,11 @@ hipError_t launch_pair_t(ApplyArgs f, ApplyArgs t, int64_t nb, hipStream_t s) {
     set_rows2<WS, NCOMP, true>(t);
     const int64_t nwork = (int64_t)f.tiles1 * f.g.n2 * nb * f.gchunk;
     const int64_t grid = 8 * ((2 * nwork + 7) / 8);
-    const size_t lds = (size_t)std::max(A2<WS, NCOMP, false>::LDS, A2<WS, NCOMP, true>::LDS) *
+    constexpr int NX = kNX;
+    const size_t lds = (size_t)std::max(A2<WS, NCOMP, false, kCG, NX>::LDS,
+                                        A2<WS, NCOMP, true, kCG, NX>::LDS) *
                        sizeof(float);
-    hipLaunchKernelGGL((apply2_pair_kernel<WS, NCOMP>), dim3((unsigned)grid), dim3(64), lds, s, f,
+    hipLaunchKernelGGL((apply2_pair_kernel<WS, NCOMP, NX>), dim3((unsigned)grid), dim3(64), lds, s, f,
                        t, (int)nwork);
     return hipGetLastError();
 }
