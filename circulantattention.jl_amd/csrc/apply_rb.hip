@@ -381,9 +381,9 @@ __device__ __forceinline__ void wait_vm_steps(int n) {
 // Per channel the 4 key rows' columns f1 - kHalo .. f1 + 63 + kHalo and the
 // 64 query pixels are staged into LDS by LDS-DMA, in 16-byte pieces (3 + 1
 // loads for complex data instead of one overlapping run of 4 + 2p pixels per
-// lane), into a ring of 3 buffers two channels ahead; the lanes read their
-// runs back from LDS.  Loads return in issue order, and each channel waits
-// with a vmcnt that counts the loads of the next channel.
+// lane), into a ring of NR buffers NR - 1 channels ahead; the lanes read
+// their runs back from LDS.  Loads return in issue order, and each channel
+// waits with a vmcnt that counts the loads of the channels staged after it.
 // ---------------------------------------------------------------------------
 constexpr int kHalo = 8;  // staged key columns beyond each side (>= p)
 constexpr int kJC = 16;   // window columns per sub-row (windows wider than 15)
@@ -403,7 +403,10 @@ struct SimStage {
     static constexpr int QOFF = KL * 256;      // query area (floats)
     static constexpr int SB = QOFF + 256;      // floats per ring buffer
     static constexpr int KL1 = KF / 64, QL1 = QF / 64;  // 4-byte loads (border)
-    static constexpr int NR = 3;               // ring buffers
+    // ring buffers: complex data three steps ahead (cfg5 on gfx950,
+    // interleaved A/B: 142.4 -> 137.9 us, five buffers 148.9 us); real data
+    // two (three ahead was within noise or slower at cfg2, cfg4a and 512x96)
+    static constexpr int NR = NCOMP == 2 ? 4 : 3;
 };
 
 // XV: pieces of 16 bytes (interior segments, and border segments when n1 is
@@ -517,8 +520,11 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
             for (int j = 0; j < WS; ++j) acc[i][j] = 0.f;
         // the previous iteration's reads of the LDS area are complete
         __builtin_amdgcn_s_waitcnt(kWaitLgkm);
-        stage(0, 0);
-        if (nst > 1) stage(1, 1);
+        constexpr int SD = S::NR - 1;  // steps staged ahead
+        static_assert((SD - 1) * NI < 64, "waits exceed vmcnt");
+#pragma unroll
+        for (int u = 0; u < SD; ++u)
+            if (u < nst) stage(u, u);
         int cur = 0;
 #pragma unroll 1
         for (int c = 0; c < nst; ++c) {
@@ -526,14 +532,11 @@ __device__ __forceinline__ void sim_body(const ApplyArgs &a, int gc, int t1, int
             // the last (cfg5 on gfx950, interleaved A/B: 145.6 -> 143.7 us)
             if (c == 0) __builtin_amdgcn_s_setprio(1);
             if (c == (3 * nst) / 4) __builtin_amdgcn_s_setprio(0);
-            // loads issued after step c's: step c + 1's
-            if (c + 1 < nst)
-                wait_vm<NI>();
-            else
-                wait_vm<0>();
+            // loads issued after step c's: those of steps c + 1 .. c + SD - 1
+            wait_vm_steps<0, NI, SD - 1>(min(SD - 1, nst - 1 - c));
             // the buffer refilled here was read for step c - 1
             __builtin_amdgcn_s_waitcnt(kWaitLgkm);
-            if (c + 2 < nst) stage(c + 2, cur == 0 ? 2 : cur - 1);
+            if (c + SD < nst) stage(c + SD, cur == 0 ? S::NR - 1 : cur - 1);
             const float *sb = lw + cur * S::SB;
 #pragma unroll
             for (int hc = 0; hc < CP; ++hc) {
@@ -760,17 +763,17 @@ __device__ __forceinline__ void sim_wide_body(const ApplyArgs &a, int t1, int c2
 #pragma unroll
             for (int j = 0; j < kJC; ++j) acc[i][j] = 0.f;
         __builtin_amdgcn_s_waitcnt(kWaitLgkm);
-        stage(0, 0);
-        if (a.C > 1) stage(1, 1);
+        constexpr int SD = S::NR - 1;  // channels staged ahead
+        static_assert((SD - 1) * NI < 64, "waits exceed vmcnt");
+#pragma unroll
+        for (int u = 0; u < SD; ++u)
+            if (u < a.C) stage(u, u);
         int cur = 0;
 #pragma unroll 1
         for (int c = 0; c < a.C; ++c) {
-            if (c + 1 < a.C)
-                wait_vm<NI>();
-            else
-                wait_vm<0>();
+            wait_vm_steps<0, NI, SD - 1>(min(SD - 1, a.C - 1 - c));
             __builtin_amdgcn_s_waitcnt(kWaitLgkm);
-            if (c + 2 < a.C) stage(c + 2, cur == 0 ? 2 : cur - 1);
+            if (c + SD < a.C) stage(c + SD, cur == 0 ? S::NR - 1 : cur - 1);
             const float *sb = lw + cur * S::SB;
             float q[4 * NCOMP], kw[4 * KW4];
 #pragma unroll
