@@ -944,6 +944,10 @@ struct A2 {
     static constexpr int NZ4 = (NSLOT + 63) / 64;         // interior: 16-byte DMA loads per lane
     static constexpr int NZ1 = (4 * NSLOT + 63) / 64;     // border: 4-byte DMA loads per lane
     static constexpr int NZB = NZ4 * 256 > NZ1 * 64 ? NZ4 * 256 : NZ1 * 64;  // chunk buffer floats
+    // border tiles, mixed form: single-slot loads per lane over the LDS span
+    // of a run of 2p chunks
+    static constexpr int ND = (2 * P * WSP + 4 * ((2 * P + 3) / 4) + 63) / 64;
+    static_assert(64 * ND <= NZB, "the single-slot window fits a chunk buffer");
     static constexpr int RF = NCOMP * (64 + 2 * kHalo);   // x floats per group
     static constexpr int XF = 4 * RF;
     static constexpr int XL = (XF / 4 + 63) / 64;         // interior: 16-byte DMA loads per lane
@@ -966,9 +970,12 @@ struct A2 {
 // coefficients, written to a.y (one float per pixel).  XV: x is staged in
 // 16-byte pieces (interior tiles, and border tiles when n1 is a multiple of
 // the 4 / NCOMP pixels of a piece, so that no piece straddles the wrap);
-// otherwise float by float.
+// otherwise float by float.  ZM (border tiles whose rotated chunks form one
+// run): chunks in 16-byte pieces as in the interior, except the rotated ones
+// (columns within p of the image border, whose slot order the reference
+// shifts), which a window of single-slot loads over that run writes.
 template <int WS, int NCOMP, bool TRANS, bool FAST, bool SUMS = false, bool XV = FAST, int CG = kCG,
-          int NX = 3>
+          int NX = 3, bool ZM = false>
 __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1, int c2, int b) {
     using S = A2<WS, NCOMP, TRANS, CG, NX>;
     constexpr int P = S::P;
@@ -976,7 +983,9 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
     constexpr int XW = kR + 2 * P;
     constexpr int AL = (NCOMP * (kHalo - P)) % 4;
     constexpr int KW4 = (NCOMP * XW + AL + 3) / 4;
-    constexpr int ZI = FAST ? S::NZ4 : S::NZ1;      // chunk loads per lane and row
+    static_assert(!ZM || (!FAST && XV && !SUMS), "mixed chunk loads are a border form");
+    constexpr int ND = ZM ? S::ND : 0;              // single-slot loads per lane (mixed form)
+    constexpr int ZI = FAST ? S::NZ4 : ZM ? S::NZ4 + ND : S::NZ1;  // chunk loads per lane and row
     constexpr int XI = XV ? S::XL : 4 * S::XL;      // x loads per lane and step
     // (column sums: one row fewer ahead where three rows of loads would
     // exceed the vmcnt field)
@@ -1008,22 +1017,55 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
     // single slots.  A lane's byte offset within an image row of nzVal does
     // not depend on the window row.
     int zo[ZI];
+    bool zon[ZM ? S::NZ4 : 1];  // mixed form: the piece's chunk is not rotated (or the lane's slot is a gap)
 #pragma unroll
-    for (int m = 0; m < ZI; ++m) {
+    for (int m = 0; m < (ZM ? S::NZ4 : ZI); ++m) {
         const int off = TRANS ? P : 0;
         // LDS slot of this lane's piece -> (chunk w, piece q); free slots and
         // pieces past the last chunk load chunk 0 / the last chunk (unused)
-        const int f = FAST ? lane + 64 * m : (lane + 64 * m) >> 2;
+        const int f = FAST || ZM ? lane + 64 * m : (lane + 64 * m) >> 2;
         const int kb = f / S::BLK, r = f - kb * S::BLK;
         const int rq = r < 4 * S::Q ? r : 0;
         const int w = min(4 * kb + rq / S::Q, S::NSRC - 1), q = rq - (rq / S::Q) * S::Q;
         if (FAST) {
             zo[m] = ((f1 - off + w) * K + 4 * q) * 4;
+        } else if (ZM) {
+            const int col = pmod(f1 - off + w, n1);
+            zo[m] = (col * K + 4 * q) * 4;
+            zon[m] = r >= 4 * S::Q || shift0(col, n1, P) == 0;
         } else {
             const int j = 4 * q + ((lane + 64 * m) & 3);
             const int col = pmod(f1 - off + w, n1);
             const int e = fold((j < WS ? j : 0) + shift0(col, n1, P), WS);
             zo[m] = (col * K + e) * 4;
+        }
+    }
+    // Mixed form: the rotated chunks are those of columns n1 - p .. n1 + p - 1
+    // (mod n1), one run [a0, a0 + 2p) of chunk indices clipped to the staged
+    // ones (n1 >= NSRC + 2p, so the run does not wrap).  The single-slot
+    // window covers ND x 64 floats from the run's first slot (moved back to
+    // stay inside the buffer); each of its lanes loads the element its LDS
+    // float holds in either form (the rotation of a chunk not in the run is
+    // zero, so there it writes what the piece loads write).
+    int zbase = 0;
+    if constexpr (ZM) {
+        const int off = TRANS ? P : 0;
+        const int c0 = pmod(f1 - off, n1);
+        const int d = pmod(n1 - P - c0, n1);
+        const int a0 = d < S::NSRC ? d : 0;
+        zbase = __builtin_amdgcn_readfirstlane(min(a0 * S::WSP + 4 * (a0 >> 2), S::NZB - 64 * ND));
+#pragma unroll
+        for (int i = 0; i < ND; ++i) {
+            const int ps = zbase + 64 * i + lane;     // LDS float
+            const int sl = ps >> 2, kb = sl / S::BLK, r = sl - kb * S::BLK;
+            const int w = 4 * kb + r / S::Q;
+            const int j = 4 * (r - (r / S::Q) * S::Q) + (ps & 3);
+            int e = 0, col = 0;
+            if (r < 4 * S::Q && w < S::NSRC) {
+                col = pmod(f1 - off + w, n1);
+                e = j < WS ? fold(j + shift0(col, n1, P), WS) : 0;
+            }
+            zo[S::NZ4 + i] = (col * K + e) * 4;
         }
     }
     // image row and chunk index of window row dd
@@ -1043,6 +1085,25 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
         // the whole offset is in the vector operand, which the range check sees
         const int so = __builtin_amdgcn_readfirstlane((n1 * r2 * K + mm * WS) * 4);
         float *dst = lz + buf * S::NZB;
+        if constexpr (ZM) {
+            // pieces of the chunks not rotated (every instruction has gap
+            // lanes, which stay active, so each is issued), then the window
+#pragma unroll
+            for (int m = 0; m < S::NZ4; ++m) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (zon[m])
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(dst + 256 * m), 16,
+                                                            zo[m] + so, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < ND; ++i) {
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(dst + zbase + 64 * i), 4,
+                                                        zo[S::NZ4 + i] + so, 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            return;
+        }
 #pragma unroll
         for (int m = 0; m < ZI; ++m) {
             __builtin_amdgcn_sched_barrier(0);
@@ -1281,9 +1342,19 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
 // border float by float
 template <int WS, int NCOMP, bool TRANS, bool SUMS, int CG = kCG, int NX = 3>
 __device__ __forceinline__ void apply2_tile(const ApplyArgs &a, int pass, int t1, int c2, int b) {
-    if (t1 >= a.fa && t1 < a.fb)
+    using S = A2<WS, NCOMP, TRANS, CG, NX>;
+    const bool xv = !SUMS && a.g.n1 % (4 / NCOMP) == 0;
+    if (t1 >= a.fa && t1 < a.fb) {
         apply2_body<WS, NCOMP, TRANS, true, SUMS, true, CG, NX>(a, pass, t1, c2, b);
-    else if (!SUMS && a.g.n1 % (4 / NCOMP) == 0)
+        return;
+    }
+    if constexpr (!SUMS) {
+        if (xv && a.g.n1 >= S::NSRC + 2 * S::P) {
+            apply2_body<WS, NCOMP, TRANS, false, SUMS, true, CG, NX, true>(a, pass, t1, c2, b);
+            return;
+        }
+    }
+    if (xv)
         apply2_body<WS, NCOMP, TRANS, false, SUMS, true, CG, NX>(a, pass, t1, c2, b);
     else
         apply2_body<WS, NCOMP, TRANS, false, SUMS, false, CG, NX>(a, pass, t1, c2, b);
