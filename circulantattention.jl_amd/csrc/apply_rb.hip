@@ -1437,12 +1437,22 @@ struct AW {
     static_assert(XD >= 2 && XD <= CHS, "x prefetch distance out of range");
 };
 
-template <int NCOMP, bool TRANS, bool FAST, bool SUMS>
+// single-slot loads per lane of the wide kernel's mixed border form: the LDS
+// span of a run of 30 sub-chunks (windows up to 31)
+constexpr int kWideMixP = 15;
+constexpr int kNDW = (2 * kWideMixP * kJC + 4 * ((2 * kWideMixP + 3) / 4) + 63) / 64;
+
+// ZM: border tiles in the mixed form of apply2_body (sub-chunks of columns
+// whose slot order is not rotated in 16-byte pieces, a window of single-slot
+// loads over the run of rotated ones); p <= kWideMixP and n1 >= NSRC + 2p
+template <int NCOMP, bool TRANS, bool FAST, bool SUMS, bool ZM = false>
 __device__ __forceinline__ void apply_wide_body(const ApplyArgs &a, int pass, int t1, int c2,
                                                 int b) {
     using S = AW<NCOMP, TRANS>;
     constexpr int KW4 = (NCOMP * (kR + kJC - 1) + 3) / 4;
-    constexpr int ZI = FAST ? S::NZ4 : S::NZ1;
+    static_assert(!ZM || !FAST, "mixed chunk loads are a border form");
+    static_assert(64 * kNDW <= S::NZB, "the single-slot window fits a chunk buffer");
+    constexpr int ZI = FAST ? S::NZ4 : ZM ? S::NZ4 + kNDW : S::NZ1;
     constexpr int XI = FAST ? S::XL : 4 * S::XL;
     constexpr int NZR = !SUMS ? S::NZR : (3 * ZI < 64 ? 4 : 3);
     static_assert(ZI + (S::XD - 1) * XI < 64 && (NZR - 1) * ZI < 64, "waits exceed vmcnt");
@@ -1509,6 +1519,48 @@ __device__ __forceinline__ void apply_wide_body(const ApplyArgs &a, int pass, in
         const int e = j < WS ? fold(j + shift0(col, n1, P), WS) : 0;
         return (col * K + e) * 4;
     };
+    // mixed form: offsets of sub-row column jc (relative to the row's first
+    // slot), the window's first LDS float and the piece lanes' enable bits.
+    // The rotated columns n1 - p .. n1 + p - 1 (mod n1) form one run of
+    // sub-chunks; each window lane loads what its LDS float holds in either
+    // form.  With n1 >= NSRC + 2p every column lies in [-n1, 2 n1), so one
+    // conditional step wraps it.
+    auto wrap1 = [&](int x) { return x < 0 ? x + n1 : (x >= n1 ? x - n1 : x); };
+    auto zm_make = [&](int jc, int (&zm)[ZI], int &zb, int &on) {
+        const int c0 = col0(jc);
+        on = 0;
+#pragma unroll
+        for (int m = 0; m < S::NZ4; ++m) {
+            const int f = lane + 64 * m;
+            const int kb = f / S::BLK, r = f - kb * S::BLK;
+            const int rq = r < 4 * S::Q ? r : 0;
+            const int w = min(4 * kb + rq / S::Q, S::NSRC - 1), q = rq - (rq / S::Q) * S::Q;
+            const int col = wrap1(c0 + w);
+            zm[m] = (col * K + kJC * jc + 4 * q) * 4;
+            if (r >= 4 * S::Q || shift0(col, n1, P) == 0) on |= 1 << m;
+        }
+        const int d = wrap1(n1 - P - wrap1(c0));
+        const int a0 = d < S::NSRC ? d : 0;
+        zb = __builtin_amdgcn_readfirstlane(min(a0 * kJC + 4 * (a0 >> 2), S::NZB - 64 * kNDW));
+#pragma unroll
+        for (int i = 0; i < kNDW; ++i) {
+            const int ps = zb + 64 * i + lane;
+            const int sl = ps >> 2, kb = sl / S::BLK, r = sl - kb * S::BLK;
+            const int w = 4 * kb + r / S::Q;
+            const int j = kJC * jc + 4 * (r - (r / S::Q) * S::Q) + (ps & 3);
+            int e = 0, col = 0;
+            if (r < 4 * S::Q && w < S::NSRC) {
+                col = wrap1(c0 + w);
+                e = j < WS ? fold(j + shift0(col, n1, P), WS) : 0;
+            }
+            zm[S::NZ4 + i] = (col * K + e) * 4;
+        }
+    };
+    int zmo[ZM && SUMS ? 2 : 1][ZM && SUMS ? ZI : 1], zmb[2] = {0, 0}, zmon[2] = {0, 0};
+    if constexpr (ZM && SUMS) {
+        zm_make(0, zmo[0], zmb[0], zmon[0]);
+        if (NJC > 1) zm_make(1, zmo[1], zmb[1], zmon[1]);
+    }
     auto stage_z = [&](int sr, int buf) {
         const int dd = sr / NJC, jc = sr - dd * NJC;
         int r2, mm;
@@ -1522,6 +1574,34 @@ __device__ __forceinline__ void apply_wide_body(const ApplyArgs &a, int pass, in
                 __builtin_amdgcn_sched_barrier(0);
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(dst + 256 * m), 16, zo[m] + so,
                                                         0, 0, 0);
+            }
+        } else if constexpr (ZM) {
+            const int so = __builtin_amdgcn_readfirstlane((n1 * r2 * K + mm * WS) * 4);
+            int zm[ZI], zb, on;
+            if constexpr (SUMS) {
+                // formed once per item (windows up to 31 have two sub-rows)
+                zb = jc == 0 ? zmb[0] : zmb[1];
+                on = jc == 0 ? zmon[0] : zmon[1];
+#pragma unroll
+                for (int m = 0; m < ZI; ++m) zm[m] = jc == 0 ? zmo[0][m] : zmo[1][m];
+            } else {
+                zm_make(jc, zm, zb, on);
+            }
+            // pieces of the sub-chunks whose columns are not rotated (gap
+            // lanes stay active, so every instruction is issued), then the
+            // window over the run of rotated ones
+#pragma unroll
+            for (int m = 0; m < S::NZ4; ++m) {
+                __builtin_amdgcn_sched_barrier(0);
+                if ((on >> m) & 1)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(dst + 256 * m), 16, zm[m] + so,
+                                                            0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < kNDW; ++i) {
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lptr)(dst + zb + 64 * i), 4,
+                                                        zm[S::NZ4 + i] + so, 0, 0, 0);
             }
         } else {
             const int so = __builtin_amdgcn_readfirstlane((n1 * r2 * K + mm * WS) * 4);
@@ -1754,6 +1834,8 @@ __device__ __forceinline__ void apply_wide_tile(const ApplyArgs &a, int pass, in
                                                 int b) {
     if (t1 >= a.fa && t1 < a.fb)
         apply_wide_body<NCOMP, TRANS, true, SUMS>(a, pass, t1, c2, b);
+    else if (a.g.p <= kWideMixP && a.g.n1 >= AW<NCOMP, TRANS>::NSRC + 2 * a.g.p)
+        apply_wide_body<NCOMP, TRANS, false, SUMS, true>(a, pass, t1, c2, b);
     else
         apply_wide_body<NCOMP, TRANS, false, SUMS>(a, pass, t1, c2, b);
 }

@@ -1,5 +1,6 @@
-"""CPU check of the 2D apply kernel's chunk staging on border tiles
-(csrc/apply_rb.hip, A2 and apply2_body), restated here.
+"""CPU check of the apply kernels' chunk staging on border tiles
+(csrc/apply_rb.hip: the 2D row kernel, A2 and apply2_body, and the
+wide-window kernel, AW and apply_wide_body), restated here.
 
 The border form stages every slot of every chunk with a single-slot load
 whose source element undoes the reference's rotation of the slot order near
@@ -128,3 +129,85 @@ def test_a_planted_short_window_is_caught():
     bad = [(w, j) for w in range(G["NSRC"]) for j in range(15)
            if mix.get(w * G["WSP"] + 4 * (w // 4) + j) != ref[w * G["WSP"] + 4 * (w // 4) + j]]
     assert bad
+
+
+# Wide windows (apply_wide_body, AW): sub-chunks of kJC = 16 slots of window
+# row dd's slots 16 jc .. 16 jc + 15; the mixed form applies for p <= 15 with
+# a window of kNDW single-slot loads per lane.
+KJC, WIDE_MIX_P = 16, 15
+KNDW = (2 * WIDE_MIX_P * KJC + 4 * ((2 * WIDE_MIX_P + 3) // 4) + 63) // 64
+
+
+def wide_geo(trans):
+    NSRC = 64 + KJC - 1 if trans else 64
+    Q, BLK = KJC // 4, KJC + 1
+    NSLOT = (NSRC + 3) // 4 * BLK
+    NZ4, NZ1 = (NSLOT + 63) // 64, (4 * NSLOT + 63) // 64
+    return dict(NSRC=NSRC, Q=Q, BLK=BLK, NZ4=NZ4, NZ1=NZ1, NZB=max(NZ4 * 256, NZ1 * 64))
+
+
+def wide_slot(G, f):
+    kb, r = divmod(f, G["BLK"])
+    rq = r if r < 4 * G["Q"] else 0
+    return r, min(4 * kb + rq // G["Q"], G["NSRC"] - 1), rq % G["Q"]
+
+
+def wide_forms(G, WS, n1, c0, jc):
+    P = (WS - 1) // 2
+    ref, mix = {}, {}
+    for m in range(G["NZ1"]):  # border form: single slots (zo_border)
+        for lane in range(64):
+            _, w, q = wide_slot(G, (lane + 64 * m) >> 2)
+            j = KJC * jc + 4 * q + ((lane + 64 * m) & 3)
+            col = (c0 + w) % n1
+            ref[64 * m + lane] = {(col, fold(j + shift0(col, n1, P), WS) if j < WS else 0)}
+    for m in range(G["NZ4"]):  # mixed form: pieces of columns not rotated
+        active = 0
+        for lane in range(64):
+            r, w, q = wide_slot(G, lane + 64 * m)
+            col = (c0 + w) % n1
+            if r >= 4 * G["Q"] or shift0(col, n1, P) == 0:
+                active += 1
+                for t in range(4):
+                    mix.setdefault(256 * m + 4 * lane + t, set()).add((col, KJC * jc + 4 * q + t))
+        assert active > 0
+    d = (n1 - P - c0 % n1) % n1
+    a0 = d if d < G["NSRC"] else 0
+    zb = min(a0 * KJC + 4 * (a0 >> 2), G["NZB"] - 64 * KNDW)
+    for i in range(KNDW):
+        for lane in range(64):
+            ps = zb + 64 * i + lane
+            kb, r = divmod(ps >> 2, G["BLK"])
+            w = 4 * kb + r // G["Q"]
+            j = KJC * jc + 4 * (r % G["Q"]) + (ps & 3)
+            col, e = 0, 0
+            if r < 4 * G["Q"] and w < G["NSRC"]:
+                col = (c0 + w) % n1
+                e = fold(j + shift0(col, n1, P), WS) if j < WS else 0
+            mix.setdefault(ps, set()).add((col, e))
+    return ref, mix
+
+
+@pytest.mark.parametrize("WS", [17, 19, 23, 27, 31])
+@pytest.mark.parametrize("trans", [False, True])
+def test_wide_mixed_border_staging_matches_single_slot_staging(WS, trans):
+    G = wide_geo(trans)
+    P = (WS - 1) // 2
+    assert P <= WIDE_MIX_P and 64 * KNDW <= G["NZB"]
+    njc = (WS + KJC - 1) // KJC
+    lo = G["NSRC"] + 2 * P
+    for n1 in sorted({lo, lo + 1, lo + 5, 128, 200, 512, 1000}):
+        edge = 2 * P + KJC  # set_wide's interior margin
+        tiles1 = (n1 + 63) // 64
+        fa = (edge + 63) // 64
+        fb = max(min((n1 - 64 - edge) // 64 + 1 if n1 - 64 - edge >= 0 else 0, tiles1), fa)
+        for t1 in [t for t in range(tiles1) if not fa <= t < fb]:
+            f1 = 64 * t1
+            for jc in range(njc):
+                c0 = f1 - (KJC * jc - P) - (KJC - 1) if trans else f1
+                ref, mix = wide_forms(G, WS, n1, c0, jc)
+                assert max(mix) < G["NZB"] and max(ref) < G["NZB"]
+                for w in range(G["NSRC"]):
+                    for jj in range(min(KJC, WS - KJC * jc)):  # slots read (the rest read as zero)
+                        pos = w * KJC + 4 * (w // 4) + jj
+                        assert mix.get(pos) == ref[pos], (n1, t1, jc, w, jj)
