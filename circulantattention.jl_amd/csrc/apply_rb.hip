@@ -983,7 +983,7 @@ __device__ __forceinline__ void apply2_body(const ApplyArgs &a, int pass, int t1
     constexpr int XW = kR + 2 * P;
     constexpr int AL = (NCOMP * (kHalo - P)) % 4;
     constexpr int KW4 = (NCOMP * XW + AL + 3) / 4;
-    static_assert(!ZM || (!FAST && XV && !SUMS), "mixed chunk loads are a border form");
+    static_assert(!ZM || (!FAST && (XV || SUMS)), "mixed chunk loads are a border form");
     constexpr int ND = ZM ? S::ND : 0;              // single-slot loads per lane (mixed form)
     constexpr int ZI = FAST ? S::NZ4 : ZM ? S::NZ4 + ND : S::NZ1;  // chunk loads per lane and row
     constexpr int XI = XV ? S::XL : 4 * S::XL;      // x loads per lane and step
@@ -1348,8 +1348,12 @@ __device__ __forceinline__ void apply2_tile(const ApplyArgs &a, int pass, int t1
         apply2_body<WS, NCOMP, TRANS, true, SUMS, true, CG, NX>(a, pass, t1, c2, b);
         return;
     }
-    if constexpr (!SUMS) {
-        if (xv && a.g.n1 >= S::NSRC + 2 * S::P) {
+    if (a.g.n1 >= S::NSRC + 2 * S::P) {
+        // (column sums stage no x)
+        if constexpr (SUMS) {
+            apply2_body<WS, NCOMP, TRANS, false, SUMS, false, CG, NX, true>(a, pass, t1, c2, b);
+            return;
+        } else if (xv) {
             apply2_body<WS, NCOMP, TRANS, false, SUMS, true, CG, NX, true>(a, pass, t1, c2, b);
             return;
         }
