@@ -142,11 +142,15 @@ int circatt_similarity(int kind, int dtype, int nsp, int64_t n1, int64_t n2, int
     pr.k = static_cast<const float *>(y);
     pr.nz = nzval;
     // 2D windows up to 15 wide: the row kernel (faster than the matrix-core
-    // kernel at every measured size); wider windows, 1D or 2D: the sub-row
-    // kernel; otherwise the matrix-core kernel
+    // kernel at every measured size); wider windows, 1D or 2D, and every
+    // Distance similarity the row kernel does not take: the sub-row kernel
+    // (both form -|x - y|^2 / 2 from the differences, as the reference does,
+    // where the matrix-core kernel expands it); otherwise the matrix-core
+    // kernel
     const bool rows_ok = sim_rows_supported(g, (int)C, ncomp, nb);
     const bool mfma_ok = fused_supported(MODE_SIM, pr);
-    if (!rows_ok && g.ws > 15 && sim_wide_supported(g, (int)C, ncomp, nb))
+    if (!rows_ok && (g.ws > 15 || kind == CIRCATT_DISTANCE) &&
+        sim_wide_supported(g, (int)C, ncomp, nb))
         return hip_result(launch_sim_wide(kind == CIRCATT_DISTANCE, ncomp, g, (int)C, nb, scale,
                                           pr.q, pr.k, nzval, as_stream(stream)),
                           "circatt_similarity");

@@ -346,6 +346,9 @@ void kernel2d(Args a) {
     int hslot[PPT];
     float nr0[NS], nr1[NS], nry[NS];
     float nlse = 0.f;
+    // Distance: lane c of the wave holds component c (mod NC) of the item's
+    // centre, k at the tile's first pixel
+    float nmu = 0.f;
 
     auto decode = [&](int item, int &unit, int &h0, int &w0) {
         const int ntiles = a.tiles_h * a.tiles_w;
@@ -432,6 +435,8 @@ void kernel2d(Args a) {
             if constexpr (MODE == BWDQ) nry[s] = bload(rsrc(a.y + uoff, ubytes), vo, so);
         }
         if constexpr (MODE == BWDQ) nlse = bload(rsrc(a.lse + (int64_t)unit * a.P, a.P * 4), rpix * 4, 0);
+        if constexpr (DIST)
+            nmu = bload(rsrc(a.k + uoff, ubytes), comp_off<CPLX, CL>(a, h0 + a.n1 * w0, lane & (NC - 1)) * 4, 0);
     };
 
     int k = 0;
@@ -450,6 +455,19 @@ void kernel2d(Args a) {
         const int64_t soff = (int64_t)unit * a.P;
         const float c2 = a.c2;
 
+        // Distance: both sides of the score product centred on mu (the
+        // expansion q.k - |k|^2 / 2 - |q|^2 / 2 of -|q - k|^2 / 2 then scales
+        // with the spread of the data, not its offset)
+        if constexpr (DIST) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const float mc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(nmu), c));
+#pragma unroll
+                for (int pp = 0; pp < PPT; ++pp) hv[pp][0][c] -= mc;
+            }
+#pragma unroll
+            for (int s = 0; s < NS; ++s) nr0[s] -= __shfl(nmu, 16 * (s >> 2) + 4 * g + (s & 3));
+        }
         __syncthreads();  // the previous item's LDS reads are done
 #pragma unroll
         for (int pp = 0; pp < PPT; ++pp) {

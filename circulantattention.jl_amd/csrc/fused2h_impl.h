@@ -413,6 +413,9 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
     // swap joins the halves
     float nh0[NT][4], nh1[NT][4], nry[NT][4];
     float nlse = 0.f;
+    // Distance: lane c of the wave holds component c (mod 16 NT) of the
+    // item's centre, k at the tile's first pixel
+    float nmu = 0.f;
 
     // register pixel of this lane in the tile at (h0, w0)
     auto regpix = [&](int h0, int w0, bool &rvalid, int &rpix) {
@@ -498,6 +501,9 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         }
         if constexpr (MODE == BWDQ)
             nlse = f2d::bload(f2d::rsrc(a.lse + (int64_t)unit * a.P, a.P * 4), rpix * 4, 0);
+        if constexpr (DIST)
+            nmu = f2d::bload(f2d::rsrc(a.k + uoff, ubytes),
+                             f2d::comp_off<CPLX, CL>(a, h0 + a.n1 * w0, lane & (16 * NT - 1)) * 4, 0);
     };
 
     int k = 0;
@@ -534,6 +540,22 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         const int64_t uoff = f2d::unit_base<CL>(a, unit);
         const int64_t soff = (int64_t)unit * a.P;
         const float c2 = a.c2;
+
+        // Distance: both sides of the score product centred on mu.  The
+        // expansion -|q - k|^2 / 2 = q.k - |k|^2 / 2 - |q|^2 / 2 (key bias
+        // and row term) is then formed from q - mu and k - mu, whose terms
+        // scale with the spread of the data rather than its offset; |q - k|
+        // and the gradient terms dS (k - q) are unchanged.
+        if constexpr (DIST) {
+#pragma unroll
+            for (int c = 0; c < 16 * NT; ++c)
+                h0v[c] -= __int_as_float(__builtin_amdgcn_readlane(__float_as_int(nmu), c));
+#pragma unroll
+            for (int h = 0; h < NT; ++h)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    nh0[h][t] -= __shfl(nmu, 16 * h + 8 * (g & 1) + 4 * (g >> 1) + t);
+        }
 
         // Largest magnitudes of what this item stages (tensors 0, 1) and, in
         // the key-centric pass, of the register v (the staged -D carries its

@@ -344,6 +344,10 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
     int hpx[PPT];
     float nr0[NS], nr1[NS], nry[NS];
     float nlse = 0.f;
+    // Distance: lane c of the wave holds component c (mod NC) of the item's
+    // centre, k at the tile's first pixel (0 past the real components); it
+    // is replaced by the next item's only after the item's last chunk is staged
+    float nmu = 0.f;
 
     // 2D tiles in bands of 8 tile rows, column by column within a band, so
     // that the items an XCD runs at once (consecutive item numbers) form a
@@ -411,6 +415,11 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
             if (MODE == MODE_BWDQ) nry[s] = cv ? a.y[uoff + comp_index(a, rpix, cc)] : 0.f;
         }
         if (MODE == MODE_BWDQ) nlse = a.lse[(int64_t)unit * a.g.P + rpix];
+        if constexpr (DIST) {
+            const int c = lane & (NC - 1);
+            const int64_t p0 = (int64_t)h0 + (int64_t)a.g.n1 * w0;
+            nmu = c < a.ncr ? a.k[uoff + comp_index(a, p0, c)] : 0.f;
+        }
     };
 
     // ---- per-item state ----
@@ -438,6 +447,21 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
         const int cr0 = chunk * chunk_rows;
         const int crn = min(chunk_rows, halo_h - cr0);
 
+        // Distance: both sides of the score product centred on mu (the
+        // expansion q.k - |k|^2 / 2 - |q|^2 / 2 of -|q - k|^2 / 2 then scales
+        // with the spread of the data, not its offset)
+        if constexpr (DIST) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const float mc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(nmu), c));
+#pragma unroll
+                for (int pp = 0; pp < PPT; ++pp) hv[pp][0][c] -= mc;
+            }
+            if (chunk == 0) {
+#pragma unroll
+                for (int s = 0; s < NS; ++s) nr0[s] -= __shfl(nmu, 16 * (s >> 2) + 4 * g + (s & 3));
+            }
+        }
         __syncthreads();  // the previous chunk's LDS reads are done
 #pragma unroll
         for (int pp = 0; pp < PPT; ++pp) {

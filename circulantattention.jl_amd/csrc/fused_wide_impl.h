@@ -106,15 +106,20 @@ __global__ __launch_bounds__(THREADS, 2) void wide_kernel(FArgs a) {
     const unsigned span1 = 2 * p1, span2 = 2 * p2;
     const float c2 = a.c2;
 
-    // components 16 t + 4 g + i (t < NT) from base c0 of the lane's pixel
-    auto load_reg = [&](auto NT_, auto &dst, const float *base, int64_t rpix, int c0) {
+    // components 16 t + 4 g + i (t < NT) from base c0 of the lane's pixel,
+    // minus those of mu when mu is given
+    auto load_reg = [&](auto NT_, auto &dst, const float *base, int64_t rpix, int c0,
+                        const float *mu = nullptr, int64_t p0 = 0) {
         constexpr int NT = decltype(NT_)::value;
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int comp = c0 + 16 * t + 4 * g + i;
-                dst[4 * t + i] = comp < a.ncr ? base[comp_index(a, rpix, min(comp, a.ncr - 1))] : 0.f;
+                const int64_t ci = comp_index(a, 0, min(comp, a.ncr - 1));
+                const bool ok = comp < a.ncr;
+                dst[4 * t + i] = ok ? base[comp_index(a, rpix, 0) + ci] : 0.f;
+                if (mu) dst[4 * t + i] -= ok ? mu[comp_index(a, p0, 0) + ci] : 0.f;
             }
     };
     using NTc = std::integral_constant<int, NTC>;
@@ -136,13 +141,19 @@ __global__ __launch_bounds__(THREADS, 2) void wide_kernel(FArgs a) {
         const float *R1 = (MODE == MODE_BWDKV ? a.v : a.dy) + uoff;
         const float *T0 = (MODE == MODE_BWDKV ? a.q : a.k) + uoff;  // staged side
         const float *T1 = (MODE == MODE_BWDKV ? a.dy : a.v) + uoff;
+        // Distance: q and k centred on mu = k at the tile's first pixel p0
+        // wherever they are loaded (the expansion q.k - |k|^2 / 2 - |q|^2 / 2
+        // of -|q - k|^2 / 2 then scales with the spread of the data, not its
+        // offset; |q - k| and the gradient terms dS (k - q) are unchanged)
+        const float *MU = DIST ? a.k + uoff : nullptr;
+        const int64_t p0 = (int64_t)h0 + (int64_t)a.g.n1 * w0;
 
         // per register pixel, over all components: |r0|^2 and, in the
         // query-centric pass, D = <dy, y>
         float qq = 0.f, dd = 0.f;
         for (int c0 = 0; c0 < a.ncr; c0 += CC) {
             float x[4 * NTC], y[4 * NTC];
-            load_reg(NTc{}, x, R0, rpix, c0);
+            load_reg(NTc{}, x, R0, rpix, c0, MU, p0);
 #pragma unroll
             for (int i = 0; i < 4 * NTC; ++i) qq += x[i] * x[i];
             if constexpr (MODE == MODE_BWDQ) {
@@ -179,8 +190,9 @@ __global__ __launch_bounds__(THREADS, 2) void wide_kernel(FArgs a) {
                         const int comp = c0 + c + i;
                         const bool ok = comp < a.ncr;
                         const int64_t idx = comp_index(a, gp, min(comp, a.ncr - 1));
-                        xv[i] = ok ? X[idx] : 0.f;
-                        if (Y) yv[i] = ok ? Y[idx] : 0.f;
+                        const float mu = ok && MU ? MU[comp_index(a, p0, comp)] : 0.f;
+                        xv[i] = ok ? X[idx] - (X == T0 ? mu : 0.f) : 0.f;
+                        if (Y) yv[i] = ok ? Y[idx] - (Y == T0 ? mu : 0.f) : 0.f;
                         n2 += xv[i] * xv[i];
                     }
                     *reinterpret_cast<f4 *>(&circatt_lds[slot * PS + c]) = xv;
@@ -232,7 +244,7 @@ __global__ __launch_bounds__(THREADS, 2) void wide_kernel(FArgs a) {
                     stage(r0, nrows, cc * CC, CC, T0, TWO ? T1 : nullptr, cc);
                     __syncthreads();
                     float x0[4 * NTC], x1[4 * NTC];
-                    load_reg(NTc{}, x0, R0, rpix, cc * CC);
+                    load_reg(NTc{}, x0, R0, rpix, cc * CC, MU, p0);
                     if (TWO) load_reg(NTc{}, x1, R1, rpix, cc * CC);
                     int bi = ib, bj = 0;
 #pragma unroll
@@ -357,7 +369,7 @@ __global__ __launch_bounds__(THREADS, 2) void wide_kernel(FArgs a) {
                 float xr[4 * NTO];
 #pragma unroll
                 for (int i = 0; i < 4 * NTO; ++i) xr[i] = 0.f;
-                if (DIST) load_reg(NTo{}, xr, R0, rpix, oc0);
+                if (DIST) load_reg(NTo{}, xr, R0, rpix, oc0, MU, p0);
                 if (rvalid) {
                     float *ob = MODE == MODE_BWDQ ? a.dq + uoff : a.dk + uoff;
 #pragma unroll

@@ -256,6 +256,79 @@ def attention_bwd(kind, q, k, v, dy, ws, nheads=1, precision="f64", A=None, dA_o
     return dq, dk, dv.reshape(v.shape)
 
 
+def attention_flash_f32(kind, q, k, v, dy, ws, nheads=1):
+    """(y, dq, dk, dv) of a Float32 flash-style restatement of the same
+    composition: the forward keeps only lse = m + log(sum exp(S - m)) per row
+    (Float32) and the backward recomputes S (rounded on its own) and
+    P = exp(S - lse) from it instead of reading the stored A, with D = <dy, y> for the softmax pullback
+    (dS = P o (dP - D), the identity of src/rrules.jl:42-56 for a real A).
+    S, the products and every reduction are Float32 (the oracle's float32
+    build), so its error against the float64 oracle is what a Float32
+    algorithm of this form incurs; the fused kernels are held to a multiple
+    of it where the scores are large."""
+    f = np.float32
+    dims = spatial_dims(q)
+    nsp, n1, n2, P, K = geometry(dims, ws)
+    qf, kf, vf, dyf = (_flat(a, nheads) for a in (q, k, v, dy))
+    nb, dh = qf.shape[0], qf.shape[1]
+    S = similarity(kind, qf, kf, dims, ws, 1.0 / math.sqrt(dh), "f32").reshape(nb, P, K)
+    m = S.max(axis=2, keepdims=True)
+    l = np.exp(S - m, dtype=f).sum(axis=2, keepdims=True, dtype=f)
+    lse = (m + np.log(l, dtype=f)).astype(f)
+    A = (np.exp(S - m, dtype=f) / l).astype(f).reshape(nb, P * K)
+    y = apply(A, vf, dims, ws, False, "f32")
+    # the backward's own evaluation of S: the channel sums in reverse order,
+    # so that it rounds independently of the forward's (as a backward pass
+    # that recomputes the scores in its own products does)
+    Sb = similarity(kind, qf[:, ::-1], kf[:, ::-1], dims, ws, 1.0 / math.sqrt(dh), "f32")
+    # (p <= 1: lse bounds every score, but the two roundings need not agree)
+    Pr = np.exp(np.minimum(Sb.reshape(nb, P, K) - lse, 0).astype(f), dtype=f).reshape(nb, P * K)
+    dA = similarity(DOT, dyf, vf, dims, ws, 1.0, "f32")
+    yd = (np.conj(y) if np.iscomplexobj(y) else y)
+    D = np.real(np.sum(dyf.astype(y.dtype) * yd, axis=1, dtype=y.dtype)).astype(f)  # (nb, P)
+    dS = (Pr.reshape(nb, P, K) * (dA.reshape(nb, P, K) - D[:, :, None])).astype(f)
+    dS = dS.reshape(nb, P * K)
+    dv = apply(Pr, dyf, dims, ws, True, "f32")
+    s4 = f(dh ** -0.25)
+    qt, kt = (qf * s4).astype(qf.dtype), (kf * s4).astype(kf.dtype)
+    dqt = apply(dS, kt, dims, ws, False, "f32")
+    dkt = apply(dS, qt, dims, ws, True, "f32")
+    if kind == DISTANCE:
+        dqt = dqt - rowsum(dS, P, K, "f32")[:, None, :] * qt
+        dkt = dkt - colsum(dS, dims, ws, "f32")[:, None, :] * kt
+    return (y.reshape(q.shape), (dqt * s4).reshape(q.shape), (dkt * s4).reshape(k.shape),
+            dv.reshape(v.shape))
+
+
+def attention_term_scales(kind, q, k, v, dy, ws, nheads=1):
+    """Float64 magnitudes of the terms each output sums, one scalar per
+    output (y, dq, dk, dv): max of A (x) |v|; of G (x) |k| (+ rowsum(G) |q|
+    for Distance) scaled like dq, with G = A o (|dA| + |D|) bounding |dS|; the
+    transposed forms for dk; A^T (x) |dy|.  A Float32 computation of an
+    output commits rounding errors of the order of the unit roundoff times
+    this scale, whatever the output's own size (a row whose softmax is one-hot
+    has dS = 0 exactly, but its terms are not small)."""
+    dims = spatial_dims(q)
+    nsp, n1, n2, P, K = geometry(dims, ws)
+    qf, kf, vf, dyf = (np.abs(_flat(a, nheads)).astype(np.float64) for a in (q, k, v, dy))
+    dh = qf.shape[1]
+    nb = qf.shape[0]
+    _, A = attention_fwd(kind, q, k, v, ws, nheads)
+    dA = similarity(DOT, _flat(dy, nheads), _flat(v, nheads), dims, ws, 1.0)
+    D = np.sum((A * dA).reshape(nb, P, K), axis=2)
+    G = (A.reshape(nb, P, K) * (np.abs(dA).reshape(nb, P, K) + np.abs(D)[:, :, None]))
+    G = G.reshape(nb, P * K)
+    s2 = 1.0 / math.sqrt(dh)
+    ty = apply(A, vf, dims, ws, False)
+    tq = apply(G, kf, dims, ws, False)
+    tk = apply(G, qf, dims, ws, True)
+    if kind == DISTANCE:
+        tq = tq + rowsum(G, P, K)[:, None, :] * qf
+        tk = tk + colsum(G, dims, ws)[:, None, :] * kf
+    tv = apply(A, dyf, dims, ws, True)
+    return float(ty.max()), float(tq.max() * s2), float(tk.max() * s2), float(tv.max())
+
+
 def attention_lse(kind, q, k, ws, nheads=1):
     """Per-row log-sum-exp of the scaled similarity, (nb, P), float64."""
     dims = spatial_dims(q)

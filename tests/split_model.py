@@ -33,6 +33,20 @@ whole image, which the halo covers for the windows used in the tests):
     is taken with q normalised per pixel and the score unscaled after the
     product (the kernels' slow path);
   * dy in the query-centric pass is normalised per pixel (same window rule).
+
+Distance similarity is formed by expansion, -|q-k|^2/2 = q.k - |k|^2/2 -
+|q|^2/2, with -|k|^2/2 a per-key bias in the score product's initial
+accumulator and -|q|^2/2 folded into the row's lse.  Each pass first centres
+both operands on one pixel of the item's keys (q - mu, k - mu; the kernels
+take mu = k at the tile's first pixel): |q-k|^2 is unchanged, but the
+expansion's terms then scale with the spread of the data instead of its
+offset.  Uncentred, the Float32 roundings of the bias, of the accumulated
+score and of the stored lse (``f32acc``, modelled as one rounding each) and
+the halves' 2^-22 per operand grow with |q||k|, which at q, k = N(0,1) + 10
+already exceeds the tolerances.  ``centre_px`` gives the centre pixel of the
+forward, query-centric and key-centric passes (different per pass, as in the
+kernels, whose tiles differ: the stored lse is the centre-independent
+log-sum-exp of the true scores); None models the kernels before centring.
 """
 from __future__ import annotations
 
@@ -114,87 +128,137 @@ def _pixel_shifts(x, keep=True):
     return np.array([shift_of(np.max(np.abs(x[:, r])), keep) for r in range(x.shape[1])])
 
 
-def _scores(qs, kx, c2, sk, cols, init, slow_ok=True):
+def _scores(qs, kx, c2, sk, cols, init, slow_ok=True, lim=F16_LIMIT, slow_sign=1):
     """Scores in log2 units of register operand qs (raw) against staged kx
-    (already shifted by sk): fast path q' = q c2 2^-sk, slow path when |q'|
-    would reach 2^15."""
+    (already shifted by sk).  Fast path q' = q c2 2^-sk; a pixel whose |q'|
+    reaches lim takes the slow path: q c2 normalised per pixel to [4, 8) and
+    the product unscaled by 2^-(shift + sk) (``slow_sign`` = -1 flips that
+    unscale, a planted mistake).  Returns (scores, per-pixel slow flags)."""
     qp = f32(qs * c2 * 2.0 ** -sk)
-    if not slow_ok or np.max(np.abs(qp)) < F16_LIMIT:
-        return score(qp, kx, cols) + init, False
+    fast = score(qp, kx, cols) + init
+    big = np.max(np.abs(qp), axis=0) >= lim if slow_ok else np.zeros(qs.shape[1], bool)
+    if not big.any():
+        return fast, big
     sq = _pixel_shifts(qs * c2, keep=False)
     qn = f32(ldexp(qs * c2, sq[None, :]))
-    return ldexp(score(qn, kx, cols), -(sq[:, None] + sk)) + init, True
+    slow = ldexp(score(qn, kx, cols), -slow_sign * (sq[:, None] + sk)) + init
+    return np.where(big[:, None], slow, fast), big
 
 
-def fused_fwd(kind, q, k, v, ws, dims, scaled=True):
+def bwd_lim(kx):
+    """The backward passes' slow-walk threshold on |q'|: 2^15, or lower so
+    that scores stay below 2^20 (|kx| < 2^e gives 2^(16 - e))."""
+    m = float(np.max(np.abs(kx)))
+    e = math.frexp(m)[1] if m > 0 else -126
+    return min(F16_LIMIT, 2.0 ** (16 - e))
+
+
+def _centred(x, mu):
+    """x - mu per component, rounded to float32 as the kernels subtract."""
+    return f32(x.astype(np.float32) - mu.astype(np.float32)[:, None])
+
+
+def _r32(x, on):
+    return np.asarray(x, np.float32).astype(np.float64) if on else np.asarray(x, np.float64)
+
+
+def fused_fwd(kind, q, k, v, ws, dims, scaled=True, centre_px=(0, 1, 2), f32acc=True,
+              slow_sign=1):
     """y (dh, P) and lse (P,) of one unit; q, k, v: (dh, P) float32 values."""
     dh, P = q.shape
     cols = window_cols(dims, ws)
     scale = 1.0 / math.sqrt(dh)
     c2 = scale * LOG2E
+    if kind == 1 and centre_px is not None:
+        mu = k[:, centre_px[0]].copy()
+        q, k = _centred(q, mu), _centred(k, mu)
     sk = shift_of(np.max(np.abs(k))) if scaled else 0
     sv = shift_of(np.max(np.abs(v))) if scaled else 0
     kx, vx = f32(ldexp(k, sk)), f32(ldexp(v, sv))
-    kb = -0.5 * c2 * np.sum(k.astype(np.float64) ** 2, axis=0) if kind == 1 else np.zeros(P)
-    s, _ = _scores(q, kx, c2, sk, cols, kb[cols], slow_ok=scaled)
+    if kind == 1:
+        n2 = _r32(np.sum(k.astype(np.float64) ** 2, axis=0), f32acc)
+        kb = _r32(-0.5 * c2 * n2, f32acc)
+    else:
+        kb = np.zeros(P)
+    s, _ = _scores(q, kx, c2, sk, cols, kb[cols], slow_ok=scaled, slow_sign=slow_sign)
+    s = _r32(s, f32acc)
     m = s.max(axis=1, keepdims=True)
     p = np.exp2(s - m)
     l = p.sum(axis=1)
     y = ldexp(apply_rows(vx, p, cols) / l[None, :], -sv)
-    lse = (m[:, 0] + np.log2(l)) * LN2
+    lse = _r32((m[:, 0] + np.log2(l)) * LN2, f32acc)
     if kind == 1:
-        lse = lse - 0.5 * scale * np.sum(q.astype(np.float64) ** 2, axis=0)
-    return y, lse
+        sq = _r32(np.sum(q.astype(np.float64) ** 2, axis=0), f32acc)
+        lse = lse - _r32(0.5 * scale * sq, f32acc)
+    return y, _r32(lse, f32acc)
 
 
-def fused_bwd(kind, q, k, v, y, dy, lse, ws, dims, scaled=True):
+def fused_bwd(kind, q, k, v, y, dy, lse, ws, dims, scaled=True, centre_px=(0, 1, 2),
+              f32acc=True, slow_sign=1):
     """(dq, dk, dv) of one unit as the two backward passes compute them."""
     dh, P = q.shape
     cols = window_cols(dims, ws)
     scale = 1.0 / math.sqrt(dh)
     c2 = scale * LOG2E
-    qd, kd = q.astype(np.float64), k.astype(np.float64)
     D = np.sum(dy.astype(np.float64) * y.astype(np.float64), axis=0)
-    q2, k2 = np.sum(qd ** 2, axis=0), np.sum(kd ** 2, axis=0)
     dist = kind == 1
+    lse = np.asarray(lse, np.float64)
+
+    def centred(px):
+        if not dist or centre_px is None:
+            return q, k
+        mu = k[:, px].copy()
+        return _centred(q, mu), _centred(k, mu)
+
+    def norms(qc, kc):
+        return (_r32(np.sum(qc.astype(np.float64) ** 2, axis=0), f32acc),
+                _r32(np.sum(kc.astype(np.float64) ** 2, axis=0), f32acc))
 
     # query-centric pass: staged k, v; registers q, dy
-    sk = shift_of(np.max(np.abs(k))) if scaled else 0
+    qc, kc = centred(centre_px[1] if centre_px is not None else 0)
+    q2, k2 = norms(qc, kc)
+    sk = shift_of(np.max(np.abs(kc))) if scaled else 0
     sv = shift_of(np.max(np.abs(v))) if scaled else 0
     sd = _pixel_shifts(dy) if scaled else np.zeros(P, int)
-    kx, vx = f32(ldexp(k, sk)), f32(ldexp(v, sv))
+    kx, vx = f32(ldexp(kc, sk)), f32(ldexp(v, sv))
     dyx = f32(ldexp(dy, sd[None, :]))
-    init = (-lse * LOG2E)[:, None] + (np.zeros((P, 1)) if not dist else
-                                      (-0.5 * c2 * q2)[:, None] - 0.5 * c2 * k2[cols])
-    s, _ = _scores(q, kx, c2, sk, cols, init, slow_ok=scaled)
-    p = np.exp2(s)
+    rowt = _r32(-lse * LOG2E - (0.5 * c2 * q2 if dist else 0.0), f32acc)
+    init = rowt[:, None] + (_r32(-0.5 * c2 * k2, f32acc)[cols] if dist else 0.0)
+    s, slow = _scores(qc, kx, c2, sk, cols, init, slow_ok=scaled, lim=bwd_lim(kx),
+                      slow_sign=slow_sign)
+    s = _r32(s, f32acc)
+    p = np.exp2(np.where(slow[:, None], np.minimum(s, 0.0), s))
     dp = score(dyx, vx, cols) - ldexp(D, sd + sv)[:, None]
     ds = f32(p * dp)
     acc = apply_rows(kx, ds, cols)
     dq = ldexp(acc, -(sd + sv + sk)[None, :])
     if dist:
-        dq = dq - ldexp(ds.astype(np.float64).sum(axis=1), -(sd + sv))[None, :] * qd
+        dq = dq - ldexp(ds.astype(np.float64).sum(axis=1), -(sd + sv))[None, :] * qc
     dq = dq * scale
 
     # key-centric pass: staged q, dy; registers k, v (v shifted as a whole)
-    sq = shift_of(np.max(np.abs(q))) if scaled else 0
+    qc, kc = centred(centre_px[2] if centre_px is not None else 0)
+    q2, k2 = norms(qc, kc)
+    sq = shift_of(np.max(np.abs(qc))) if scaled else 0
     sd2 = shift_of(np.max(np.abs(dy))) if scaled else 0
     sv2 = shift_of(np.max(np.abs(v))) if scaled else 0
-    qx, dyx2 = f32(ldexp(q, sq)), f32(ldexp(dy, sd2))
+    qx, dyx2 = f32(ldexp(qc, sq)), f32(ldexp(dy, sd2))
     vr = f32(ldexp(v, sv2))
     # the window is symmetric: the queries whose windows hold key c are the
     # keys of c's own window, cols[c]
-    init = (-lse * LOG2E)[cols] + (0.0 if not dist else
-                                   -0.5 * c2 * q2[cols] - 0.5 * c2 * k2[:, None])
-    s, _ = _scores(k, qx, c2, sq, cols, init, slow_ok=scaled)
-    p = np.exp2(s)
+    colt = _r32(-lse * LOG2E - (0.5 * c2 * q2 if dist else 0.0), f32acc)
+    init = colt[cols] + (_r32(-0.5 * c2 * k2, f32acc)[:, None] if dist else 0.0)
+    s, slow = _scores(kc, qx, c2, sq, cols, init, slow_ok=scaled, lim=bwd_lim(qx),
+                      slow_sign=slow_sign)
+    s = _r32(s, f32acc)
+    p = np.exp2(np.where(slow[:, None], np.minimum(s, 0.0), s))
     dp = score(vr, dyx2, cols) - ldexp(D, sv2 + sd2)[cols]
     ds = f32(p * dp)
     acc0 = apply_rows(qx, ds, cols)
     acc1 = apply_rows(dyx2, f32(p), cols)
     dk = ldexp(acc0, -(sv2 + sd2 + sq))
     if dist:
-        dk = dk - ldexp(ds.astype(np.float64).sum(axis=1), -(sv2 + sd2))[None, :] * kd
+        dk = dk - ldexp(ds.astype(np.float64).sum(axis=1), -(sv2 + sd2))[None, :] * kc
     dk = dk * scale
     dv = ldexp(acc1, -sd2)
     return dq, dk, dv

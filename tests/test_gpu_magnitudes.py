@@ -10,10 +10,15 @@ Large q and k make the scores large, and a Float32 computation of the softmax
 is then ill-conditioned whatever the arithmetic: the reference's own Float32
 algorithm (the oracle's float32 build, unfused, A materialised) misses 1e-4
 on dq, dk from q, k ~ 1e2 on, and a flash-style backward, which recomputes
-P = exp(S - lse) from the stored lse, loses more.  For q, k scaled past 1 the
-bar is therefore the reference's own Float32 error (x 8) where that is
-larger than the tolerance, and for q, k >= 1e2 the gradients are only
-required to be finite.
+P = exp(S - lse) from the stored lse, loses more.  For q, k scaled past 1
+every output is held to the large-score bar of tests/large_scores.py: 8x the
+error of a Float32 flash-style restatement, or of the unit roundoff on the
+magnitude of the terms the output sums, whichever is larger.  From about
+q, k x 1e2 the split-half backward passes switch waves to their slow walk
+(q normalised per pixel, each score unscaled by 2^-eu after its product;
+at x 1e2 only the waves holding the largest values), and from x 1e4 the
+forward too; a slow walk with a wrong unscale fails that bar (shown on the
+CPU model by tests/test_split_model.py).
 """
 import math
 
@@ -21,6 +26,7 @@ import numpy as np
 import pytest
 
 from conftest import TOL_FWD, TOL_GRAD, rel_err
+from large_scores import abs_err, flash_bounds
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -113,19 +119,14 @@ def _across_magnitudes(ca, cuda, case, which, mag, cplx, kind, seed0):
     y, dq, dk, dv = fused(ca, cuda, kind, q, k, v, dy, ws, nh)
     yr, _ = O.attention_fwd(kind, *(f64(a) for a in (q, k, v)), ws, nh)
     gr = O.attention_bwd(kind, *(f64(a) for a in (q, k, v, dy)), ws, nh)
-    tol_y, tol_g = TOL_FWD, TOL_GRAD
     if sq > 1:
-        # the reference's own Float32 algorithm against the float64 oracle
-        y32, A32 = O.attention_fwd(kind, q, k, v, ws, nh, precision="f32")
-        tol_y = max(tol_y, 8 * rel_err(y32, yr))
-        if sq < 1e2:
-            g32 = O.attention_bwd(kind, q, k, v, dy, ws, nh, precision="f32", A=A32)
-            tol_g = max(tol_g, 8 * max(rel_err(a, b) for a, b in zip(g32, gr)))
-    assert rel_err(y, yr) < tol_y
+        bars = flash_bounds(kind, q, k, v, dy, ws, nh, [yr, *gr])
+        for name, o, r, b in zip(("y", "dq", "dk", "dv"), (y, dq, dk, dv), (yr, *gr), bars):
+            assert abs_err(o, r) <= b, (name, abs_err(o, r), b)
+        return
+    assert rel_err(y, yr) < TOL_FWD
     for name, g, r in zip(("dq", "dk", "dv"), (dq, dk, dv), gr):
-        assert np.all(np.isfinite(g)), name
-        if sq < 1e2:
-            assert rel_err(g, r) < tol_g, (name, rel_err(g, r), tol_g)
+        assert rel_err(g, r) < TOL_GRAD, (name, rel_err(g, r))
 
 
 @pytest.mark.parametrize("kind", [0, 1])

@@ -100,3 +100,73 @@ def test_scaled_split_within_tolerance(dims, ws, which, mag, kind):
     e = model_errors(kind, dims, ws, q, k, v, dy, scaled=True)
     assert e[0] < TOL_FWD, e
     assert max(e[1:]) < TOL_GRAD, e
+
+
+def offset_inputs(seed, dims, dh, c):
+    rng = np.random.default_rng(seed)
+    P = int(np.prod(dims))
+    q, k = ((rng.standard_normal((dh, P)) + c).astype(np.float32) for _ in range(2))
+    v, dy = (rng.standard_normal((dh, P)).astype(np.float32) for _ in range(2))
+    return q, k, v, dy
+
+
+def model_errors_c(kind, dims, ws, q, k, v, dy, **kw):
+    dh, P = q.shape
+    shape = (1, dh, *reversed(dims))
+    qo, ko, vo, dyo = (a.astype(np.float64).reshape(shape) for a in (q, k, v, dy))
+    yr, _ = O.attention_fwd(kind, qo, ko, vo, ws)
+    gr = O.attention_bwd(kind, qo, ko, vo, dyo, ws)
+    y, lse = M.fused_fwd(kind, q, k, v, ws, dims, True, **kw)
+    g = M.fused_bwd(kind, q, k, v, y.astype(np.float32), dy, lse, ws, dims, True, **kw)
+    return [rel_err(y, yr.reshape(dh, P))] + [rel_err(a, b.reshape(dh, P)) for a, b in zip(g, gr)]
+
+
+@pytest.mark.parametrize("dims,ws", [((16, 16), 15), ((12, 10), 5), ((9, 11), 3)])
+@pytest.mark.parametrize("c", [3.0, 10.0, 30.0])
+def test_distance_centred_on_offset_inputs(dims, ws, c):
+    """Distance similarity is translation-invariant (src/similarity.jl:55-78
+    forms -|x - y|^2 / 2 directly).  The kernels' expansion q.k - |k|^2/2
+    - |q|^2/2 is not: on q, k = N(0,1) + c its Float32 terms grow with c^2.
+    Centred on one key pixel per pass (a different one in each pass) the
+    expansion meets the usual bar at every offset; uncentred it is at least
+    five times worse from c = 10 (near the forward bar there) and misses the
+    gradient bar at c = 30."""
+    q, k, v, dy = offset_inputs(60 + ws + int(c), dims, 16, c)
+    e = model_errors_c(1, dims, ws, q, k, v, dy)
+    assert e[0] < TOL_FWD and max(e[1:]) < TOL_GRAD, e
+    if c >= 10:
+        e0 = model_errors_c(1, dims, ws, q, k, v, dy, centre_px=None)
+        assert min(a / b for a, b in zip(e0, e)) > 5, (e0, e)
+        if c >= 30:
+            assert max(e0[1:]) > TOL_GRAD, e0
+
+
+@pytest.mark.parametrize("dims,ws", [((16, 16), 15), ((12, 10), 5)])
+@pytest.mark.parametrize("kind,mag", [(0, 3e2), (0, 1e3), (0, 1e4), (1, 1e2), (1, 1e3), (1, 1e4)])
+def test_slow_walk_within_flash_bound(dims, ws, kind, mag):
+    """q, k scaled so far that the split-half walks take their slow form
+    (q normalised per pixel, every score unscaled by 2^-eu after its
+    product): the modelled kernels stay within the large-score bar of
+    tests/large_scores.py for y, dq, dk and dv, and the same model with the
+    unscale's sign flipped (a planted mistake) fails it."""
+    from large_scores import abs_err, flash_bounds
+    rng = np.random.default_rng(70 + ws + kind)
+    P = int(np.prod(dims))
+    q, k, v, dy = (rng.standard_normal((16, P)).astype(np.float32) for _ in range(4))
+    q, k = q * np.float32(mag), k * np.float32(mag)
+    shape = (1, 16, *reversed(dims))
+    qo, ko, vo, dyo = (a.reshape(shape) for a in (q, k, v, dy))
+    yr, _ = O.attention_fwd(kind, *(a.astype(np.float64) for a in (qo, ko, vo)), ws)
+    gr = O.attention_bwd(kind, *(a.astype(np.float64) for a in (qo, ko, vo, dyo)), ws)
+    refs = [yr.reshape(16, P)] + [g.reshape(16, P) for g in gr]
+    bars = flash_bounds(kind, qo, ko, vo, dyo, ws, 1, refs)
+    with np.errstate(all="ignore"):
+        for sign in (1, -1):
+            y, lse = M.fused_fwd(kind, q, k, v, ws, dims, True, slow_sign=sign)
+            g = M.fused_bwd(kind, q, k, v, y.astype(np.float32), dy, lse, ws, dims, True,
+                            slow_sign=sign)
+            ok = [abs_err(a, r) <= b for a, r, b in zip([y, *g], refs, bars)]
+            if sign == 1:
+                assert all(ok), ([abs_err(a, r) / b for a, r, b in zip([y, *g], refs, bars)])
+            else:
+                assert not all(ok)
