@@ -203,11 +203,14 @@ def spatial_dims(x):
     return tuple(reversed(x.shape[2:]))
 
 
-def attention_fwd(kind, q, k, v, ws, nheads=1, precision="f64"):
+def attention_fwd(kind, q, k, v, ws, nheads=1, precision="f64", trans=False):
     """y, A_nz of circulant_attention (src/attention.jl:19-26) or, for
     nheads > 1, of circulant_mh_attention's per-head computation
     (src/attention.jl:38-42).  tau = sqrt(channels per head); q and k are each
-    divided by sqrt(tau), so S(q,k) is scaled by 1/sqrt(dh)."""
+    divided by sqrt(tau), so S(q,k) is scaled by 1/sqrt(dh).  trans: y is the
+    transposed apply Aᵀ ⊗ v of the same adjacency
+    (circulant_transposed_attention / circulant_mh_transposed_attention,
+    src/attention.jl:72-80, 98-103)."""
     dims = spatial_dims(q)
     nsp, n1, n2, P, K = geometry(dims, ws)
     qf, kf, vf = (_flat(a, nheads) for a in (q, k, v))
@@ -215,11 +218,12 @@ def attention_fwd(kind, q, k, v, ws, nheads=1, precision="f64"):
     scale = 1.0 / math.sqrt(dh)
     S = similarity(kind, qf, kf, dims, ws, scale, precision)
     A = softmax(S, K, precision)
-    y = apply(A, vf, dims, ws, False, precision)
+    y = apply(A, vf, dims, ws, trans, precision)
     return y.reshape(q.shape), A
 
 
-def attention_bwd(kind, q, k, v, dy, ws, nheads=1, precision="f64", A=None, dA_out=None):
+def attention_bwd(kind, q, k, v, dy, ws, nheads=1, precision="f64", A=None, dA_out=None,
+                  trans=False):
     """(dq, dk, dv) for the composition adjacency -> ⊗ (the path
     test/grad.jl:17-21 differentiates) with the rrules of src/rrules.jl:
       ⊗ (:58-72):        dA = sim_Dot(dy, v), dv = Aᵀ ⊠ dy
@@ -230,6 +234,8 @@ def attention_bwd(kind, q, k, v, dy, ws, nheads=1, precision="f64", A=None, dA_o
       Dot (:18-32):      dq̃ = dS ⊠ k̃, dk̃ = dSᵀ ⊠ q̃
       Distance (:1-16):  dq̃ = dS ⊠ k̃ - rowsum(dS)∘q̃, dk̃ = dSᵀ ⊠ q̃ - colsum(dS)∘k̃
       q̃ = q/sqrt(tau) (src/attention.jl:21):  dq = dq̃/sqrt(tau), same for k.
+    trans (y = Aᵀ ⊗ v, the rrule of src/rrules.jl:74-88):
+                         dA = sim_Dot(v, dy), dv = A ⊠ dy.
     """
     dims = spatial_dims(q)
     nsp, n1, n2, P, K = geometry(dims, ws)
@@ -238,10 +244,13 @@ def attention_bwd(kind, q, k, v, dy, ws, nheads=1, precision="f64", A=None, dA_o
     s4 = dh ** -0.25  # 1/sqrt(tau), tau = sqrt(dh)
     if A is None:
         _, A = attention_fwd(kind, q, k, v, ws, nheads, precision)
-    dA = similarity(DOT, dyf, vf, dims, ws, 1.0, precision)
+    if trans:
+        dA = similarity(DOT, vf, dyf, dims, ws, 1.0, precision)
+    else:
+        dA = similarity(DOT, dyf, vf, dims, ws, 1.0, precision)
     if dA_out is not None:
         dA = dA + np.asarray(dA_out, dA.dtype).reshape(dA.shape)
-    dv = apply(A, dyf, dims, ws, True, precision)
+    dv = apply(A, dyf, dims, ws, not trans, precision)
     dS = softmax_bwd(A, dA, K, precision)
     qt, kt = qf * s4, kf * s4
     dqt = apply(dS, kt, dims, ws, False, precision)

@@ -416,3 +416,86 @@ def test_dot_and_sums_carry_gradients(ca, cuda):
     w = torch.arange(B * nh, dtype=torch.float32, device=cuda).reshape(B, nh, 1, 1)
     (A.sum((1, 2)) * w).sum().backward()
     assert torch.equal(ta.grad, w.expand(B, nh, 48, 9))
+
+
+# ---------------------------------------------------------------------------
+# the transposed apply and its rrule
+# ---------------------------------------------------------------------------
+def _f64(a):
+    return a.astype(np.complex128 if np.iscomplexobj(a) else np.float64)
+
+
+@pytest.mark.parametrize("mh", [False, True], ids=["transposed", "mh_transposed"])
+@pytest.mark.parametrize("nsp", [1, 2])
+@pytest.mark.parametrize("cplx", [False, True])
+@pytest.mark.parametrize("kind", [0, 1])
+def test_transposed_attention_gradients(ca, cuda, mh, nsp, cplx, kind):
+    """y = Aᵀ ⊗ v for A = circulant_(mh_)adjacency(simfun, q/sqrt(tau),
+    k/sqrt(tau)): circulant_transposed_attention (src/attention.jl:72-80) and
+    circulant_mh_transposed_attention (:98-103), differentiated through the
+    transposed apply's rrule (src/rrules.jl:74-88: dA = sim_Dot(v, dy),
+    dv = A ⊠ dy), the softmax and the similarity, against the oracle's
+    composition (pinned by finite differences in tests/test_oracle.py)."""
+    dims = (14,) if nsp == 1 else (12, 10)
+    ws, C, B = 5, 8, 2
+    nh = 2 if mh else 1
+    shape = (B, C, *reversed(dims))
+    seed = 990 + 10 * kind + 20 * nsp + (5 if cplx else 0) + (40 if mh else 0)
+    q, k, v, dy = (seeded(seed + i, shape, cplx) for i in range(4))
+    tq, tk, tv = (torch.from_numpy(a).to(cuda).requires_grad_(True) for a in (q, k, v))
+    s4 = (C // nh) ** -0.25  # q, k / sqrt(tau), tau = sqrt(channels per head)
+    simfun = ca.DotSimilarity() if kind == 0 else ca.DistanceSimilarity()
+    if mh:
+        A = ca.circulant_mh_adjacency(simfun, tq * s4, tk * s4, ws, nh)
+        y = ca.circulant_mh_transposed_attention(A, tv)
+    else:
+        A = ca.circulant_adjacency(simfun, tq * s4, tk * s4, ws)
+        y = ca.circulant_transposed_attention(A, tv)
+    td = torch.from_numpy(dy).to(cuda)
+    loss = (y * td.conj()).real.sum() if cplx else (y * td).sum()
+    loss.backward()
+    yr, _ = O.attention_fwd(kind, *(_f64(a) for a in (q, k, v)), ws, nh, trans=True)
+    gr = O.attention_bwd(kind, *(_f64(a) for a in (q, k, v, dy)), ws, nh, trans=True)
+    assert rel_err(y.detach().cpu().numpy(), yr) < TOL_FWD
+    for name, t, r in zip(("dq", "dk", "dv"), (tq, tk, tv), gr):
+        assert rel_err(t.grad.cpu().numpy(), r) < TOL_GRAD, name
+
+
+def test_cfg5_composition_full_size(ca, cuda):
+    """BASELINE cfg5 / README.md:128-134 at full size (320x320, 32 complex
+    channels, B = 2, 2 heads, ws = 11): y, A = mh attention; u, B = mh
+    attention of (y, y, y); C = A + m*B with m of Julia size (1, 1, 2, 2);
+    w = C ⨷ u.  A, B, C and w against the oracle (the float64 C restatement,
+    at full size), rows of A and B summing to one, and linearity of ⨷:
+    C ⨷ u = A ⨷ u + m (B ⨷ u)."""
+    dims, ws, Cc, Bb, nh = (320, 320), 11, 32, 2, 2
+    P, K = 320 * 320, 121
+    shape = (Bb, Cc, *reversed(dims))
+    q, k, v = (seeded(1005 + i, shape, True) for i in range(3))
+    m = seeded(1008, (Bb, nh, 1, 1))
+    tq, tk, tv = (torch.from_numpy(a).to(cuda) for a in (q, k, v))
+    y, A = ca.circulant_mh_attention(ca.DotSimilarity(), tq, tk, tv, ws, nh)
+    u, Bm = ca.circulant_mh_attention(ca.DotSimilarity(), y, y, y, ws, nh)
+    tm = torch.from_numpy(m).to(cuda)
+    Cm = A + ca.scale(tm, Bm)
+    w = ca.Otimes(Cm, u)
+    # rows of the two adjacencies sum to one; linearity of the apply
+    for X in (A, Bm):
+        assert torch.max(torch.abs(X.sum(2) - 1)).item() < 1e-5
+    lin = ca.Otimes(A, u) + ca.Otimes(ca.scale(tm, Bm), u)
+    assert rel_err(w.cpu().numpy(), lin.cpu().numpy()) < TOL_FWD
+    # against the oracle, step by step
+    yr, Ar = O.attention_fwd(0, *(_f64(a) for a in (q, k, v)), ws, nh)
+    assert rel_err(A.nzval.cpu().numpy().reshape(Ar.shape), Ar) < TOL_FWD
+    assert rel_err(y.cpu().numpy(), yr) < TOL_FWD
+    yh = _f64(y.cpu().numpy())
+    ur, Br = O.attention_fwd(0, yh, yh, yh, ws, nh)
+    assert rel_err(Bm.nzval.cpu().numpy().reshape(Br.shape), Br) < TOL_FWD
+    assert rel_err(u.cpu().numpy(), ur) < TOL_FWD
+    Cr = O.axpby(np.ones(Bb * nh), Ar, m.reshape(-1), Br)
+    del Ar, Br
+    assert rel_err(Cm.nzval.cpu().numpy().reshape(Cr.shape), Cr) < TOL_FWD
+    uh = _f64(u.cpu().numpy()).reshape(Bb * nh, Cc // nh, P)
+    wr = O.apply(Cr, uh, dims, ws).reshape(shape)
+    assert rel_err(w.cpu().numpy(), wr) < TOL_FWD
+    assert Cm.nzval.numel() == Bb * nh * P * K

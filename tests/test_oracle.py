@@ -245,9 +245,9 @@ def test_attention_fwd_dense(dims, ws, nheads, cplx, kind):
 # backward vs central finite differences
 # ---------------------------------------------------------------------------
 
-def fd_grads(kind, q, k, v, dy, ws, nheads, h=1e-6):
+def fd_grads(kind, q, k, v, dy, ws, nheads, h=1e-6, trans=False):
     def loss(qq, kk, vv):
-        y, _ = O.attention_fwd(kind, qq, kk, vv, ws, nheads)
+        y, _ = O.attention_fwd(kind, qq, kk, vv, ws, nheads, trans=trans)
         return np.sum(np.real(y * np.conj(dy)))
 
     grads = []
@@ -284,6 +284,26 @@ def test_attention_bwd_fd(dims, ws, nheads, cplx, kind):
     fq, fk, fv = fd_grads(kind, q, k, v, dy, ws, nheads)
     for got, ref in ((dq, fq), (dk, fk), (dv, fv)):
         np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("dims,ws,nheads", [((4, 3), 3, 1), ((5,), 3, 2), ((3, 3), 5, 2)])
+@pytest.mark.parametrize("cplx", [False, True])
+@pytest.mark.parametrize("kind", [O.DOT, O.DISTANCE])
+def test_transposed_attention_bwd_fd(dims, ws, nheads, cplx, kind):
+    """y = Aᵀ ⊗ v of the adjacency (circulant_transposed_attention and its
+    multi-head form, src/attention.jl:72-80, 98-103): the rrule of
+    src/rrules.jl:74-88 (dA = sim_Dot(v, dy), dv = A ⊠ dy) composed with the
+    softmax and similarity pullbacks, against central finite differences; the
+    plain apply's pullback (dA = sim_Dot(dy, v)) in its place fails."""
+    B, C = 2, 2 * nheads
+    shape = (B, C, *reversed(dims))
+    q, k, v, dy = (rand_signal(shape, cplx) for _ in range(4))
+    got = O.attention_bwd(kind, q, k, v, dy, ws, nheads, trans=True)
+    ref = fd_grads(kind, q, k, v, dy, ws, nheads, trans=True)
+    for a, b in zip(got, ref):
+        np.testing.assert_allclose(a, b, rtol=1e-6, atol=1e-7)
+    wrong = O.attention_bwd(kind, q, k, v, dy, ws, nheads, trans=False)
+    assert max(np.max(np.abs(a - b)) for a, b in zip(wrong, ref)) > 1e-3
 
 
 @pytest.mark.parametrize("dims,ws,nheads", [((4, 3), 3, 1), ((6,), 5, 2)])
