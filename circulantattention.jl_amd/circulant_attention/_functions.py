@@ -86,6 +86,117 @@ def axpby_raw(alpha, X, beta=None, Y=None, nb=1):
     return Z
 
 
+def fill_raw(t, value):
+    """t[...] = value (circatt_fill); t contiguous float32."""
+    L.check(L.lib.circatt_fill(ptr(t), t.numel(), float(value), stream_ptr(t.device)),
+            "circatt_fill")
+    return t
+
+
+def copy_blocks_raw(dst, src, block, ninner, dsi, ssi, nouter, dso, sso, dst_off=0, src_off=0):
+    """Strided device block copy (circatt_copy_blocks); sizes, strides and
+    offsets in bytes."""
+    L.check(L.lib.circatt_copy_blocks(ctypes.c_void_p(dst.data_ptr() + dst_off),
+                                      ctypes.c_void_p(src.data_ptr() + src_off), block, ninner,
+                                      dsi, ssi, nouter, dso, sso, stream_ptr(dst.device)),
+            "circatt_copy_blocks")
+    return dst
+
+
+def replicate_raw(x, inner, r, outer):
+    """x viewed as (outer, inner) -> (outer, r, inner): every inner block
+    repeated r times (repeat or broadcast over one batch dim)."""
+    x = _c(x)
+    out = torch.empty((outer, r, inner), dtype=x.dtype, device=x.device)
+    es = x.element_size()
+    return copy_blocks_raw(out, x, inner * es, r, inner * es, 0, outer, r * inner * es, inner * es)
+
+
+def sum_middle_raw(x, inner, nsum, outer):
+    """x viewed as (outer, nsum, inner) -> (outer, inner), summed over nsum
+    (circatt_sum_middle, double accumulation in order)."""
+    x = _c(x)
+    out = torch.empty((outer, inner), dtype=torch.float32, device=x.device)
+    L.check(L.lib.circatt_sum_middle(ptr(x), ptr(out), inner, nsum, outer, stream_ptr(x.device)),
+            "circatt_sum_middle")
+    return out
+
+
+def count_unequal(a, b, floats=True):
+    """Number of positions where a and b differ (circatt_count_unequal),
+    read back to the host."""
+    a, b = _c(a), _c(b)
+    cnt = torch.empty((1,), dtype=torch.int64, device=a.device)
+    L.check(L.lib.circatt_count_unequal(1 if floats else 0, a.numel(), ptr(a), ptr(b), ptr(cnt),
+                                        stream_ptr(a.device)), "circatt_count_unequal")
+    return int(cnt.item())
+
+
+class ReplicateFn(torch.autograd.Function):
+    """(outer, inner) -> (outer, r, inner): repeat(A, 1, 1, ...) over one batch
+    dim (src/array.jl:9,49-52) and the broadcasts of scale (src/array.jl:179-186);
+    pullback: the sum over the r copies."""
+
+    @staticmethod
+    def forward(ctx, x, inner, r, outer):
+        ctx.meta = (inner, r, outer, x.shape)
+        return replicate_raw(x, inner, r, outer)
+
+    @staticmethod
+    def backward(ctx, g):
+        inner, r, outer, shape = ctx.meta
+        return sum_middle_raw(g, inner, r, outer).reshape(shape), None, None, None
+
+
+class SumMiddleFn(torch.autograd.Function):
+    """(outer, nsum, inner) -> (outer, 1, inner): sum(A; dims=d) over one batch
+    dim (src/array.jl:132-154); pullback: the cotangent replicated nsum times."""
+
+    @staticmethod
+    def forward(ctx, x, inner, nsum, outer):
+        ctx.meta = (inner, nsum, outer, x.shape)
+        return sum_middle_raw(x, inner, nsum, outer).reshape(outer, 1, inner)
+
+    @staticmethod
+    def backward(ctx, g):
+        inner, nsum, outer, shape = ctx.meta
+        return replicate_raw(g, inner, nsum, outer).reshape(shape), None, None, None
+
+
+class CatFn(torch.autograd.Function):
+    """Parts viewed as (outer, inner_i) joined into (outer, sum_i inner_i)
+    (cat along a batch dim, src/array.jl:62-64); pullback: each part's
+    columns copied back out."""
+
+    @staticmethod
+    def forward(ctx, outer, *parts):
+        parts = [_c(p) for p in parts]
+        inners = [p.numel() // outer for p in parts]
+        tot = sum(inners)
+        out = torch.empty((outer, tot), dtype=parts[0].dtype, device=parts[0].device)
+        es = out.element_size()
+        off = 0
+        for p, n in zip(parts, inners):
+            copy_blocks_raw(out, p, n * es, 1, 0, 0, outer, tot * es, n * es, dst_off=off * es)
+            off += n
+        ctx.meta = (outer, inners, [p.shape for p in parts])
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        outer, inners, shapes = ctx.meta
+        g = _c(g)
+        tot = sum(inners)
+        es = g.element_size()
+        grads, off = [], 0
+        for n, shp in zip(inners, shapes):
+            d = torch.empty((outer, n), dtype=g.dtype, device=g.device)
+            copy_blocks_raw(d, g, n * es, 1, 0, 0, outer, n * es, tot * es, src_off=off * es)
+            grads.append(d.reshape(shp))
+            off += n
+        return (None, *grads)
+
+
 class SimilarityFn(torch.autograd.Function):
     """nzval = scale * circulant_similarity(kind, x, y, ws): forward
     src/similarity.jl:31-103, pullback src/rrules.jl:1-32."""
@@ -232,7 +343,7 @@ class BatchDotFn(torch.autograd.Function):
         dA = dB = None
         if B is None:
             if ctx.needs_input_grad[0]:
-                dA = g.reshape(nb, 1).expand(nb, A.numel() // nb).reshape(A.shape)
+                dA = replicate_raw(g, 1, A.numel() // nb, nb).reshape(A.shape)
         else:
             if ctx.needs_input_grad[0]:
                 dA = axpby_raw(g, B, None, None, nb).reshape(A.shape)

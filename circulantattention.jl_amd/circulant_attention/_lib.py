@@ -72,6 +72,10 @@ SIGNATURES = {
     "circatt_fused_bwd_noalloc_max_rows": (_i64, []),
     "circatt_fused_bwd_noalloc": (_int, [_int, _int, _int, _i64, _i64, _i32, _i64, _i64, _i64,
                                          _p, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
+    "circatt_fill": (_int, [_p, _i64, _f32, _p]),
+    "circatt_copy_blocks": (_int, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]),
+    "circatt_sum_middle": (_int, [_p, _p, _i64, _i64, _i64, _p]),
+    "circatt_count_unequal": (_int, [_int, _i64, _p, _p, _p, _p]),
     "circatt_malloc": (_int, [ctypes.POINTER(_p), _i64]),
     "circatt_free": (_int, [_p]),
     "circatt_memcpy": (_int, [_p, _p, _i64, _int]),

@@ -16,8 +16,9 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib as L
-from ._functions import (AxpbyFn, ApplyFn, BatchDotFn, FusedAttentionFn, SimilarityFn, SoftmaxFn,
-                         geometry, ptr, require, stream_ptr)
+from ._functions import (AxpbyFn, ApplyFn, BatchDotFn, CatFn, FusedAttentionFn, ReplicateFn,
+                         SimilarityFn, SoftmaxFn, SumMiddleFn, count_unequal, fill_raw, geometry,
+                         ptr, replicate_raw, require, similarity_raw, stream_ptr)
 
 
 class AbstractSimilarity:
@@ -115,8 +116,8 @@ class Circulant:
         spatial, batch = dims[:-2], dims[-2:]
         P = int(math.prod(spatial))
         K = ws ** len(spatial)
-        nz = torch.ones((*reversed(batch), P, K), dtype=torch.float32, device=device)
-        return cls(nz, ws, spatial)
+        nz = torch.empty((*reversed(batch), P, K), dtype=torch.float32, device=device)
+        return cls(fill_raw(nz, 1.0), ws, spatial)
 
     # ---- metadata ----
     @property
@@ -206,7 +207,10 @@ class Circulant:
         batch = list(self.batch) + [1] * max(0, len(counts) - 2 - len(self.batch))
         reps = counts[2:] + [1] * (len(batch) - len(counts[2:]))
         nz = self.nzval.reshape(*reversed(batch), self.P, self.K)
-        return Circulant(nz.repeat(*reversed(reps), 1, 1), self.kernel_length, self.spatial_size)
+        for j, c in enumerate(reps):
+            if c > 1:
+                nz = _replicate_axis(nz, len(batch) - 1 - j, c)
+        return Circulant(nz, self.kernel_length, self.spatial_size)
 
     def __eq__(self, other):
         """A == B (src/array.jl:101-115): sizes, spatial size, kernel length
@@ -217,12 +221,14 @@ class Circulant:
             return NotImplemented
         return (self.size() == other.size() and self.spatial_size == other.spatial_size
                 and self.kernel_length == other.kernel_length
-                and torch.equal(self.nzval, other.nzval))
+                and count_unequal(self.nzval, other.nzval) == 0)
 
     __hash__ = None
 
     def copy(self):
-        return Circulant(self.nzval.clone(), self.kernel_length, self.spatial_size)
+        n = self.nzval.numel()
+        nz = ReplicateFn.apply(self.nzval, n, 1, 1).reshape(self.nzval.shape)
+        return Circulant(nz, self.kernel_length, self.spatial_size)
 
     def similar(self):
         return Circulant(torch.empty_like(self.nzval), self.kernel_length, self.spatial_size)
@@ -297,12 +303,22 @@ class Circulant:
 
 
 def _sum_batch_axis(nz, ax):
-    """Sum nzval over one batch axis with circatt_axpby (keepdim)."""
-    n = nz.shape[ax]
-    out = nz.select(ax, 0).unsqueeze(ax)
-    for i in range(1, n):
-        out = AxpbyFn.apply(1.0, out, 1.0, nz.select(ax, i).unsqueeze(ax), 1)
-    return out
+    """Sum nzval over one batch axis (keepdim) with circatt_sum_middle."""
+    shape = list(nz.shape)
+    outer, inner = int(math.prod(shape[:ax])), int(math.prod(shape[ax + 1:]))
+    out = SumMiddleFn.apply(nz, inner, shape[ax], outer)
+    shape[ax] = 1
+    return out.reshape(shape)
+
+
+def _replicate_axis(nz, ax, count):
+    """repeat along torch axis ax (Julia's repeat: the whole axis tiled count
+    times) with circatt_copy_blocks."""
+    shape = list(nz.shape)
+    outer, inner = int(math.prod(shape[:ax])), int(math.prod(shape[ax:]))
+    out = ReplicateFn.apply(nz, inner, count, outer)
+    shape[ax] *= count
+    return out.reshape(shape)
 
 
 class CirculantSum(torch.autograd.Function):
@@ -329,12 +345,16 @@ class CirculantSum(torch.autograd.Function):
         P = int(math.prod(spatial))
         K = ws ** nsp
         g = g.contiguous().reshape(-1, P)
+        nb = g.shape[0]
         if not col:
-            return g.unsqueeze(-1).expand(-1, P, K).reshape(shape), None, None, None
-        # column sums: entry (r, t) has column c(r, t); gather g at colVal
-        _, colval = _pattern(spatial, ws, g.device)
-        idx = (colval.long() - 1).reshape(1, P * K).expand(g.shape[0], -1)
-        return torch.gather(g, 1, idx).reshape(shape), None, None, None
+            return replicate_raw(g, 1, K, nb * P).reshape(shape), None, None, None
+        # column sums: entry (r, t) takes the cotangent of its column c(r, t),
+        # which is the Dot similarity of a one-channel signal of ones
+        # (rows r) with g (columns c): 1 * g[c(r, t)], exact
+        ones = fill_raw(torch.empty((nb, 1, *reversed(spatial)), dtype=torch.float32,
+                                    device=g.device), 1.0)
+        dA = similarity_raw(L.DOT, ones, g.reshape(nb, 1, *reversed(spatial)), spatial, ws, 1.0)
+        return dA.reshape(shape), None, None, None
 
 
 # ---------------------------------------------------------------------------
@@ -386,7 +406,11 @@ def cat(*As: Circulant, dims: int = 3) -> Circulant:
         if [d for i, d in enumerate(b) if i != ax] != \
                 [d for i, d in enumerate(parts[0][1]) if i != ax]:
             raise AssertionError("cat: batch dims other than `dims` must match")
-    nz = torch.cat([p for p, _ in parts], dim=nd - 1 - ax)
+    td = nd - 1 - ax                   # torch axis of the joined batch dim
+    shp = list(parts[0][0].shape)
+    outer = int(math.prod(shp[:td]))
+    shp[td] = sum(p.shape[td] for p, _ in parts)
+    nz = CatFn.apply(outer, *[p for p, _ in parts]).reshape(shp)
     return Circulant(nz, A0.kernel_length, A0.spatial_size)
 
 
@@ -634,9 +658,25 @@ def scale(c: torch.Tensor, A: Circulant) -> Circulant:
         out.append(max(ci, ai))
     rb = tuple(reversed(out))
     nz = A.nzval.reshape(*tuple(reversed(ab)), A.P, A.K)
-    if tuple(nz.shape[:-2]) != rb:
-        nz = nz.expand(*rb, A.P, A.K)  # materialised by AxpbyFn's contiguous()
-    alpha = c.reshape(*tuple(reversed(cb))).expand(*rb).reshape(-1)
+    alpha = c.reshape(*tuple(reversed(cb)))
+    # broadcast A's values and the factors to the joint batch (Julia batch
+    # dim j is torch axis nd - 1 - j)
+    for j in range(nd):
+        ax = nd - 1 - j
+        if ab[j] == 1 and out[j] > 1:
+            nz = _broadcast_axis(nz, ax, out[j])
+        if cb[j] == 1 and out[j] > 1:
+            alpha = _broadcast_axis(alpha, ax, out[j])
     nb = int(math.prod(rb))
-    z = AxpbyFn.apply(alpha.contiguous(), nz, None, None, nb)
+    z = AxpbyFn.apply(alpha.reshape(nb), nz, None, None, nb)
     return Circulant(z.reshape(*rb, A.P, A.K), A.kernel_length, A.spatial_size)
+
+
+def _broadcast_axis(x, ax, count):
+    """x with a size-1 torch axis ax broadcast to count (materialised with
+    circatt_copy_blocks)."""
+    shape = list(x.shape)
+    outer, inner = int(math.prod(shape[:ax])), int(math.prod(shape[ax + 1:]))
+    out = ReplicateFn.apply(x, inner, count, outer)
+    shape[ax] = count
+    return out.reshape(shape)

@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
 #include <mutex>
 #include <string>
 
@@ -527,6 +528,70 @@ int circatt_malloc(void **ptr, int64_t bytes) {
 }
 
 int circatt_free(void *ptr) { return hip_result(hipFree(ptr), "circatt_free"); }
+
+int circatt_fill(float *dst, int64_t n, float value, void *stream) {
+    if (n < 0) return fail(CIRCATT_ERR_INVALID, "n=%lld must be >= 0", (long long)n);
+    if (n == 0) return ok();
+    CIRCATT_NONNULL(dst);
+    uint32_t bits;
+    std::memcpy(&bits, &value, 4);
+    return hip_result(launch_fill(reinterpret_cast<uint32_t *>(dst), n, bits, as_stream(stream)),
+                      "circatt_fill");
+}
+
+int circatt_copy_blocks(void *dst, const void *src, int64_t block_bytes, int64_t ninner,
+                        int64_t dst_stride_inner, int64_t src_stride_inner, int64_t nouter,
+                        int64_t dst_stride_outer, int64_t src_stride_outer, void *stream) {
+    if (block_bytes < 0 || ninner < 0 || nouter < 0)
+        return fail(CIRCATT_ERR_INVALID, "negative block size or count");
+    if (dst_stride_inner < 0 || src_stride_inner < 0 || dst_stride_outer < 0 || src_stride_outer < 0)
+        return fail(CIRCATT_ERR_INVALID, "negative stride");
+    if (block_bytes == 0 || ninner == 0 || nouter == 0) return ok();
+    CIRCATT_NONNULL(dst);
+    CIRCATT_NONNULL(src);
+    // the destination blocks must not overlap (a destination byte written
+    // twice would depend on the order of the writes)
+    if ((ninner > 1 && dst_stride_inner < block_bytes) ||
+        (nouter > 1 && dst_stride_outer < (ninner - 1) * dst_stride_inner + block_bytes))
+        return fail(CIRCATT_ERR_INVALID, "destination blocks overlap");
+    const int64_t dst_end = (nouter - 1) * dst_stride_outer + (ninner - 1) * dst_stride_inner + block_bytes;
+    const int64_t src_end = (nouter - 1) * src_stride_outer + (ninner - 1) * src_stride_inner + block_bytes;
+    const char *d0 = static_cast<const char *>(dst), *s0 = static_cast<const char *>(src);
+    if (d0 < s0 + src_end && s0 < d0 + dst_end)
+        return fail(CIRCATT_ERR_INVALID, "source and destination ranges overlap");
+    return hip_result(launch_copy_blocks(dst, src, block_bytes, ninner, dst_stride_inner,
+                                         src_stride_inner, nouter, dst_stride_outer,
+                                         src_stride_outer, as_stream(stream)),
+                      "circatt_copy_blocks");
+}
+
+int circatt_sum_middle(const float *src, float *dst, int64_t inner, int64_t nsum, int64_t outer,
+                       void *stream) {
+    if (inner < 0 || nsum < 0 || outer < 0) return fail(CIRCATT_ERR_INVALID, "negative size");
+    if (inner == 0 || outer == 0) return ok();
+    if (nsum == 0) return circatt_fill(dst, inner * outer, 0.f, stream);
+    CIRCATT_NONNULL(src);
+    CIRCATT_NONNULL(dst);
+    if (dst < src + inner * nsum * outer && src < dst + inner * outer)
+        return fail(CIRCATT_ERR_INVALID, "src and dst overlap");
+    return hip_result(launch_sum_middle(src, dst, inner, nsum, outer, as_stream(stream)),
+                      "circatt_sum_middle");
+}
+
+int circatt_count_unequal(int kind, int64_t n, const void *a, const void *b, int64_t *count,
+                          void *stream) {
+    if (kind != 0 && kind != 1) return fail(CIRCATT_ERR_INVALID, "kind=%d must be 0 or 1", kind);
+    if (n < 0) return fail(CIRCATT_ERR_INVALID, "n=%lld must be >= 0", (long long)n);
+    CIRCATT_NONNULL(count);
+    if (n > 0) {
+        CIRCATT_NONNULL(a);
+        CIRCATT_NONNULL(b);
+    }
+    return hip_result(launch_count_unequal(kind == 1, n, static_cast<const uint32_t *>(a),
+                                           static_cast<const uint32_t *>(b), count,
+                                           as_stream(stream)),
+                      "circatt_count_unequal");
+}
 
 int circatt_memcpy(void *dst, const void *src, int64_t bytes, int kind) {
     static const hipMemcpyKind kinds[] = {hipMemcpyHostToDevice, hipMemcpyDeviceToHost,

@@ -59,6 +59,19 @@ hipError_t launch_axpby(int64_t nnz, int64_t nb, const float *alpha, float alpha
                         const float *X, const float *beta, float beta0, const float *Y, float *Z,
                         hipStream_t s);
 
+// Batch-dimension operations (batch_ops.hip): fill with a 32-bit pattern;
+// strided block copy dst[o*dso + i*dsi + e] = src[o*sso + i*ssi + e] (bytes,
+// e < block); dst[i + inner*o] = sum_s src[i + inner*(s + nsum*o)]; count of
+// unequal 32-bit words (floats: as Float32 values) into one device int64.
+hipError_t launch_fill(uint32_t *dst, int64_t n, uint32_t bits, hipStream_t s);
+hipError_t launch_copy_blocks(void *dst, const void *src, int64_t block, int64_t ninner,
+                              int64_t dsi, int64_t ssi, int64_t nouter, int64_t dso, int64_t sso,
+                              hipStream_t s);
+hipError_t launch_sum_middle(const float *src, float *dst, int64_t inner, int64_t nsum,
+                             int64_t outer, hipStream_t s);
+hipError_t launch_count_unequal(bool floats, int64_t n, const uint32_t *a, const uint32_t *b,
+                                int64_t *count, hipStream_t s);
+
 // Arithmetic of the fused kernels' matrix products (circatt_set_math):
 // CIRCATT_MATH_SPLIT_F16 or CIRCATT_MATH_F32.
 int math_mode();

@@ -22,6 +22,7 @@ import ChainRulesCore as CRC
 import Zygote
 
 include("libcircatt.jl")
+include("devops.jl")
 
 include("array.jl")
 export Circulant, circulant

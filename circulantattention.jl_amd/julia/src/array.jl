@@ -23,30 +23,32 @@ function Base.getproperty(A::CircCSR, s::Symbol)
     s === :nnz && return length(getfield(A, :nzVal))
     return getfield(A, s)
 end
-Base.copy(A::CircCSR) = CircCSR(copy(A.rowPtr), copy(A.colVal), copy(A.nzVal), A.dims)
-Base.similar(A::CircCSR) = CircCSR(copy(A.rowPtr), copy(A.colVal), similar(A.nzVal), A.dims)
+Base.copy(A::CircCSR) = CircCSR(dcopy(A.rowPtr), dcopy(A.colVal), dcopy(A.nzVal), A.dims)
+Base.similar(A::CircCSR) = CircCSR(dcopy(A.rowPtr), dcopy(A.colVal), similar(A.nzVal), A.dims)
 
 nbatch(A::CircCSR) = prod(A.dims[3:end]; init=1)
 slots(A::CircCSR) = length(A.nzVal) ÷ (A.dims[1] * nbatch(A))   # K
 
-# scalar reads copy one row to the host (debugging and printing only)
+# scalar reads copy row i's slots to the host one by one (debugging and
+# printing only)
 function Base.getindex(A::CircCSR{T,N}, I::Vararg{Int,N}) where {T,N}
     i, j = I[1], I[2]
     b = LinearIndices(A.dims[3:end])[I[3:end]...]
     K = slots(A)
-    cols = Array(reshape(A.colVal, :, nbatch(A))[(i - 1) * K + 1:i * K, b])
-    vals = Array(reshape(A.nzVal, :, nbatch(A))[(i - 1) * K + 1:i * K, b])
+    base = (b - 1) * A.dims[1] * K + (i - 1) * K
     s = zero(T)
     for t in 1:K
-        cols[t] == j && (s += vals[t])
+        read_scalar(A.colVal, base + t) == j && (s += read_scalar(A.nzVal, base + t))
     end
     return s
 end
 
+# the reference's == of two CSR arrays (src/array.jl:87-101): sizes, then
+# nzVal, rowPtr and colVal element by element, compared on the device
 function Base.:(==)(A::CircCSR, B::CircCSR)
     size(A) == size(B) || return false
-    return Array(A.nzVal) == Array(B.nzVal) && Array(A.rowPtr) == Array(B.rowPtr) &&
-           Array(A.colVal) == Array(B.colVal)
+    return count_unequal(A.nzVal, B.nzVal) == 0 && count_unequal(A.rowPtr, B.rowPtr) == 0 &&
+           count_unequal(A.colVal, B.colVal) == 0
 end
 
 function Base.show(io::IO, ::MIME"text/plain", A::CircCSR)
@@ -69,7 +71,7 @@ function circulant_csr(::Type{T}, M::Int, spatsize::NTuple{S,Int}, batchsize::Tu
     colVal = ROCArray{Int32}(undef, P * K, batchsize...)
     check(circatt_pattern(nsp, n1, n2, Int32(M), Int64(nb), dptr(rowPtr), dptr(colVal),
                           stream_ptr()), "circatt_pattern")
-    nzVal = AMDGPU.ones(Float32, P * K, batchsize...)
+    nzVal = dfill!(ROCArray{Float32}(undef, P * K, batchsize...), 1f0)
     return CircCSR(rowPtr, colVal, nzVal, (P, P, batchsize...))
 end
 
@@ -99,6 +101,16 @@ end
 function Adapt.adapt_structure(to, A::Circulant{T, N, M}) where {T, N, M}
     Circulant(Adapt.adapt_structure(to, A.data), M, A.spatial_size)
 end
+
+# eager release of a Circulant's device arrays (the reference's
+# CUDA.unsafe_free!, src/array.jl:27)
+function AMDGPU.unsafe_free!(A::CircCSR)
+    AMDGPU.unsafe_free!(A.rowPtr)
+    AMDGPU.unsafe_free!(A.colVal)
+    AMDGPU.unsafe_free!(A.nzVal)
+    return nothing
+end
+AMDGPU.unsafe_free!(A::Circulant) = AMDGPU.unsafe_free!(A.data)
 
 """circulant(M, x): a Circulant shaped for signal x (src/array.jl:29)."""
 circulant(M::Int, x::AbstractArray{T, N}) where {T,N} =
@@ -162,18 +174,19 @@ function _circulant_reshape(A::Circulant{T, N, M}, dims...) where {T, N, M}
     reshape(A, dims...)
 end
 
+# Julia's repeat over the batch dims (src/array.jl:9,49-52), on the device
 function Base.repeat(A::CircCSR, counts::Int...)
     (length(counts) >= 2 && counts[1] == 1 && counts[2] == 1) ||
         throw(ArgumentError("repeat(A, 1, 1, counts...): the (P, P) dims of a Circulant cannot be repeated"))
     bc = counts[3:end]
-    rp = repeat(A.rowPtr, 1, bc...)
-    cv = repeat(A.colVal, 1, bc...)
-    nz = repeat(A.nzVal, 1, bc...)
+    rp = drepeat(A.rowPtr, bc...)
+    cv = drepeat(A.colVal, bc...)
+    nz = drepeat(A.nzVal, bc...)
     return CircCSR(rp, cv, nz, (A.dims[1], A.dims[2], size(nz)[2:end]...))
 end
 
 function Base.repeat(A::Circulant{T, N, M}, dims::Int...) where {T, N, M}
-    data = repeat(A.data, dims...)
+    data = Base.repeat(A.data, dims...)
     Circulant(data, M, spatial_size(A))
 end
 
@@ -182,9 +195,9 @@ end
 function Base.cat(As::Circulant{T, N, M}...; dims=3) where {T, N, M}
     dims isa Integer && dims >= 3 || throw(ArgumentError("cat of Circulants joins batch dims (dims >= 3)"))
     d = dims - 1
-    rp = cat((A.data.rowPtr for A in As)...; dims=d)
-    cv = cat((A.data.colVal for A in As)...; dims=d)
-    nz = cat((A.data.nzVal for A in As)...; dims=d)
+    rp = dcat((A.data.rowPtr for A in As)...; dims=d)
+    cv = dcat((A.data.colVal for A in As)...; dims=d)
+    nz = dcat((A.data.nzVal for A in As)...; dims=d)
     P = size(As[1], 1)
     Circulant(CircCSR(rp, cv, nz, (P, P, size(nz)[2:end]...)), M, spatial_size(As[1]))
 end
@@ -206,7 +219,7 @@ function axpby!(Z::ROCArray{Float32}, alpha, X::ROCArray{Float32}, beta, Y, nb::
 end
 
 with_nzval(X::Circulant{T, N, M}, nz) where {T, N, M} =
-    Circulant(CircCSR(copy(X.data.rowPtr), copy(X.data.colVal), nz, size(X)), M, spatial_size(X))
+    Circulant(CircCSR(dcopy(X.data.rowPtr), dcopy(X.data.colVal), nz, size(X)), M, spatial_size(X))
 
 function Base.:(+)(X::Circulant{T, N, M}, Y::Circulant{T, N, M}) where {T, N, M}
     @assert size(X) == size(Y) "Circulant + Circulant needs equal sizes"
@@ -238,7 +251,7 @@ end
 
 function LinearAlgebra.dot(X::Circulant, Y::Circulant)
     @assert size(X) == size(Y) "dot needs equal sizes"
-    return Array(batch_dot(X.data.nzVal, Y.data.nzVal, 1))[1]
+    return read_scalar(batch_dot(X.data.nzVal, Y.data.nzVal, 1))
 end
 
 function Base.:(==)(A::Circulant, B::Circulant)
@@ -271,19 +284,15 @@ function rowcol_sum(A::Circulant, col::Bool)
     return out
 end
 
-"""nzVal summed over batch dims `sdims` (Julia dims >= 3) with circatt_axpby."""
+"""nzVal summed over batch dims `sdims` (Julia dims >= 3; circatt_sum_middle),
+the indices of the first slice kept (src/array.jl:132-154)."""
 function sum_batchdims(A::CircCSR, sdims)
     nz, rp, cv = A.nzVal, A.rowPtr, A.colVal
     for d in sort(collect(sdims); rev=true)
         ax = d - 1  # dim of nzVal
-        n = size(nz, ax)
-        first = copy(selectdim(nz, ax, 1:1))
-        for i in 2:n
-            axpby!(first, 1f0, first, 1f0, copy(selectdim(nz, ax, i:i)), 1)
-        end
-        nz = first
-        rp = copy(selectdim(rp, ax, 1:1))
-        cv = copy(selectdim(cv, ax, 1:1))
+        nz = dsum(nz, ax)
+        rp = dfirst(rp, ax)
+        cv = dfirst(cv, ax)
     end
     return CircCSR(rp, cv, nz, (A.dims[1], A.dims[2], size(nz)[2:end]...))
 end
@@ -292,7 +301,7 @@ function Base.sum(A::Circulant; dims=:)
     nb = nbatch(A)
     bs = size(A)[3:end]
     if dims isa Colon
-        return Array(batch_dot(A.data.nzVal, nothing, 1))[1]
+        return read_scalar(batch_dot(A.data.nzVal, nothing, 1))
     end
     d = dims isa Integer ? (Int(dims),) : Tuple(Int(x) for x in dims)
     if all(>(2), d)
@@ -311,7 +320,8 @@ end
 # ---- scale (src/array.jl:179-189) ------------------------------------------
 
 """scale(c, A) = c .* A with c of size (1, 1, batch...) broadcast against A's
-batch dims (circatt_axpby with one factor per slice)."""
+batch dims (src/array.jl:179-189): the factors and A's arrays broadcast on
+the device, then circatt_axpby with one factor per slice."""
 function scale(c::ROCArray{Tc}, A::Circulant{Ta, N, M}) where {Tc<:Real, Ta, N, M}
     @assert size(c, 1) == 1 && size(c, 2) == 1 "Scaling of non-batchdims of CuSparseArrayCSR not implemented"
     nd = max(ndims(c), ndims(A)) - 2
@@ -322,18 +332,20 @@ function scale(c::ROCArray{Tc}, A::Circulant{Ta, N, M}) where {Tc<:Real, Ta, N, 
         (cb[i] == rb[i] || cb[i] == 1) && (ab[i] == rb[i] || ab[i] == 1) ||
             throw(DimensionMismatch("cannot broadcast scale factor $cb against batch $ab"))
     end
-    reps = ntuple(i -> rb[i] ÷ ab[i], nd)
-    X = reshape(A.data.nzVal, :, ab...)
-    rp = reshape(A.data.rowPtr, :, ab...)
-    cv = reshape(A.data.colVal, :, ab...)
-    if any(>(1), reps)
-        X, rp, cv = repeat(X, 1, reps...), repeat(rp, 1, reps...), repeat(cv, 1, reps...)
+    Tc === Float32 || throw(ArgumentError("libcircatt scale factors are Float32, got $Tc"))
+    X = dbroadcast(reshape(A.data.nzVal, :, ab...), (size(A.data.nzVal, 1), rb...))
+    if ab == rb  # the new Circulant gets its own index arrays, as the reference's copies
+        rp, cv = dcopy(A.data.rowPtr), dcopy(A.data.colVal)
+    else
+        rp = dbroadcast(reshape(A.data.rowPtr, :, ab...), (size(A.data.rowPtr, 1), rb...))
+        cv = dbroadcast(reshape(A.data.colVal, :, ab...), (size(A.data.colVal, 1), rb...))
     end
-    alpha = ROCArray{Float32}(vec(Float32.(Array(c)) .* ones(Float32, 1, 1, rb...)))
-    Z = axpby!(similar(X), alpha, X, nothing, nothing, prod(rb; init=1))
+    alpha = dbroadcast(reshape(c, cb...), rb)
+    Z = axpby!(similar(X), vec(alpha), X, nothing, nothing, prod(rb; init=1))
     P = size(A, 1)
-    return Circulant(CircCSR(copy(rp), copy(cv), Z, (P, P, rb...)), M, spatial_size(A))
+    return Circulant(CircCSR(rp, cv, Z, (P, P, rb...)), M, spatial_size(A))
 end
-scale(c, A) = c .* A
+scale(c::Number, A::Circulant) = c * A
+scale(c::Array, A::Circulant) = scale(upload(Float32.(c)), A)
 
 Base.:(*)(c::ROCArray, A::Circulant) = scale(c, A)

@@ -6,12 +6,12 @@
 @doc raw"""
     y, A = circulant_attention(simfun::AbstractSimilarity, q, k, v, W::Int; materialize=true)
 
-Perform circulant attention on `y=Av`, where A is a row-softmax normalized
-circulant-sparse attention matrix (A = rowsoftmax(S)). Each non-zero entry ``S_{ij}``
-is generated via the similarity function acting on the channel representations of `q` and `k`
-at (linearly indexed) pixels `i`, `j` (``S_{ij} = \mathrm{simfun}(q_i, k_j)``).
-Note: q and k are internally scaled by `sqrt(sqrt(channels))`.  With `materialize=false`
-the fused kernels compute `y` without forming `A` (returned as `nothing`).
+Sliding-window attention with circular boundaries: `A` is the adjacency of
+`q` against `k` (`simfun` scores over each pixel's W-wide window, row
+softmax) and `y = A ⊗ v`.  Both `q` and `k` are divided by the fourth root of
+the channel count first, so the scores carry a factor ``1/\sqrt{C}``.  With
+`materialize=false` the fused kernels produce `y` without forming `A`, which
+is then returned as `nothing`.
 """
 function circulant_attention(simfun::AbstractSimilarity, q::T, k::T, v::T, W::Int; materialize::Bool=true,
                              channels_last::Bool=false) where {Tv, N, T<: AbstractArray{Tv,N}}
@@ -32,12 +32,12 @@ circulant_attention(q::T, k::T, v::T, W::Int; kws...) where T = circulant_attent
     y, A = circulant_mh_attention(simfun::AbstractSimilarity, q, k, v, W::Int, nheads::Int;
                                   materialize=true, honor_simfun=false)
 
-Performs circulant multi-head attention, i.e., performing circulant attention of
-`nheads`-groups separately and concatenating the result along channels. The
-number of channels in `q`, `k`, `v` must be divisible by `nheads`.
-The returned adjacency matrix `A` will have `size(A, 3) == nheads`.
-As in the reference (src/attention.jl:40), `simfun` is ignored and the dot
-similarity is used unless `honor_simfun=true`.
+Circulant attention per head: the channels of `q`, `k` and `v` split into
+`nheads` consecutive groups (the channel count must be a multiple of
+`nheads`), each group attended on its own and the outputs placed back in
+channel order.  `A` has one (P, P) matrix per head and batch:
+`size(A) == (P, P, nheads, B)`.  Like the reference (src/attention.jl:40)
+the dot similarity is used whatever `simfun` is, unless `honor_simfun=true`.
 """
 function circulant_mh_attention(simfun::AbstractSimilarity, q::T, k::T, v::T, W::Int, nheads::Int;
                                 materialize::Bool=true, honor_simfun::Bool=false,
@@ -87,7 +87,8 @@ end
     y = circulant_attention(A::Circulant, x::AbstractArray)
     y = A ⊗ x # \otimes
 
-Applies circulant matrix `A` to `x`.
+The product of the sparse circulant matrix `A` (one per batch) with the
+pixels-by-channels matrix of `x`; `y` has the size of `x`.
 See also [`circulant_adjacency`](@ref).
 """
 circulant_attention(A::Circulant, x) = circulant_attention!(similar(x), A, x)
@@ -104,7 +105,8 @@ circulant_transposed_attention(A::Circulant, x) = circulant_transposed_attention
     y = circulant_mh_attention(A::Circulant, x::AbstractArray)
     y = A ⨷ x # \Otimes
 
-Applies circulant matrix `A` (with channel dimension > 1) to `x`.
+⊗ per head: `A` of size (P, P, nheads, B) applied to the `nheads` channel
+groups of `x`.
 """
 function circulant_mh_attention(A::Circulant{Ta, 4}, x::AbstractArray{T, N}) where {Ta, T, N}
     nheads = size(A, 3)

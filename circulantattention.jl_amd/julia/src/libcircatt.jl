@@ -134,6 +134,27 @@ circatt_fused_bwd_noalloc(kind, dtype, nsp, n1, n2, ws, C, nheads, B, q, k, v, y
            Ptr{Cvoid}),
           kind, dtype, nsp, n1, n2, ws, C, nheads, B, q, k, v, y, dy, lse, dq, dk, dv, stream)
 
+circatt_fill(dst, n, value, stream) =
+    ccall((:circatt_fill, libcircatt), Cint, (Ptr{Cfloat}, Int64, Cfloat, Ptr{Cvoid}),
+          dst, n, value, stream)
+
+circatt_copy_blocks(dst, src, block_bytes, ninner, dst_stride_inner, src_stride_inner, nouter,
+                    dst_stride_outer, src_stride_outer, stream) =
+    ccall((:circatt_copy_blocks, libcircatt), Cint,
+          (Ptr{Cvoid}, Ptr{Cvoid}, Int64, Int64, Int64, Int64, Int64, Int64, Int64, Ptr{Cvoid}),
+          dst, src, block_bytes, ninner, dst_stride_inner, src_stride_inner, nouter,
+          dst_stride_outer, src_stride_outer, stream)
+
+circatt_sum_middle(src, dst, inner, nsum, outer, stream) =
+    ccall((:circatt_sum_middle, libcircatt), Cint,
+          (Ptr{Cfloat}, Ptr{Cfloat}, Int64, Int64, Int64, Ptr{Cvoid}),
+          src, dst, inner, nsum, outer, stream)
+
+circatt_count_unequal(kind, n, a, b, count, stream) =
+    ccall((:circatt_count_unequal, libcircatt), Cint,
+          (Cint, Int64, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Int64}, Ptr{Cvoid}),
+          kind, n, a, b, count, stream)
+
 circatt_malloc(ptr, bytes) =
     ccall((:circatt_malloc, libcircatt), Cint, (Ptr{Ptr{Cvoid}}, Int64), ptr, bytes)
 

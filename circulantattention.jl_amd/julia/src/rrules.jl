@@ -4,10 +4,17 @@
 # circatt_similarity (∂A of ⊗) and circatt_apply (its ∂x), circatt_axpby and
 # circatt_batch_dot (scale), circatt_fused_bwd (fused attention).
 
-"""Cotangent on device memory shaped like `like` (dense ROCArray)."""
+"""Cotangent on device memory shaped like `like` (dense ROCArray): a
+ROCArray as is, a constant (Fill) filled on the device, a host array
+uploaded; anything else is rejected rather than staged through the host."""
 as_device(Δ::ROCArray, like) = Δ
-as_device(Δ::Zygote.FillArrays.Fill, like) = fill!(similar(like), Δ.value)
-as_device(Δ::AbstractArray, like) = copyto!(similar(like), Array(Δ))
+as_device(Δ::Zygote.FillArrays.Fill, like) = dfill!(similar(like), Δ.value)
+function as_device(Δ::Array, like)
+    @assert size(Δ) == size(like) "cotangent of size $(size(Δ)) for an output of size $(size(like))"
+    return reshape(upload(convert(Array{eltype(like)}, Δ)), size(like))
+end
+as_device(Δ::AbstractArray, like) = throw(ArgumentError(
+    "libcircatt takes device cotangents (ROCArray), a Fill or a host Array; got $(typeof(Δ))"))
 
 cotangent_nzval(Δ::Circulant) = Δ.data.nzVal
 cotangent_nzval(Δ::CircCSR) = Δ.nzVal
@@ -107,6 +114,14 @@ function LinearAlgebra.dot(f::Zygote.FillArrays.Fill{T,N}, A::Circulant{T,N}) wh
     return f.value * sum(A)
 end
 
+"""A Circulant on A's pattern with batch size sz[3:end] and every value v
+(a constant cotangent made a Circulant on the device)."""
+function filled_like(A::Circulant, sz::Tuple, v)
+    C = Circulant{Float32}(kernel_length(A), (spatial_size(A)..., sz[3:end]...))
+    dfill!(C.data.nzVal, v)
+    return C
+end
+
 _scale_collectnz(X::Circulant) = X.data.nzVal
 _scale_collectnz(X::Zygote.FillArrays.Fill) = X.value
 
@@ -117,24 +132,30 @@ function CRC.rrule(::typeof(scale), c::AbstractArray{T,N}, A::Circulant{T,N}) wh
     function scale_pullback(dB)
         ΔB = CRC.unthunk(dB)
         ∂c = CRC.@thunk begin
-            # per-slice dots of ΔB with A (A repeated to ΔB's batch where it
-            # broadcast), then summed over the batch dims where c has size 1
+            # per-slice dots of ΔB with A (A broadcast to ΔB's batch), then
+            # summed over the batch dims where c has size 1, all on the device
             bs = size(ΔB)[3:end]
-            ab = size(A)[3:end]
-            reps = bs .÷ ab
+            ab = ntuple(i -> size(A, i + 2), length(bs))
             Anz = reshape(A.data.nzVal, :, ab...)
-            Ab = any(>(1), reps) ? repeat(Anz, 1, reps...) : Anz
+            Ab = ab == bs ? Anz : dbroadcast(Anz, (size(Anz, 1), bs...))
             nb = prod(bs; init=1)
             g = _scale_collectnz(ΔB)
-            per = g isa Number ? g .* Array(batch_dot(Ab, nothing, nb)) : Array(batch_dot(g, Ab, nb))
+            per = if g isa Number
+                d = batch_dot(Ab, nothing, nb)
+                axpby!(d, Float32(g), d, nothing, nothing, 1)
+            else
+                batch_dot(g, Ab, nb)
+            end
             s = reshape(per, bs...)
-            sumdims = Tuple(filter(d -> size(c, d + 2) == 1, 1:length(bs)))
-            s = isempty(sumdims) ? s : sum(s; dims=sumdims)
-            project_c(ROCArray(reshape(Float32.(s), size(c)...)))
+            for d in 1:length(bs)
+                size(c, d + 2) == 1 && bs[d] > 1 && (s = dsum(s, d))
+            end
+            project_c(reshape(s, size(c)...))
         end
         ∂A = CRC.@thunk begin
+            ΔBc = ΔB isa Zygote.FillArrays.Fill ? filled_like(A, size(ΔB), ΔB.value) : ΔB
             sumdims = filter(d -> size(A,d)==1, 1:ndims(A))
-            project_A(sum(scale(c, ΔB); dims=sumdims))
+            project_A(sum(scale(c, ΔBc); dims=sumdims))
         end
         return (CRC.NoTangent(), ∂c, ∂A)
     end

@@ -7,12 +7,10 @@ abstract type AbstractSimilarity end
 @doc raw"""
     DotSimilarity()
 
-Used in `circulant_attention`, `circulant_similarity`, and `circulant_adjacency` to indicate use of
-dot-product similarity:
-
-``
-    S_{ij} = \mathrm{Real}(q[i]^H k[j]).
-``
+Selects the inner-product score between the channel vectors of query pixel
+`i` and key pixel `j`: ``S_{ij} = \mathrm{Re}\,\langle k_j, q_i\rangle``
+(the real part of the Hermitian product for complex signals).  Pass it to
+`circulant_similarity`, `circulant_adjacency` or `circulant_attention`.
 
 See also [`DistanceSimilarity`](@ref).
 """
@@ -21,12 +19,10 @@ struct DotSimilarity <: AbstractSimilarity end
 @doc raw"""
     DistanceSimilarity()
 
-Used in `circulant_attention`, `circulant_similarity`, and `circulant_adjacency` to indicate use of
-distance similarity (the reference's kernel computes the negated half, src/similarity.jl:55-78):
-
-``
-    S_{ij} = -\frac{1}{2}\mathrm{sum}(\mathrm{abs2}, q[i] - k[j]).
-``
+Selects minus half the squared Euclidean distance between the channel
+vectors of query pixel `i` and key pixel `j`:
+``S_{ij} = -\tfrac{1}{2}\lVert q_i - k_j\rVert^2`` (the sign and the half are
+those of the reference's kernel, src/similarity.jl:55-78).
 
 See also [`DotSimilarity`](@ref).
 """
@@ -57,9 +53,10 @@ end
 """
     circulant_similarity(simfun::AbstractSimilarity, x, y, W::Int)
 
-Returns Circulant matrix with circulant-sparse data. Each non-zero `S[i,j,b]` is
-populated by `simfun` evaluated at the linearized pixel locations of `x` and `y`,
-i.e. `S[i,j,b] = simfun(x[...,i,b], y[...,j,b], W)` for max(i⃗, j⃗) ≤ W.
+A new `Circulant` of size (P, P, 1, B) holding, for every pixel `i` of `x`
+and every pixel `j` in the circularly wrapped W-wide window around it, the
+score of `simfun` between the channels of `x` at `i` and of `y` at `j`
+(batch by batch).  Pixels are linear (column-major) indices; W is odd.
 
 See also [`DotSimilarity`](@ref), [`DistanceSimilarity`](@ref).
 """
@@ -93,7 +90,8 @@ end
 """
     NNlib.softmax(A::Circulant)
 
-Row-wise softmax of Circulant matrix `A`.
+A new `Circulant` whose rows (the W^S window slots of each pixel) are
+normalised by a softmax.
 """
 function NNlib.softmax(A::Circulant)
     data = circulant_softmax(A.data)
@@ -109,7 +107,8 @@ end
 """
     circulant_adjacency(simfun::AbstractSimilarity, x, y, W::Int)
 
-Equivalent to `(softmax ∘ circulant_similarity)(simfun, x, y, W)`.
+The row-softmax of `circulant_similarity(simfun, x, y, W)`: each row holds
+the attention weights of one pixel over its window.
 
 See also [`circulant_similarity`](@ref), [`NNlib.softmax`](@ref).
 """

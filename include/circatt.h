@@ -250,6 +250,42 @@ int circatt_fused_bwd_noalloc(int kind, int dtype, int nsp, int64_t n1, int64_t 
                               const float *lse, void *dq, void *dk, void *dv, void *stream);
 
 /*
+ * Batch-dimension operations on a Circulant's CSR arrays (and other device
+ * arrays), so that a host binding needs no array-library kernels of its own:
+ *
+ * circatt_fill: dst[i] = value for i < n.  The nzVal = 1 of a new pattern
+ * (CUDA.ones at src/circulant.jl:68,90), a constant cotangent made dense.
+ *
+ * circatt_copy_blocks: for o < nouter, i < ninner, copies block_bytes bytes
+ * from src + o*src_stride_outer + i*src_stride_inner to
+ * dst + o*dst_stride_outer + i*dst_stride_inner (all in bytes; a stride of 0
+ * replicates).  repeat over batch dims (src/array.jl:9,49-52), cat along a
+ * batch dim (src/array.jl:62-64), the broadcast of a scale factor over heads
+ * or batches (src/array.jl:179-186).  Destination blocks must not overlap each
+ * other or the source; works on any element type (16, 8, 4 or 1-byte units,
+ * the widest that divides every address, size and stride).
+ *
+ * circatt_sum_middle: dst[i + inner*o] = sum_s src[i + inner*(s + nsum*o)]
+ * for a column-major (inner, nsum, outer) Float32 array, summed in double in
+ * order of s.  sum(A; dims=d) over a batch dim d (src/array.jl:132-154), the
+ * ∂c of the scale rrule over c's size-1 dims (src/rrules.jl:98-104), and the
+ * pullback of repeat.
+ *
+ * circatt_count_unequal: *count (one device int64, overwritten) = the number
+ * of i < n with a[i] != b[i], comparing 32-bit words (kind 0: Int32 rowPtr,
+ * colVal) or Float32 values as floats (kind 1: -0 == 0, NaN != NaN).  == of
+ * Circulants (src/array.jl:87-117) reads the count back.
+ */
+int circatt_fill(float *dst, int64_t n, float value, void *stream);
+int circatt_copy_blocks(void *dst, const void *src, int64_t block_bytes, int64_t ninner,
+                        int64_t dst_stride_inner, int64_t src_stride_inner, int64_t nouter,
+                        int64_t dst_stride_outer, int64_t src_stride_outer, void *stream);
+int circatt_sum_middle(const float *src, float *dst, int64_t inner, int64_t nsum, int64_t outer,
+                       void *stream);
+int circatt_count_unequal(int kind, int64_t n, const void *a, const void *b, int64_t *count,
+                          void *stream);
+
+/*
  * Device memory helpers for hosts without a GPU array package (the reference
  * gets these from CUDA.jl).  kind: 0 host->device, 1 device->host,
  * 2 device->device.

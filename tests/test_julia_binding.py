@@ -7,7 +7,12 @@ tests pin what can be checked without it.
   order (int -> Cint, int64_t -> Int64, int32_t -> Int32, float -> Cfloat,
   T* -> Ptr{T}, void** -> Ptr{Ptr{Cvoid}}, const char* -> Cstring), and every
   header function is bound exactly once;
-* no other Julia file calls ccall (everything goes through those bindings);
+* no other Julia file calls ccall (everything goes through those bindings),
+  and none launches array kernels of its own or stages device data through
+  the host: AMDGPU.ones/zeros, fill!, repeat, cat, copy(selectdim ...),
+  copyto!, Array(...) and dotted broadcast operators do not appear outside
+  comments and docstrings (the Circulant's fill, repeat, cat, batch sums,
+  broadcasts and == are libcircatt entry points, devops.jl);
 * the module exports every name the reference exports
   (src/CirculantAttention.jl:4,19,22-23,26) and defines the reference's
   method extensions and rules: NNlib.softmax(!), NNlib.batched_mul(!),
@@ -183,3 +188,41 @@ def test_project_toml_names_the_package():
     assert 'name = "CirculantAttention"' in text
     for dep in ("AMDGPU", "ChainRulesCore", "NNlib", "Zygote", "Adapt"):
         assert re.search(rf"^{dep} = \"[0-9a-f-]{{36}}\"$", text, flags=re.M), dep
+
+
+def _code_only(text):
+    """Julia source without docstrings, string literals and comments."""
+    text = re.sub(r'(@doc\s+raw)?"""(.*?)"""', "", text, flags=re.S)
+    text = re.sub(r'"(?:[^"\\\n]|\\.)*"', '""', text)
+    return "\n".join(l.split("#")[0] for l in text.splitlines())
+
+
+FORBIDDEN = [r"AMDGPU\.(ones|zeros|fill|rand|randn)\b", r"(?<![\w.])fill!\(",
+             r"(?<![\w.])repeat\(", r"(?<![\w.])cat\(", r"copy\(\s*selectdim", r"copyto!\(",
+             r"(?<![\w.])Array\(", r"\s\.(\*|\+|-|/|\^|=|÷)\s", r"\)\.(\*|\+|-|/)"]
+
+
+def test_no_array_kernels_or_host_staging_outside_libcircatt():
+    src = os.path.join(JL, "src")
+    for f in sorted(os.listdir(src)):
+        if not f.endswith(".jl"):
+            continue
+        code = _code_only(open(os.path.join(src, f)).read())
+        for pat in FORBIDDEN:
+            m = re.search(pat, code)
+            assert m is None, (f, pat, code[max(0, m.start() - 60):m.end() + 20])
+
+
+def test_forbidden_patterns_are_caught():
+    """The guard's patterns match the calls it exists to keep out."""
+    bad = ["nz = AMDGPU.ones(Float32, 4)", "fill!(similar(x), 1)", "r = repeat(x, 1, 2)",
+           "c = cat(a, b; dims=2)", "copy(selectdim(x, 2, 1:1))", "copyto!(y, x)",
+           "h = Array(x)", "y = c .* x", "z = (a).+ b"]
+    for line in bad:
+        assert any(re.search(p, _code_only(line)) for p in FORBIDDEN), line
+    ok = ["function Base.repeat(A::CircCSR, counts::Int...)", "data = Base.repeat(A.data, 2)",
+          "dfill!(x, 1f0)", "# c .* A in a comment", '"""Array(x) in a docstring"""',
+          "splitheads.((q, k, v), nheads)", "function Base.cat(As::Circulant...; dims=3)",
+          'throw(ArgumentError("repeat(A, 1, 1, counts...)"))']
+    for line in ok:
+        assert not any(re.search(p, _code_only(line)) for p in FORBIDDEN), line
