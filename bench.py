@@ -20,9 +20,14 @@ dP and dQ, dk/dv pass 2U for dV and dK; recomputation and softmax work not
 counted) against MI355X's dense FP32 MFMA peak, 157.3 TFLOP/s.  Kernel times
 come from HIP events on the stream the kernels run on.
 
+Inputs: q, k, v, dy drawn on the host in that order from NumPy's PCG64
+(seed 1000 + config number: 1003 for cfg3), N(0,1) float32 (ComplexF32:
+(re + i im)/sqrt(2)), and copied to the device; the same arrays feed both legs.
+
 cpu_baseline: the oracle's float32 build (oracle/circatt_oracle.c: the
 reference's unfused algorithm, OpenMP over all host cores) timed on a bounded
-sample of the same workload (a few (head, batch) units).
+sample of the same workload: the first (head, batch) units of the very inputs
+the GPU step uses.
 """
 from __future__ import annotations
 
@@ -58,29 +63,47 @@ def describe(name):
             f"{sp}x{C}x{B}, nheads={nh}, ws={ws}, A not materialised")
 
 
-def cpu_baseline(name, budget_s=12.0):
-    """Time the float32 oracle (reference's unfused algorithm, OpenMP) on
-    whole (head, batch) units of the workload until ~budget_s of CPU work."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+SEEDS = {"cfg3": 1003, "cfg4a": 1004, "cfg4b": 1005, "cfg5": 1006}
+
+
+def host_inputs(name):
+    """q, k, v, dy of the workload, drawn on the host in that order from
+    NumPy's PCG64 (the same bits go to the GPU and to the CPU baseline)."""
     import numpy as np
+
+    dims, C, B, nh, ws, kind, cplx = CONFIGS[name]
+    rng = np.random.default_rng(SEEDS[name])
+    shape = (B, C, *reversed(dims))
+    out = []
+    for _ in range(4):
+        if cplx:
+            a = rng.standard_normal(shape, dtype=np.float32) + 1j * rng.standard_normal(
+                shape, dtype=np.float32)
+            out.append((a / np.sqrt(2)).astype(np.complex64))
+        else:
+            out.append(rng.standard_normal(shape, dtype=np.float32))
+    return out
+
+
+def cpu_baseline(name, inputs, budget_s=12.0):
+    """Time the float32 oracle (reference's unfused algorithm, OpenMP) on
+    whole (head, batch) units of the workload's own inputs, in unit order,
+    until ~budget_s of CPU work."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
     import oracle as O
 
     dims, C, B, nh, ws, kind, cplx = CONFIGS[name]
     dh = C // nh
     P = int(math.prod(dims))
-    rng = np.random.default_rng(1000 + 3)
-    shape = (1, dh, *reversed(dims))
 
-    def signal():
-        if cplx:
-            return ((rng.standard_normal(shape) + 1j * rng.standard_normal(shape)) /
-                    np.sqrt(2)).astype(np.complex64)
-        return rng.standard_normal(shape).astype(np.float32)
+    def unit(a, u):  # head g of batch b, unit g + nh*b (src/attention.jl:44)
+        b, g = divmod(u, nh)
+        return a[b:b + 1, g * dh:(g + 1) * dh]
 
     units, total = 0, 0.0
     while units < nh * B and total < budget_s:
-        q, k, v, dy = (signal() for _ in range(4))
+        q, k, v, dy = (unit(a, units) for a in inputs)
         t0 = time.perf_counter()
         _, A = O.attention_fwd(kind, q, k, v, ws, 1, precision="f32")
         O.attention_bwd(kind, q, k, v, dy, ws, 1, precision="f32", A=A)
@@ -93,9 +116,9 @@ def cpu_baseline(name, budget_s=12.0):
         "unit": "Mpixel/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"{units} of {nh * B} (head,batch) units of {name}, fwd+bwd of the "
-                   f"reference's unfused algorithm (float32 C/OpenMP restatement), "
-                   f"{total:.1f} s"),
+        "sample": (f"the first {units} of {nh * B} (head,batch) units of {name}'s own inputs "
+                   f"(the GPU step's bits), fwd+bwd of the reference's unfused algorithm "
+                   f"(float32 C/OpenMP restatement), {total:.1f} s"),
     }
 
 
@@ -279,11 +302,9 @@ def main():
     K = ws ** nsp
     dh = C // nh
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(1003)
-    dtype = torch.complex64 if cplx else torch.float32
-    shape = (B, C, *reversed(dims))
-    q, k, v, dy = (torch.randn(shape, device=dev, dtype=dtype, generator=g) for _ in range(4))
+    host = host_inputs(args.config)
+    q, k, v, dy = (torch.from_numpy(a).to(dev) for a in host)
+    torch.cuda.synchronize()
     y = torch.empty_like(q)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
     lse = torch.empty((B * nh, P), device=dev, dtype=torch.float32)
@@ -379,10 +400,12 @@ def main():
                 "tflops": flops[n] / (kern_ms[n] / 1e3) / 1e12} for n in kern_ms}
     dom = max(kern_ms, key=kern_ms.get)
     achieved = kern[dom]["tflops"]
-    traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
-    if os.path.exists(tfile):
-        traffic = json.load(open(tfile)).get(dom)
+    traffic, traffic_src = None, None
+    tfile = os.path.join("profiles", f"traffic_{args.config}.json")
+    if os.path.exists(os.path.join(ROOT, tfile)):
+        traffic = json.load(open(os.path.join(ROOT, tfile))).get(dom)
+        traffic_src = (f"{tfile}: HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and "
+                       f"WRITE_SIZE runs (not measured in this run)")
     out = {
         "metric": base["metric"],
         "value": round(mpix, 3),
@@ -401,12 +424,13 @@ def main():
         "vs_baseline": None,
         "dtype": "c32" if cplx else "f32",
         "math": math_mode,
-        "data": "synthetic N(0,1), seeded, resident in HBM",
+        "data": f"synthetic N(0,1), NumPy PCG64 seed {SEEDS[args.config]}, resident in HBM",
         "config": {"workload": describe(args.config), "spatial": list(dims), "C": C, "B": B,
                    "nheads": nh, "ws": ws, "similarity": "Distance" if kind else "Dot"},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 3),
                      "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": traffic},
+                     "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src},
         "step_roofline": {"alg_tflop_per_step": 6 * U / 1e12,
                           "achieved_tflops": round(6 * U / (ms_step / 1e3) / 1e12, 3),
                           "frac": round(6 * U / (ms_step / 1e3) / 1e12 / PEAK_FP32_TFLOPS, 4),
@@ -417,7 +441,7 @@ def main():
     if args.calib_copy_mib > 0:
         out["calib_copy_bytes"] = calib_copy(args.calib_copy_mib)
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(args.config)
+        out["cpu_baseline"] = cpu_baseline(args.config, host)
     print(json.dumps(out), flush=True)
 
 

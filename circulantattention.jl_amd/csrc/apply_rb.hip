@@ -2429,21 +2429,19 @@ void set_band(ApplyArgs &a, int ncomp, int64_t nb) {
 bool band_supported(const Geom &g) { return g.nsp == 2 && g.ws > 15 && (g.ws + kJC - 1) / kJC <= 2; }
 
 // the band kernels' LDS passes 64 KiB: raise the kernel's dynamic limit once
+// per instantiation (the callers keep the result in a function-local static,
+// initialised exactly once, also when several host threads launch at once)
 template <typename Kern>
-hipError_t band_lds_attr(Kern kern, size_t bytes, bool &done) {
-    if (done) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-    if (e == hipSuccess) done = true;
-    return e;
+hipError_t band_lds_attr(Kern kern, size_t bytes) {
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 template <int NCOMP, bool TRANS>
 hipError_t launch_band(ApplyArgs a, int64_t nb, hipStream_t s) {
-    static bool attr = false;
     set_band<TRANS>(a, NCOMP, nb);
     const int64_t grid = 8LL * a.brg * a.tiles1 * a.gchunk;
     const size_t lds = (size_t)AB<NCOMP, TRANS>::LDS * sizeof(float);
-    hipError_t e = band_lds_attr(apply_band_kernel<NCOMP, TRANS>, lds, attr);
+    static const hipError_t e = band_lds_attr(apply_band_kernel<NCOMP, TRANS>, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((apply_band_kernel<NCOMP, TRANS>), dim3((unsigned)grid), dim3(64 * kBR), lds,
                        s, a);
@@ -2451,13 +2449,12 @@ hipError_t launch_band(ApplyArgs a, int64_t nb, hipStream_t s) {
 }
 template <int NCOMP>
 hipError_t launch_band_pair(ApplyArgs af, ApplyArgs at, int64_t nb, hipStream_t s) {
-    static bool attr = false;
     set_band<false>(af, NCOMP, nb);
     set_band<true>(at, NCOMP, nb);
     const int64_t grid = 16LL * af.brg * af.tiles1 * af.gchunk;
     const size_t lds =
         (size_t)std::max(AB<NCOMP, false>::LDS, AB<NCOMP, true>::LDS) * sizeof(float);
-    hipError_t e = band_lds_attr(apply_band_pair_kernel<NCOMP>, lds, attr);
+    static const hipError_t e = band_lds_attr(apply_band_pair_kernel<NCOMP>, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((apply_band_pair_kernel<NCOMP>), dim3((unsigned)grid), dim3(64 * kBR), lds,
                        s, af, at);

@@ -229,6 +229,9 @@ struct Args {
     // template argument; cl selects the instantiation.
     int cl, nheads, ncrall;
     FastDiv div_nh;
+    // per-wave phase sums of the split-half kernels in phase-timing builds
+    // (CIRCATT_F2H_PHASE); unused otherwise
+    float *phase;
 };
 
 // Layout of q, k, v, y, dy and the gradients.  Planar (CL = false, the
@@ -780,14 +783,11 @@ hipError_t launch(const Args &a0, int cus, hipStream_t s) {
     using G = Geo<P, NT, GR::WH, GR::WW>;
     static_assert(GR::bytes <= kLdsCap, "halo does not fit LDS");
     auto kern = kernel2d<P, NT, CPLX, DIST, MODE, CL>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)GR::bytes);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    // set once per instantiation (a function-local static is initialised
+    // exactly once, also when several host threads launch at the same time)
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)GR::bytes);
+    if (attr != hipSuccess) return attr;
     Args a = a0;
     a.tiles_h = (a.n1 + G::TH - 1) / G::TH;
     a.tiles_w = (a.n2 + G::TW - 1) / G::TW;

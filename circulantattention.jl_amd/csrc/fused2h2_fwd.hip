@@ -9,4 +9,17 @@ hipError_t launch_f2h2_fwd(int p, bool cplx, bool dist, const f2d::Args &a, int 
     return f2h::dispatch<f2h::FWD, 2>(p, cplx, dist, a, cus, s);
 }
 
+#if CIRCATT_F2H_PHASE
+// phase-timing builds of these kernels only: the buffer of 512 floats the
+// waves write to
+float *&phase_buffer() {
+    static float *p = nullptr;
+    return p;
+}
+#endif
+
 }  // namespace circatt
+
+#if CIRCATT_F2H_PHASE
+extern "C" void circatt_debug_set_phase_buffer(float *p) { circatt::phase_buffer() = p; }
+#endif

@@ -51,13 +51,17 @@
 // its items: staging (without the barriers), the barrier after the maxima, the
 // barrier after the staging, and the walk with its epilogue.  Wave w of
 // workgroup b < 8 writes the four sums (as 32-bit integers) to floats
-// 4 (16 b + w) .. + 3 past the end of its output (y, dq or dk: offset
-// unit_stride * nunits), which the caller must allocate.
+// 4 (16 b + w) .. + 3 of a dedicated buffer of 512 floats, which such a build
+// takes through circatt_debug_set_phase_buffer (defined in fused2h_fwd.hip
+// only when CIRCATT_F2H_PHASE is set; a null buffer writes nothing).
 #ifndef CIRCATT_F2H_PHASE
 #define CIRCATT_F2H_PHASE 0
 #endif
 #if CIRCATT_F2H_PHASE
 #define F2H_PHASE(...) __VA_ARGS__
+namespace circatt {
+float *&phase_buffer();
+}
 #else
 #define F2H_PHASE(...)
 #endif
@@ -1151,9 +1155,8 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         w0 = xw0;
     }
 #if CIRCATT_F2H_PHASE
-    if (blockIdx.x < 8 && lane == 0) {
-        float *o = (MODE == FWD ? a.yout : MODE == BWDQ ? a.dq : a.dk) +
-                   (int64_t)a.unit_stride * a.nunits + 4 * (16 * blockIdx.x + wv);
+    if (blockIdx.x < 8 && lane == 0 && a.phase) {
+        float *o = a.phase + 4 * (16 * blockIdx.x + wv);
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = __uint_as_float((unsigned)phase[i]);
     }
@@ -1166,14 +1169,13 @@ hipError_t launch2h(const Args &a0, int cus, hipStream_t s) {
     constexpr int bytes = LGeo<P, NT, MODE, DIST>::bytes;
     static_assert(bytes <= (int)f2d::kLdsCap, "halo does not fit LDS");
     auto kern = kernel2h<P, NT, CPLX, DIST, MODE, CL>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    // set once per instantiation (a function-local static is initialised
+    // exactly once, also when several host threads launch at the same time)
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (attr != hipSuccess) return attr;
     Args a = a0;
+    F2H_PHASE(a.phase = phase_buffer();)
     a.tiles_h = (a.n1 + G::TH - 1) / G::TH;
     a.tiles_w = (a.n2 + G::TW - 1) / G::TW;
     const int64_t nitems = (int64_t)a.tiles_h * a.tiles_w * a.nunits;

@@ -766,14 +766,11 @@ constexpr size_t kLdsMax = 160 * 1024;
 template <int NSP, int NC, bool DIST, int MODE, int PC>
 hipError_t launch_inst(const FusedPlan &pl, hipStream_t s) {
     auto kern = fused_kernel<NSP, NC, DIST, MODE, PC>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)kLdsMax);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    // set once per instantiation (a function-local static is initialised
+    // exactly once, also when several host threads launch at the same time)
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
+    if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL(kern, pl.grid, dim3(256), pl.lds_bytes, s, pl.a);
     return hipGetLastError();
 }

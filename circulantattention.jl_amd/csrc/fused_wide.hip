@@ -8,14 +8,11 @@ namespace {
 template <int NSP, bool DIST, int MODE>
 hipError_t launch_one(const FArgs &a, size_t lds, dim3 grid, hipStream_t s) {
     auto kern = wide::wide_kernel<NSP, DIST, MODE>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)wide::kLdsBudget);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    // set once per instantiation (a function-local static is initialised
+    // exactly once, also when several host threads launch at the same time)
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide::kLdsBudget);
+    if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL(kern, grid, dim3(wide::THREADS), lds, s, a);
     return hipGetLastError();
 }

@@ -3,10 +3,10 @@
 A copy of libcircatt built with CIRCATT_F2H_PHASE=1 makes every wave of
 kernel2h sum s_memtime spans of four phases over its items (staging, the two
 barriers, the walk with its epilogue) and lets the waves of workgroups 0..7
-write the sums past the end of their output.  This script builds that copy
-(on a machine with hipcc; the other objects come from the in-tree build) and,
-on an MI355X, runs the three cfg3 kernels with enlarged outputs and prints
-the phases per wave slot.
+write the sums to a buffer of 512 floats given to that copy's extra entry
+point circatt_debug_set_phase_buffer.  This script builds that copy (on a
+machine with hipcc; the other objects come from the in-tree build) and, on an
+MI355X, runs the three cfg3 kernels and prints the phases per wave slot.
 
     python circulantattention.jl_amd/microbench/phase_timing.py --build [--no-prio]
     python circulantattention.jl_amd/microbench/phase_timing.py [--no-prio]
@@ -79,9 +79,11 @@ def run(no_prio: bool) -> None:
     shape = (B, C, n2, n1)
     dt, DT = (torch.complex64, L.C32) if cplx else (torch.float32, L.F32)
     q, k, v, dy = (torch.randn(shape, device=dev, generator=g, dtype=dt) for _ in range(4))
-    N, EX = q.numel() * (2 if cplx else 1), 8 * 16 * 4
-    yb, dqb, dkb = (torch.zeros(N + EX, device=dev) for _ in range(3))
-    dv = torch.empty_like(q)
+    yb, dqb, dkb, dv = (torch.empty_like(q) for _ in range(4))
+    phase = torch.zeros(8 * 16 * 4, device=dev)
+    lib.circatt_debug_set_phase_buffer.restype = None
+    lib.circatt_debug_set_phase_buffer.argtypes = [ctypes.c_void_p]
+    lib.circatt_debug_set_phase_buffer(ptr(phase))
     lse = torch.empty((B * nh, P), device=dev)
     wb = lib.circatt_fused_bwd_workspace_bytes(2, n1, n2, nh, B)
     work = torch.empty((wb // 4,), device=dev)
@@ -107,8 +109,7 @@ def run(no_prio: bool) -> None:
     torch.cuda.synchronize()
     print(f"{CFG}, cycles summed over each wave's items (mean over the 8 sampled workgroups)"
           + (", equal wave priorities" if no_prio else ""))
-    for name, f, buf in (("forward", fwd, yb), ("query-centric", bwd_dq, dqb),
-                         ("key-centric", bwd_dkdv, dkb)):
+    for name, f in (("forward", fwd), ("query-centric", bwd_dq), ("key-centric", bwd_dkdv)):
         for _ in range(50):
             f()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -116,7 +117,7 @@ def run(no_prio: bool) -> None:
         f()
         e1.record()
         torch.cuda.synchronize()
-        t = buf[N:].view(torch.int32).cpu().numpy().reshape(8, 16, 4)[:, :nw].astype("int64")
+        t = phase.view(torch.int32).cpu().numpy().reshape(8, 16, 4)[:, :nw].astype("int64")
         tot = t.sum(axis=2)
         m = t.mean(axis=(0, 1))
         print(f"{name}: kernel {e0.elapsed_time(e1) * 1e3:.1f} us, "
