@@ -267,11 +267,20 @@ enum { FWD = f2d::FWD, BWDQ = f2d::BWDQ, BWDKV = f2d::BWDKV };
 // their (8 + 2P) x (2 + 2P) window region: 2x8 blocks, or at windows 3 and
 // 11 4x4 blocks, which cover that region with fewer pixels (ws 11: 15
 // blocks, 240 pixels, against 18 blocks, 288).
-// Element 4 g + r of a block (the score accumulator's row) sits at block row
-// r % 2, column 2 g + r / 2 (2x8), or at row r, column g (4x4).  LDS slots
-// are column-major with CR slots per column: CR = 2 mod 4 for 2x8 blocks and
-// CR = 4 mod 16 for 4x4 blocks, which keeps the 16-byte reads of a block's
-// rows (slot stride 144 bytes) free of bank conflicts.  4x4 blocks reach
+// Element e = 4 g + r of a block (the score accumulator's row) sits at block
+// row e / 8, column e % 8 (2x8 blocks, row-major), or at row r, column g
+// (4x4).  LDS slots are column-major with CR slots per column: CR = 2 mod 4
+// for 2x8 blocks and CR = 4 mod 16 for 4x4 blocks, which keeps the 16-byte
+// reads of a block's rows (slot stride 80 or 144 bytes) free of bank
+// conflicts.  With 2x8 blocks the row-major element order also keeps the
+// transposing reads free of them: the 16 lanes of a lane group read 32-byte
+// runs of four slots CR apart, and the 32 lanes of two groups eight slots of
+// one block row, which fall on distinct banks of the 64 (4 bytes each): the
+// slot stride is an odd number of 16-byte units and CR is even.  2x2 element
+// groups put two of a group's four runs on the same banks.  Per-slot Float32
+// scalars are stored row-major for 2x8 blocks (so that a lane group's four
+// elements are adjacent) and column-major, like the slots, for 4x4 blocks.
+// 4x4 blocks reach
 // BR * NKH - (8 + 2P) rows past the staged ones, into the pad rows of the
 // column; those rows, and staged-region columns past the last staged one,
 // hold zeros written once per launch and are read only under the mask.
@@ -292,6 +301,10 @@ struct HGeo {
     static constexpr int LPX = CR * HWD;                    // LDS pixel slots per tensor
     // slot offset of block b within a wavefront's region
     static constexpr int bslot(int b) { return BR * (b / NKW) + CR * BC * (b % NKW); }
+    // index of the scalar of the pixel at slot row `row`, column `col`, and
+    // the scalar offset of block b within a wavefront's region
+    static constexpr int sidx(int row, int col) { return BR == 2 ? col + HWD * row : row + CR * col; }
+    static constexpr int sbslot(int b) { return sidx(BR * (b / NKW), BC * (b % NKW)); }
     // central pair of the streamed forward: two blocks of the block row that
     // holds key rows 8, 9 (in every query's window when 2P >= 9)
     static constexpr int PCENT = (8 / BR) * NKW / 2;
@@ -309,15 +322,15 @@ __host__ __device__ constexpr uint64_t hmask(int P, int bi, int bj, int r) {
     uint64_t m = 0;
     for (int lane = 0; lane < 64; ++lane) {
         const int j = lane & 15, g = lane >> 4;
-        const int kr = BR == 2 ? 2 * bi + (r & 1) : 4 * bi + r;
-        const int kc = BR == 2 ? 8 * bj + 2 * g + (r >> 1) : 4 * bj + g;
+        const int kr = BR == 2 ? 2 * bi + (g >> 1) : 4 * bi + r;
+        const int kc = BR == 2 ? 8 * bj + 4 * (g & 1) + r : 4 * bj + g;
         const int u1 = kr - (j & 7), u2 = kc - (j >> 3);
         if (u1 >= 0 && u1 <= 2 * P && u2 >= 0 && u2 <= 2 * P) m |= 1ull << lane;
     }
     return m;
 }
-static_assert(hmask<2>(7, 3, 1, 2) == f2d::lane_mask(7, 3, 1, 2) && hmask<2>(5, 0, 0, 1) == f2d::lane_mask(5, 0, 0, 1),
-              "2x8 masks as the Float32 kernels'");
+// the Float32 kernels (f2d::lane_mask) keep the 2x2 element groups
+static_assert(hmask<2>(7, 3, 1, 2) != f2d::lane_mask(7, 3, 1, 2), "row-major 2x8 elements");
 
 template <int P, int NT, int MODE, bool DIST>
 struct LGeo {
@@ -392,21 +405,25 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         return v;
     };
     // score-type rows: element j of a block, halves 8 g .. 8 g + 7 of its slot
-    const int slotA = BR == 2 ? 8 * wh + (j & 1) + CR * (2 * ww + (j >> 1))
+    const int slotA = BR == 2 ? 8 * wh + (j >> 3) + CR * (2 * ww + (j & 7))
                               : 8 * wh + (j & 3) + CR * (2 * ww + (j >> 2));
     const char *const pA0 = lds + opaque(L::OT0 + slotA * SB + 16 * g);
     const char *const pA1 = lds + opaque(L::OT1 + slotA * SB + 16 * g);
     // apply-type rows from slots by transposing reads: lane (j, g) receives
     // channel j (hi; lo 16 halves further) of elements 4g + t, t = 0..3, so
     // lane j of group g addresses channels 4 (j & 3) .. + 3 of element
-    // 4g + (j >> 2), which sits at row (j >> 2) & 1, column 2g + (j >> 3)
-    const int slotE = 8 * wh + CR * (2 * ww + (BR == 2 ? 2 * g : g));
-    const int slotT = BR == 2 ? slotE + ((j >> 2) & 1) + CR * (j >> 3) : slotE + (j >> 2);
+    // 4g + (j >> 2), which sits at row g / 2, column 4 (g % 2) + (j >> 2)
+    // (2x8) or at row j >> 2, column g (4x4)
+    const int slotE = BR == 2 ? 8 * wh + (g >> 1) + CR * (2 * ww + 4 * (g & 1))
+                              : 8 * wh + CR * (2 * ww + g);
+    const int slotT = BR == 2 ? slotE + CR * (j >> 2) : slotE + (j >> 2);
     const char *const pR0 = lds + opaque(L::OT0 + slotT * SB + 8 * (j & 3));
     const char *const pR1 = lds + opaque(L::OT1 + slotT * SB + 8 * (j & 3));
-    // per-slot Float32 scalars of elements 4g .. 4g+3
-    const float *const pS0 = reinterpret_cast<const float *>(lds + opaque(L::OS0 + slotE * 4));
-    const float *const pS1 = reinterpret_cast<const float *>(lds + opaque(L::OS1 + slotE * 4));
+    // per-slot Float32 scalars of elements 4g .. 4g+3 (adjacent)
+    const int sidxE = BR == 2 ? G::sidx(8 * wh + (g >> 1), 2 * ww + 4 * (g & 1))
+                              : G::sidx(8 * wh, 2 * ww + g);
+    const float *const pS0 = reinterpret_cast<const float *>(lds + opaque(L::OS0 + sidxE * 4));
+    const float *const pS1 = reinterpret_cast<const float *>(lds + opaque(L::OS1 + sidxE * 4));
 
     // ---- prefetch registers ----
     float h0v[16 * NT], h1v[16 * NT], hs0 = 0.f, hs1 = 0.f;
@@ -439,6 +456,7 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
     const bool big = a.n1 >= HH && a.n2 >= HWD;
     const int px = threadIdx.x;
     const int kw = px / HH, kh = px - kw * HH;
+    const int hsid = G::sidx(kh, kw);  // scalar index of the staged pixel
     auto load_stage = [&](int unit, int h0, int w0) {
         // halo origin (h0 - P, w0 - P) mod (n1, n2), uniform
         int hsh = h0 - P, wsh = w0 - P;
@@ -526,8 +544,8 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
             f4 *const z1 = reinterpret_cast<f4 *>(lds + L::OT1 + i * SB);
 #pragma unroll
             for (int q = 0; q < SB / 16; ++q) z0[q] = z1[q] = f4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (L::NSCAL >= 1) reinterpret_cast<float *>(lds + L::OS0)[i] = 0.f;
-            if constexpr (L::NSCAL >= 2) reinterpret_cast<float *>(lds + L::OS1)[i] = 0.f;
+            if constexpr (L::NSCAL >= 1) reinterpret_cast<float *>(lds + L::OS0)[G::sidx(i % CR, i / CR)] = 0.f;
+            if constexpr (L::NSCAL >= 2) reinterpret_cast<float *>(lds + L::OS1)[G::sidx(i % CR, i / CR)] = 0.f;
         }
     }
     int unit, h0, w0;
@@ -627,12 +645,12 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
             if constexpr (KV) {
                 // staged queries: A_q = -lse log2(e) [- c2 |q|^2 / 2], and
                 // -D in the scale of the dP product
-                reinterpret_cast<float *>(lds + L::OS0)[hslot] =
+                reinterpret_cast<float *>(lds + L::OS0)[hsid] =
                     -hs0 * kLog2e - (DIST ? 0.5f * c2 * n2 : 0.f);
-                reinterpret_cast<float *>(lds + L::OS1)[hslot] =
+                reinterpret_cast<float *>(lds + L::OS1)[hsid] =
                     -__builtin_amdgcn_ldexpf(hs1, s1 + s2);
             } else if constexpr (DIST) {
-                reinterpret_cast<float *>(lds + L::OS0)[hslot] = -0.5f * c2 * n2;  // key bias
+                reinterpret_cast<float *>(lds + L::OS0)[hsid] = -0.5f * c2 * n2;  // key bias
             }
         }
         // register operands (the score product's side pre-scaled by c2):
@@ -771,12 +789,12 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
                 lo[h] = ldtr(pR + boff + 64 * h + 32);
             }
         };
-        // per-slot scalars of elements 4g + r of block b
+        // per-slot scalars of elements 4g + r of block b (4 adjacent floats)
         auto scal = [&](auto B, const float *pS) {
             constexpr int b = decltype(B)::value;
-            constexpr int boff = G::bslot(b);
+            constexpr int boff = G::sbslot(b);
             const f2 lo = *reinterpret_cast<const f2 *>(pS + boff);
-            const f2 hi = *reinterpret_cast<const f2 *>(pS + boff + (BR == 2 ? CR : 2));
+            const f2 hi = *reinterpret_cast<const f2 *>(pS + boff + 2);
             return f4{lo[0], lo[1], hi[0], hi[1]};
         };
 

@@ -29,8 +29,8 @@ def geo(P, NT):
 
 def element(BR, bi, bj, g, r):
     """Wave-relative key position of element 4 g + r of block (bi, bj)."""
-    if BR == 2:
-        return 2 * bi + (r & 1), 8 * bj + 2 * g + (r >> 1)
+    if BR == 2:  # row-major: element e at block row e // 8, column e % 8
+        return 2 * bi + (g >> 1), 8 * bj + 4 * (g & 1) + r
     return 4 * bi + r, 4 * bj + g
 
 
@@ -63,9 +63,30 @@ def test_block_rows_read_conflict_free(P, NT):
     G = geo(P, NT)
     units = set()
     for j in range(16):
-        row, col = (j & 1, j >> 1) if G["BR"] == 2 else (j & 3, j >> 2)
+        row, col = element(G["BR"], 0, 0, j >> 2, j & 3)
         units.add(((row + G["CR"] * col) * G["SB"] // 16) % 16)
     assert len(units) == 16
+
+
+@pytest.mark.parametrize("P,NT", [c for c in CASES if c[0] not in (1, 5)])
+def test_transposing_reads_conflict_free(P, NT):
+    """Apply-type rows of 2x8 blocks: lane j of lane group g reads 8 bytes,
+    channels 4 (j & 3) .. + 3 of element 4 g + (j >> 2), at
+    slot * SB + 8 (j & 3) (+ 32 for the low halves, + 64 per sub-pixel).  The
+    32 lanes of groups (0, 1) and of groups (2, 3) read 256 bytes each: every
+    4-byte bank of the 64 must be hit once.  2x2 element groups hit half of
+    them twice."""
+    G = geo(P, NT)
+    for h in range(NT):
+        for lo in (0, 32):
+            for half in (0, 1):
+                banks = []
+                for lane in range(32 * half, 32 * half + 32):
+                    j, g = lane & 15, lane >> 4
+                    row, col = element(2, 0, 0, g, j >> 2)
+                    a = (row + G["CR"] * col) * G["SB"] + 64 * h + lo + 8 * (j & 3)
+                    banks += [(a // 4) % 64, (a // 4 + 1) % 64]
+                assert sorted(banks) == list(range(64)), (h, lo, half)
 
 
 @pytest.mark.parametrize("P,NT", CASES)
