@@ -64,6 +64,9 @@ def describe(name):
 
 
 SEEDS = {"cfg3": 1003, "cfg4a": 1004, "cfg4b": 1005, "cfg5": 1006}
+# the bound BASELINE.md gives each configuration (cfg4b, 1D with 32 channels
+# and a window of 63, is HBM-bound; the others are matrix-core bound)
+BOUND = {"cfg3": "mfma", "cfg4a": "mfma", "cfg4b": "hbm", "cfg5": "mfma"}
 
 
 def host_inputs(name):
@@ -398,6 +401,13 @@ def main():
     flops = {"fwd": 2 * U, "bwd_dq": 2 * U, "bwd_dkdv": 2 * U}
     kern = {n: {"avg_ms": kern_ms[n], "alg_gflop": flops[n] / 1e9,
                 "tflops": flops[n] / (kern_ms[n] / 1e3) / 1e12} for n in kern_ms}
+    # algorithmic HBM bytes per launch: T = one q-sized tensor, L = lse or D
+    Tb = 4.0 * B * P * C * cfac
+    Lb = 4.0 * B * nh * P
+    alg_bytes = {"fwd": 4 * Tb + Lb, "bwd_dq": 6 * Tb + 2 * Lb, "bwd_dkdv": 6 * Tb + 2 * Lb}
+    for n in kern:
+        kern[n]["alg_gb"] = alg_bytes[n] / 1e9
+        kern[n]["gbs"] = alg_bytes[n] / (kern_ms[n] / 1e3) / 1e9
     dom = max(kern_ms, key=kern_ms.get)
     achieved = kern[dom]["tflops"]
     traffic, traffic_src = None, None
@@ -427,10 +437,20 @@ def main():
         "data": f"synthetic N(0,1), NumPy PCG64 seed {SEEDS[args.config]}, resident in HBM",
         "config": {"workload": describe(args.config), "spatial": list(dims), "C": C, "B": B,
                    "nheads": nh, "ws": ws, "similarity": "Distance" if kind else "Dot"},
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 3),
-                     "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": traffic,
-                     "traffic_source": traffic_src},
+        "roofline": ({"bound": "mfma", "kernel": dom, "achieved": round(achieved, 3),
+                      "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                      "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": traffic,
+                      "traffic_source": traffic_src}
+                     if BOUND[args.config] == "mfma" else
+                     {"bound": "hbm", "kernel": dom, "achieved": round(kern[dom]["gbs"], 1),
+                      "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                      "frac": round(kern[dom]["gbs"] / PEAK_HBM_GBS, 4), "traffic": traffic,
+                      "traffic_source": traffic_src,
+                      "alg_bytes": "fwd 4T + L, each backward pass 6T + 2L (T: one q-sized tensor, "
+                                   "L: lse or D)"}),
+        "step_hbm": {"alg_mb_per_step": round((12 * Tb + 4 * Lb) / 1e6, 1),
+                     "achieved_gbs": round((12 * Tb + 4 * Lb) / (ms_step / 1e3) / 1e9, 1),
+                     "frac": round((12 * Tb + 4 * Lb) / (ms_step / 1e3) / 1e9 / PEAK_HBM_GBS, 4)},
         "step_roofline": {"alg_tflop_per_step": 6 * U / 1e12,
                           "achieved_tflops": round(6 * U / (ms_step / 1e3) / 1e12, 3),
                           "frac": round(6 * U / (ms_step / 1e3) / 1e12 / PEAK_FP32_TFLOPS, 4),
