@@ -50,7 +50,8 @@ Plan make_plan(FusedMode mode, const FusedProblem &pr) {
     const int ntensor = mode == MODE_SIM ? 1 : 2;
     const int nscalar = mode == MODE_BWDKV ? 2 : (dist ? 1 : 0);
     const int ppt = pl.nc * ntensor <= 32 ? 2 : 1;
-    a.hg = plan_halo(pr.g.nsp, pr.g.p, pl.nc, ntensor, nscalar, ppt);
+    // (Distance: nc floats after the halo hold the item's centre)
+    a.hg = plan_halo(pr.g.nsp, pr.g.p, pl.nc, ntensor, nscalar, ppt, dist ? pl.nc : 0);
     if (!a.hg.ok) return pl;
     if (pr.g.nsp == 2) {
         a.tiles_h = (pr.g.n1 + 7) / 8;

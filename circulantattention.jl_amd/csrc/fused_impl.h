@@ -95,9 +95,10 @@ struct HaloGeo {
 };
 
 // ntensor staged [pixel][NC+4] tensors and nscalar staged per-pixel scalars;
-// ppt halo pixels per thread and stage (register staging capacity).
+// ppt halo pixels per thread and stage (register staging capacity); extra
+// floats after them (the Distance centre).
 __host__ __device__ constexpr HaloGeo plan_halo(int nsp, int p, int nc, int ntensor,
-                                                int nscalar, int ppt) {
+                                                int nscalar, int ppt, int extra = 0) {
     HaloGeo h{};
     const int PS = nc + 4;
     const int bpp = ntensor * PS + nscalar;  // floats per staged pixel
@@ -113,7 +114,7 @@ __host__ __device__ constexpr HaloGeo plan_halo(int nsp, int p, int nc, int nten
         int cr = 0;
         for (; rows >= 2; rows -= 2) {
             cr = rows + ((2 - rows % 4) + 4) % 4;
-            if ((size_t)cr * h.halo_w * bpp * 4 <= kLdsBudget && rows * h.halo_w <= cap_px) break;
+            if ((size_t)(cr * h.halo_w * bpp + extra) * 4 <= kLdsBudget && rows * h.halo_w <= cap_px) break;
         }
         if (rows < 2) return h;
         h.chunk_rows = rows;
@@ -127,13 +128,13 @@ __host__ __device__ constexpr HaloGeo plan_halo(int nsp, int p, int nc, int nten
         h.halo_w = 1;
         int rows = h.halo_h;  // chunks are whole 16-row LDS blocks
         for (; rows >= 16; rows -= 16)
-            if ((size_t)rows * bpp * 4 <= kLdsBudget && rows <= cap_px) break;
+            if ((size_t)(rows * bpp + extra) * 4 <= kLdsBudget && rows <= cap_px) break;
         if (rows < 16) return h;
         h.chunk_rows = rows;
         h.cr = rows;
     }
     h.nchunks = (h.halo_h + h.chunk_rows - 1) / h.chunk_rows;
-    h.lds_floats = h.cr * h.halo_w * bpp;
+    h.lds_floats = h.cr * h.halo_w * bpp + extra;
     h.ok = true;
     return h;
 }
@@ -285,7 +286,7 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
     constexpr bool BIAS = CF::BIAS;
     constexpr bool TWO = MODE == MODE_BWDQ || MODE == MODE_BWDKV;
     constexpr bool CT = PC >= 0;
-    constexpr HaloGeo GC = plan_halo(NSP, CT ? PC : 0, NC, NTEN, CF::NLDS_SCAL, PPT);
+    constexpr HaloGeo GC = plan_halo(NSP, CT ? PC : 0, NC, NTEN, CF::NLDS_SCAL, PPT, DIST ? NC : 0);
     static_assert(!CT || GC.ok, "compiled-in window does not fit");
     // geometry: constants when compiled in
     const int p1 = CT ? GC.p1 : a.hg.p1;
@@ -309,6 +310,7 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
     const int oT1 = chunk_px * PS;
     const int oS0 = NTEN * chunk_px * PS;
     const int oS1 = oS0 + chunk_px;
+    const int oMU = oS0 + CF::NLDS_SCAL * chunk_px;  // Distance: the item's centre (NC floats)
 
     // Per-lane LDS bases.  LDS block (i, jb) of this wavefront starts at
     // pixel (wh + KH*i - cr0) + CR*(ww + KW*jb); its element kk = 4g + r sits
@@ -449,19 +451,13 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
 
         // Distance: both sides of the score product centred on mu (the
         // expansion q.k - |k|^2 / 2 - |q|^2 / 2 of -|q - k|^2 / 2 then scales
-        // with the spread of the data, not its offset)
-        if constexpr (DIST) {
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const float mc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(nmu), c));
-#pragma unroll
-                for (int pp = 0; pp < PPT; ++pp) hv[pp][0][c] -= mc;
-            }
-            if (chunk == 0) {
-#pragma unroll
-                for (int s = 0; s < NS; ++s) nr0[s] -= __shfl(nmu, 16 * (s >> 2) + 4 * g + (s & 3));
-            }
-        }
+        // with the spread of the data, not its offset).  Lane c of wave 0
+        // publishes component c of the item's centre in LDS; every chunk's
+        // staged tensor-0 pixels and the register pixel subtract it as they
+        // are written (broadcast reads: no per-component registers are held).
+        // The previous item's centre was last read before its last chunk's
+        // "chunk staged" barrier, which every wave has passed.
+        if (DIST && chunk == 0 && threadIdx.x < NC) circatt_lds[oMU + threadIdx.x] = nmu;
         __syncthreads();  // the previous chunk's LDS reads are done
 #pragma unroll
         for (int pp = 0; pp < PPT; ++pp) {
@@ -470,10 +466,10 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
                 float n2 = 0.f;
 #pragma unroll
                 for (int c = 0; c < NC; c += 4) {
-                    *reinterpret_cast<f4 *>(&circatt_lds[o0 + c]) =
-                        f4{hv[pp][0][c], hv[pp][0][c + 1], hv[pp][0][c + 2], hv[pp][0][c + 3]};
-                    n2 += hv[pp][0][c] * hv[pp][0][c] + hv[pp][0][c + 1] * hv[pp][0][c + 1] +
-                          hv[pp][0][c + 2] * hv[pp][0][c + 2] + hv[pp][0][c + 3] * hv[pp][0][c + 3];
+                    f4 x = f4{hv[pp][0][c], hv[pp][0][c + 1], hv[pp][0][c + 2], hv[pp][0][c + 3]};
+                    if constexpr (DIST) x = x - *reinterpret_cast<const f4 *>(&circatt_lds[oMU + c]);
+                    *reinterpret_cast<f4 *>(&circatt_lds[o0 + c]) = x;
+                    n2 += x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
                 }
                 if (NTEN > 1) {
 #pragma unroll
@@ -496,6 +492,7 @@ __global__ __launch_bounds__(256, 2) void fused_kernel(FArgs a) {
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
                 reg0[s] = nr0[s];
+                if constexpr (DIST) reg0[s] -= circatt_lds[oMU + 16 * (s >> 2) + 4 * g + (s & 3)];
                 if (TWO) reg1[s] = nr1[s];
             }
             float qq = 0.f, dd = 0.f;
