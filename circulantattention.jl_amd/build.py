@@ -23,7 +23,9 @@ ARCH = "gfx950"
 SOURCES = ["api.cpp", "unfused.hip", "apply_rb.hip", "fused.hip", "fused_fwd.hip", "fused_sim.hip",
            "fused_bwdq.hip", "fused_bwdkv.hip", "fused2d_fwd.hip", "fused2d_bwdq.hip",
            "fused2d_bwdkv.hip", "fused2h_fwd.hip", "fused2h_bwdq.hip", "fused2h_bwdkv.hip",
-           "fused2h2_fwd.hip", "fused2h2_bwdq.hip", "fused2h2_bwdkv.hip", "fused_wide.hip",
+           "fused2h2_fwd.hip", "fused2h2_bwdq.hip", "fused2h2_bwdkv.hip", "fused1h_fwd.hip",
+           "fused1h_bwdq.hip", "fused1h_bwdkv.hip", "fused1h2_fwd.hip", "fused1h2_bwdq.hip",
+           "fused1h2_bwdkv.hip", "fused_wide.hip",
            "batch_ops.hip"]
 FLAGS = [
     f"--offload-arch={ARCH}",

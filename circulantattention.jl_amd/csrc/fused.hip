@@ -144,7 +144,11 @@ bool fused_supported(FusedMode mode, const FusedProblem &pr) {
 // hipErrorNotSupported otherwise.
 hipError_t launch_f2d(FusedMode mode, const FusedProblem &pr, hipStream_t s) {
     const int ncr = pr.dh * pr.ncomp;
-    if (mode == MODE_SIM || !f2d::supported(pr.g.nsp, pr.g.p, ncr, pr.g.P) ||
+    // one-dimensional signals: the split-half kernels of the windows they
+    // instantiate (no Float32 matrix-core counterpart)
+    const bool one = pr.g.nsp == 1 && math_mode() == CIRCATT_MATH_SPLIT_F16 &&
+                     f2h::supported1(pr.g.p, ncr) && pr.g.P * ncr * 4 < (int64_t)INT32_MAX;
+    if (mode == MODE_SIM || !(one || f2d::supported(pr.g.nsp, pr.g.p, ncr, pr.g.P)) ||
         pr.nunits > INT32_MAX)
         return hipErrorNotSupported;
     f2d::Args a{};
@@ -164,6 +168,16 @@ hipError_t launch_f2d(FusedMode mode, const FusedProblem &pr, hipStream_t s) {
     const int nt = ncr / 16;
     const bool cplx = pr.ncomp == 2, dist = pr.kind == 1;
     const int cus = device_cus();
+    if (one) {
+        if (nt == 1) {
+            if (mode == MODE_FWD) return launch_f1h_fwd(pr.g.p, cplx, dist, a, cus, s);
+            if (mode == MODE_BWDQ) return launch_f1h_bwdq(pr.g.p, cplx, dist, a, cus, s);
+            return launch_f1h_bwdkv(pr.g.p, cplx, dist, a, cus, s);
+        }
+        if (mode == MODE_FWD) return launch_f1h2_fwd(pr.g.p, cplx, dist, a, cus, s);
+        if (mode == MODE_BWDQ) return launch_f1h2_bwdq(pr.g.p, cplx, dist, a, cus, s);
+        return launch_f1h2_bwdkv(pr.g.p, cplx, dist, a, cus, s);
+    }
     if (nt == 1 && math_mode() == CIRCATT_MATH_SPLIT_F16) {
         hipError_t e = hipErrorNotSupported;
         if (mode == MODE_FWD) e = launch_f2h_fwd(pr.g.p, cplx, dist, a, cus, s);

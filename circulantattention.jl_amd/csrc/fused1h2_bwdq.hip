@@ -1,0 +1,12 @@
+// Instantiations of the split-half kernels for one-dimensional signals,
+// query-centric backward, 32 real components per head (fused2h_impl.h).
+#include "fused2h_impl.h"
+
+namespace circatt {
+
+hipError_t launch_f1h2_bwdq(int p, bool cplx, bool dist, const f2d::Args &a, int cus,
+                            hipStream_t s) {
+    return f2h::dispatch1<f2h::BWDQ, 2>(p, cplx, dist, a, cus, s);
+}
+
+}  // namespace circatt

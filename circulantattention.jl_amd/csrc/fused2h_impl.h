@@ -284,31 +284,41 @@ enum { FWD = f2d::FWD, BWDQ = f2d::BWDQ, BWDKV = f2d::BWDKV };
 // BR * NKH - (8 + 2P) rows past the staged ones, into the pad rows of the
 // column; those rows, and staged-region columns past the last staged one,
 // hold zeros written once per launch and are read only under the mask.
-template <int P, int NT>
+//
+// One-dimensional signals (ONE): a wavefront holds 16 consecutive register
+// pixels and walks 16x1 LDS blocks (BR = 16) of the 16 + 2P keys around them;
+// the workgroup's wavefronts are stacked along the line (TH = 16 per
+// wavefront, TW = 1) and the staged halo is one slot column of TH + 2P pixels,
+// padded with zero slots to the end of the last wavefront's last block.
+template <int P, int NT, bool ONE = false>
 struct HGeo {
-    static constexpr int WH = grid_wh<NT>(), WW = 8;
+    static constexpr int WH = ONE ? 8 * grid_wh<NT>() : grid_wh<NT>(), WW = ONE ? 1 : 8;
     static constexpr int THREADS = 64 * WH * WW;
-    static constexpr int TH = 8 * WH, TW = 2 * WW;
-    static constexpr int BR = (P == 1 || P == 5) ? 4 : 2;  // block rows
+    static constexpr int TH = ONE ? 16 * WH : 8 * WH, TW = ONE ? 1 : 2 * WW;
+    static constexpr int BR = ONE ? 16 : (P == 1 || P == 5) ? 4 : 2;  // block rows
     static constexpr int BC = 16 / BR;                                   // block columns
-    static constexpr int NKH = (8 + 2 * P + BR - 1) / BR;
-    static constexpr int NKW = (2 + 2 * P + BC - 1) / BC;
+    static constexpr int NKH = ONE ? (16 + 2 * P + 15) / 16 : (8 + 2 * P + BR - 1) / BR;
+    static constexpr int NKW = ONE ? 1 : (2 + 2 * P + BC - 1) / BC;
     static constexpr int NBLK = NKH * NKW;
     static constexpr int HH = TH + 2 * P;
-    static constexpr int HWD = 2 * (WW - 1) + BC * NKW;
-    static constexpr int CR = BR == 2 ? HH + ((2 - HH % 4) + 4) % 4     // LDS column stride
-                                      : HH + ((4 - HH % 16) + 16) % 16;
+    static constexpr int HWD = ONE ? 1 : 2 * (WW - 1) + BC * NKW;
+    static constexpr int CR = ONE     ? 16 * (WH - 1) + 16 * NKH   // LDS column stride
+                              : BR == 2 ? HH + ((2 - HH % 4) + 4) % 4
+                                        : HH + ((4 - HH % 16) + 16) % 16;
     static constexpr int LPX = CR * HWD;                    // LDS pixel slots per tensor
     // slot offset of block b within a wavefront's region
     static constexpr int bslot(int b) { return BR * (b / NKW) + CR * BC * (b % NKW); }
     // index of the scalar of the pixel at slot row `row`, column `col`, and
     // the scalar offset of block b within a wavefront's region
     static constexpr int sidx(int row, int col) { return BR == 2 ? col + HWD * row : row + CR * col; }
+    // first slot row of wavefront row wh's region
+    static constexpr int wrow(int wh) { return ONE ? 16 * wh : 8 * wh; }
     static constexpr int sbslot(int b) { return sidx(BR * (b / NKW), BC * (b % NKW)); }
     // central pair of the streamed forward: two blocks of the block row that
     // holds key rows 8, 9 (in every query's window when 2P >= 9)
     static constexpr int PCENT = (8 / BR) * NKW / 2;
-    static_assert(8 * (WH - 1) + BR * NKH <= CR, "a wavefront's blocks stay within their column's slots");
+    static_assert(wrow(WH - 1) + BR * NKH <= CR, "a wavefront's blocks stay within their column's slots");
+    static_assert(HH <= CR, "the staged rows fit the column");
     static_assert((8 / BR) * NKW % 2 == 0, "the central pair lies in one block row");
 };
 static_assert(HGeo<5, 2>::LPX == 520 && HGeo<5, 2>::NBLK == 15, "4x4 blocks at ws 11");
@@ -317,14 +327,16 @@ static_assert(HGeo<7, 1>::LPX == f2d::Geo<7, 1, 2, 8>::LPX && HGeo<7, 1>::NBLK =
 
 // lane j + 16 g holds query (j % 8, j / 8) and key element 4 g + r of block
 // (bi, bj); bit set where the key lies in the query's window
+// (BR = 16: 16x1 register and LDS blocks of a one-dimensional signal, element
+// 4 g + r of block bi at row 16 bi + 4 g + r, query j at row j)
 template <int BR>
 __host__ __device__ constexpr uint64_t hmask(int P, int bi, int bj, int r) {
     uint64_t m = 0;
     for (int lane = 0; lane < 64; ++lane) {
         const int j = lane & 15, g = lane >> 4;
-        const int kr = BR == 2 ? 2 * bi + (g >> 1) : 4 * bi + r;
-        const int kc = BR == 2 ? 8 * bj + 4 * (g & 1) + r : 4 * bj + g;
-        const int u1 = kr - (j & 7), u2 = kc - (j >> 3);
+        const int kr = BR == 16 ? 16 * bi + 4 * g + r : BR == 2 ? 2 * bi + (g >> 1) : 4 * bi + r;
+        const int kc = BR == 16 ? 0 : BR == 2 ? 8 * bj + 4 * (g & 1) + r : 4 * bj + g;
+        const int u1 = kr - (BR == 16 ? j : j & 7), u2 = kc - (BR == 16 ? 0 : j >> 3);
         if (u1 >= 0 && u1 <= 2 * P && u2 >= 0 && u2 <= 2 * P) m |= 1ull << lane;
     }
     return m;
@@ -332,9 +344,22 @@ __host__ __device__ constexpr uint64_t hmask(int P, int bi, int bj, int r) {
 // the Float32 kernels (f2d::lane_mask) keep the 2x2 element groups
 static_assert(hmask<2>(7, 3, 1, 2) != f2d::lane_mask(7, 3, 1, 2), "row-major 2x8 elements");
 
-template <int P, int NT, int MODE, bool DIST>
+// WIDE (one-dimensional planar Float32 signals whose length is a multiple of
+// 4): the next item's halo and register pixels arrive by 16-byte LDS-DMA
+// loads (4 pixels of one channel per lane) into planar buffers, XS (staged
+// tensors: channel-major rows of NXS pixels from the halo origin rounded down
+// to a multiple of 4, XA pixels earlier) and XR (register tensors: rows of the
+// tile's TH pixels), which the staging and the register set-up read.  A lane
+// of a dword load moves 4 bytes, and a wavefront can keep only so many loads
+// in flight: with the short walks of a one-dimensional window the dword loads
+// of the staged and register pixels bounded the passes.
+template <int P, int NT, int MODE, bool DIST, bool ONE = false, bool WIDE = false>
 struct LGeo {
-    using G = HGeo<P, NT>;
+    using G = HGeo<P, NT, ONE>;
+    static constexpr int NCH = 16 * NT;                                // real components per pixel
+    static constexpr int XA = (4 - P % 4) % 4;                         // halo origin - XS origin
+    static constexpr int NXS = (G::HH + XA + 3) / 4 * 4;               // XS pixels per row
+    static constexpr int NRT = MODE == FWD ? 1 : MODE == BWDQ ? 3 : 2;  // register tensors
     static constexpr int SB = slot_bytes<NT>();
     static constexpr int OT0 = 0;                  // tensor 0 slots (K, or Q in BWDKV)
     static constexpr int OT1 = G::LPX * SB;        // tensor 1 slots (V, or dY in BWDKV)
@@ -343,15 +368,20 @@ struct LGeo {
     static constexpr int NSCAL = MODE == BWDKV ? 2 : (DIST ? 1 : 0);
     // per-item exchange of maxima: 4 words of (item << 9 | biased exponent)
     static constexpr int OX = OS0 + NSCAL * G::LPX * 4;
-    static constexpr int bytes = OX + 16;
+    static constexpr int OXS = OX + 16;                         // (WIDE) staged tensors, planar
+    static constexpr int OXR = OXS + (WIDE ? 2 * NCH * NXS * 4 : 0);  // (WIDE) register tensors
+    static constexpr int bytes = OXR + (WIDE ? NRT * NCH * G::TH * 4 : 0);
+    static_assert(!WIDE || (ONE && G::TH <= 256), "register rows: one DMA instruction per channel");
 };
 
-// NT: 16-channel sub-pixels per pixel (1 or 2, i.e. 16 or 32 real components)
-template <int P, int NT, bool CPLX, bool DIST, int MODE, bool CL>
-__global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
-    constexpr int WH = grid_wh<NT>();
-    using G = HGeo<P, NT>;
-    using L = LGeo<P, NT, MODE, DIST>;
+// NT: 16-channel sub-pixels per pixel (1 or 2, i.e. 16 or 32 real components);
+// ONE: one-dimensional signal (n2 = 1)
+template <int P, int NT, bool CPLX, bool DIST, int MODE, bool CL, bool ONE = false, bool WIDE = false>
+__global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args a) {
+    using G = HGeo<P, NT, ONE>;
+    using L = LGeo<P, NT, MODE, DIST, ONE, WIDE>;
+    static_assert(!WIDE || (ONE && !CPLX && !CL), "planar DMA rows: one-dimensional planar Float32");
+    constexpr int WH = G::WH;
     constexpr int BR = G::BR;
     constexpr int SB = L::SB;
     constexpr int CR = G::CR, HH = G::HH, HWD = G::HWD, NKW = G::NKW, NBLK = G::NBLK;
@@ -359,7 +389,7 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
     // tile only the TW + 2P that lie in some query's window (the slot columns
     // past them are read by the last LDS blocks under the window mask and
     // hold zeros, written once)
-    constexpr int SWC = NT == 1 ? HWD : G::TW + 2 * P;
+    constexpr int SWC = ONE ? 1 : NT == 1 ? HWD : G::TW + 2 * P;
     constexpr int NPX = HH * SWC;
     constexpr int NPAIR = (NBLK + 1) / 2;
     constexpr bool KV = MODE == BWDKV;
@@ -391,6 +421,12 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
                                                     : NPAIR / CIRCATT_F2H_BWD_PFD;
     static_assert(PFP >= 0 && PFP < NPAIR, "the next item's loads must be issued in the walk");
     static_assert(NPX <= G::THREADS, "one staged pixel per thread");
+    // HALF: two threads per staged pixel of 32 components, one sub-pixel of
+    // 16 each (where the halo has at most half as many pixels as the
+    // workgroup has threads: one-dimensional signals), so that the staging
+    // loads spread over more wavefronts; NCS components staged per thread
+    constexpr bool HALF = NT == 2 && 2 * NPX <= G::THREADS;
+    constexpr int NCS = HALF ? 16 : 16 * NT;
     static_assert(NT == 1 || NT == 2, "16 or 32 real components per head");
     static_assert(HH % 2 == 0, "row pairs");
     char *const lds = reinterpret_cast<char *>(circatt_lds2);
@@ -398,35 +434,38 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int wh = wv % WH, ww = wv / WH;
     const int j = lane & 15, g = lane >> 4;
-    const int jh = j & 7, jw = j >> 3;
+    const int jh = ONE ? j : j & 7, jw = ONE ? 0 : j >> 3;
 
     auto opaque = [](int v) {
         asm volatile("" : "+v"(v));
         return v;
     };
     // score-type rows: element j of a block, halves 8 g .. 8 g + 7 of its slot
-    const int slotA = BR == 2 ? 8 * wh + (j >> 3) + CR * (2 * ww + (j & 7))
-                              : 8 * wh + (j & 3) + CR * (2 * ww + (j >> 2));
+    const int slotA = ONE       ? G::wrow(wh) + j
+                      : BR == 2 ? 8 * wh + (j >> 3) + CR * (2 * ww + (j & 7))
+                                : 8 * wh + (j & 3) + CR * (2 * ww + (j >> 2));
     const char *const pA0 = lds + opaque(L::OT0 + slotA * SB + 16 * g);
     const char *const pA1 = lds + opaque(L::OT1 + slotA * SB + 16 * g);
     // apply-type rows from slots by transposing reads: lane (j, g) receives
     // channel j (hi; lo 16 halves further) of elements 4g + t, t = 0..3, so
     // lane j of group g addresses channels 4 (j & 3) .. + 3 of element
     // 4g + (j >> 2), which sits at row g / 2, column 4 (g % 2) + (j >> 2)
-    // (2x8) or at row j >> 2, column g (4x4)
-    const int slotE = BR == 2 ? 8 * wh + (g >> 1) + CR * (2 * ww + 4 * (g & 1))
-                              : 8 * wh + CR * (2 * ww + g);
+    // (2x8), at row j >> 2, column g (4x4) or at row 4g + (j >> 2) (16x1)
+    const int slotE = ONE       ? G::wrow(wh) + 4 * g
+                      : BR == 2 ? 8 * wh + (g >> 1) + CR * (2 * ww + 4 * (g & 1))
+                                : 8 * wh + CR * (2 * ww + g);
     const int slotT = BR == 2 ? slotE + CR * (j >> 2) : slotE + (j >> 2);
     const char *const pR0 = lds + opaque(L::OT0 + slotT * SB + 8 * (j & 3));
     const char *const pR1 = lds + opaque(L::OT1 + slotT * SB + 8 * (j & 3));
     // per-slot Float32 scalars of elements 4g .. 4g+3 (adjacent)
-    const int sidxE = BR == 2 ? G::sidx(8 * wh + (g >> 1), 2 * ww + 4 * (g & 1))
-                              : G::sidx(8 * wh, 2 * ww + g);
+    const int sidxE = ONE       ? G::wrow(wh) + 4 * g
+                      : BR == 2 ? G::sidx(8 * wh + (g >> 1), 2 * ww + 4 * (g & 1))
+                                : G::sidx(8 * wh, 2 * ww + g);
     const float *const pS0 = reinterpret_cast<const float *>(lds + opaque(L::OS0 + sidxE * 4));
     const float *const pS1 = reinterpret_cast<const float *>(lds + opaque(L::OS1 + sidxE * 4));
 
     // ---- prefetch registers ----
-    float h0v[16 * NT], h1v[16 * NT], hs0 = 0.f, hs1 = 0.f;
+    float h0v[NCS], h1v[NCS], hs0 = 0.f, hs1 = 0.f;
     int hslot;
     // register operands: lane groups g and g ^ 2 (lanes l, l ^ 32) share a
     // pixel and its channels 8 (g & 1) .. + 7 of each sub-pixel h; each loads
@@ -440,7 +479,7 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
 
     // register pixel of this lane in the tile at (h0, w0)
     auto regpix = [&](int h0, int w0, bool &rvalid, int &rpix) {
-        const int rh = h0 + 8 * wh + jh, rw = w0 + 2 * ww + jw;
+        const int rh = h0 + G::wrow(wh) + jh, rw = w0 + 2 * ww + jw;
         rvalid = rh < a.n1 && rw < a.n2;
         rpix = rvalid ? rh + a.n1 * rw : 0;
     };
@@ -454,12 +493,17 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         w0 = tw * G::TW;
     };
     const bool big = a.n1 >= HH && a.n2 >= HWD;
-    const int px = threadIdx.x;
+    const int px = HALF ? threadIdx.x >> 1 : threadIdx.x;
+    const int hsub = HALF ? threadIdx.x & 1 : 0;  // staged sub-pixel (HALF)
     const int kw = px / HH, kh = px - kw * HH;
     const int hsid = G::sidx(kh, kw);  // scalar index of the staged pixel
-    auto load_stage = [&](int unit, int h0, int w0) {
+    // wavefronts with no staged pixel issue no staging loads (one-dimensional
+    // halos only: in 2D every wavefront or all but one stage pixels, and the
+    // branch would split the walk's basic block around the prefetch)
+    const bool stw = !ONE || (HALF ? 32 * wv : 64 * wv) < NPX;
+    auto load_stage = [&](int unit, int h0, int w0) __attribute__((always_inline)) {
         // halo origin (h0 - P, w0 - P) mod (n1, n2), uniform
-        int hsh = h0 - P, wsh = w0 - P;
+        int hsh = h0 - P, wsh = ONE ? 0 : w0 - P;
         while (hsh < 0) hsh += a.n1;
         while (wsh < 0) wsh += a.n2;
         const int64_t uoff = f2d::unit_base<CL>(a, unit);
@@ -467,6 +511,40 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         const auto r0 = f2d::rsrc((KV ? a.q : a.k) + uoff, ubytes);
         const auto r1 = f2d::rsrc((KV ? a.dy : a.v) + uoff, ubytes);
         hslot = px < NPX ? kh + CR * kw : -1;
+        if constexpr (WIDE) {
+            // this wavefront's share of the XS rows: instruction i = (tensor,
+            // channel, part of 256 pixels); lane l of part m loads pixels
+            // o4 + 4 (64 m + l) .. + 3 (mod n1: o4 and n1 are multiples of 4, so
+            // no chunk straddles the wrap)
+            constexpr int NPART = (L::NXS + 255) / 256, NI = 2 * L::NCH * NPART;
+            constexpr int NW = G::THREADS / 64, KW = (NI + NW - 1) / NW;
+            const int o4 = hsh >= L::XA ? hsh - L::XA : hsh - L::XA + a.n1;
+            const bool bigx = a.n1 >= L::NXS;
+#pragma unroll
+            for (int kk = 0; kk < KW; ++kk) {
+                const int i = wv + NW * kk;
+                if (i < NI) {
+                    const int part = i % NPART, tc = i / NPART;
+                    const int t = tc / L::NCH, c = tc - t * L::NCH;
+                    const int l4 = 64 * part + lane;
+                    int p4 = o4 + 4 * l4;
+                    p4 = bigx ? (p4 >= a.n1 ? p4 - a.n1 : p4) : p4 % a.n1;
+                    typedef __attribute__((address_space(3))) void *lptr;
+                    char *const dst = lds + L::OXS + ((t * L::NCH + c) * L::NXS + 256 * part) * 4;
+                    if (l4 < L::NXS / 4)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(t ? r1 : r0, (lptr)dst, 16,
+                                                                (p4 + c * a.P) * 4, 0, 0, 0);
+                }
+            }
+        }
+        if (!stw) {
+            // (zeros rather than an early return, which would keep the
+            // previous item's values live across the walk)
+#pragma unroll
+            for (int c = 0; c < NCS; ++c) h0v[c] = h1v[c] = 0.f;
+            hs0 = hs1 = 0.f;
+            return;
+        }
         int gh = hsh + kh, gw = wsh + kw;
         if (big) {
             gh -= gh >= a.n1 ? a.n1 : 0;
@@ -476,10 +554,15 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
             gw %= a.n2;
         }
         const int gp = gh + a.n1 * gw;
-        if constexpr (CPLX) {
+        // (component offsets are linear in the component, so the sub-pixel's
+        // first one joins the per-lane offset)
+        if constexpr (WIDE) {
+            // (read from the XS rows at the item's start)
+        } else if constexpr (CPLX) {
+            const int vb = (f2d::pix_off<true, CL>(a, gp) + f2d::comp_soff<true, CL>(a, 16 * hsub)) * 4;
 #pragma unroll
-            for (int c = 0; c < 8 * NT; ++c) {
-                const int vo = f2d::pix_off<true, CL>(a, gp) * 4, so = f2d::comp_soff<true, CL>(a, 2 * c) * 4;
+            for (int c = 0; c < NCS / 2; ++c) {
+                const int vo = vb, so = f2d::comp_soff<true, CL>(a, 2 * c) * 4;
                 const f2d::f2 x0 = f2d::bload2(r0, vo, so);
                 const f2d::f2 x1 = f2d::bload2(r1, vo, so);
                 h0v[2 * c] = x0[0];
@@ -488,9 +571,10 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
                 h1v[2 * c + 1] = x1[1];
             }
         } else {
+            const int vb = (f2d::pix_off<false, CL>(a, gp) + f2d::comp_soff<false, CL>(a, 16 * hsub)) * 4;
 #pragma unroll
-            for (int c = 0; c < 16 * NT; ++c) {
-                const int vo = f2d::pix_off<false, CL>(a, gp) * 4, so = f2d::comp_soff<false, CL>(a, c) * 4;
+            for (int c = 0; c < NCS; ++c) {
+                const int vo = vb, so = f2d::comp_soff<false, CL>(a, c) * 4;
                 h0v[c] = f2d::bload(r0, vo, so);
                 h1v[c] = f2d::bload(r1, vo, so);
             }
@@ -501,7 +585,7 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
             hs1 = f2d::bload(f2d::rsrc(a.dbuf + soff, a.P * 4), gp * 4, 0);
         }
     };
-    auto load_regs = [&](int unit, int h0, int w0) {
+    auto load_regs = [&](int unit, int h0, int w0) __attribute__((always_inline)) {
         bool rvalid;
         int rpix;
         regpix(h0, w0, rvalid, rpix);
@@ -509,8 +593,28 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         const int ubytes = f2d::unit_bytes<CL>(a, unit);
         const auto r0 = f2d::rsrc((KV ? a.k : a.q) + uoff, ubytes);
         const auto r1 = f2d::rsrc((KV ? a.v : a.dy) + uoff, ubytes);
+        if constexpr (WIDE) {
+            // this wavefront's share of the XR rows: instruction i = (tensor,
+            // channel); lane l loads the tile's pixels h0 + 4l .. + 3 (those past
+            // n1 belong to no register pixel)
+            constexpr int NI = L::NRT * L::NCH;
+            constexpr int NW = G::THREADS / 64, KW = (NI + NW - 1) / NW;
+            const auto ry = f2d::rsrc(a.y + uoff, ubytes);
 #pragma unroll
-        for (int h = 0; h < NT; ++h) {
+            for (int kk = 0; kk < KW; ++kk) {
+                const int i = wv + NW * kk;
+                if (i < NI) {
+                    const int rt = i / L::NCH, c = i - rt * L::NCH;
+                    typedef __attribute__((address_space(3))) void *lptr;
+                    char *const dst = lds + L::OXR + (rt * L::NCH + c) * G::TH * 4;
+                    if (lane < G::TH / 4)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(rt == 0 ? r0 : rt == 1 ? r1 : ry, (lptr)dst,
+                                                                16, (h0 + 4 * lane + c * a.P) * 4, 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < NT && !WIDE; ++h) {
             const int vo = f2d::comp_off<CPLX, CL>(a, rpix, 16 * h + 8 * (g & 1) + 4 * (g >> 1)) * 4;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -534,7 +638,7 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
     F2H_PHASE(uint64_t phase[4] = {0, 0, 0, 0};)
     unsigned *const xwords = reinterpret_cast<unsigned *>(lds + L::OX);
     if (threadIdx.x < 4) xwords[threadIdx.x] = 0u;
-    if constexpr (NT == 2 || BR == 4) {
+    if constexpr (NT == 2 || BR == 4 || ONE) {
         // slots never staged (pad rows, columns past the staged ones): zero
         // halves and scalars, so that the masked products over them stay
         // finite
@@ -559,6 +663,31 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         bool rvalid;
         int rpix;
         regpix(h0, w0, rvalid, rpix);
+        if constexpr (WIDE) {
+            // the item's rows are in LDS once every wavefront's loads are
+            // (vmcnt(0): the DMA writes count as this wavefront's loads)
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            const float *const xs = reinterpret_cast<const float *>(lds + L::OXS);
+            const float *const xr = reinterpret_cast<const float *>(lds + L::OXR);
+            const int xp = min(px, NPX - 1) + L::XA;
+#pragma unroll
+            for (int c = 0; c < NCS; ++c) {
+                h0v[c] = xs[(16 * hsub + c) * L::NXS + xp];
+                h1v[c] = xs[(L::NCH + 16 * hsub + c) * L::NXS + xp];
+            }
+            // register pixels past n1 read zeros
+            const int rp = G::wrow(wh) + j;
+#pragma unroll
+            for (int h = 0; h < NT; ++h)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int comp = 16 * h + 8 * (g & 1) + 4 * (g >> 1) + t;
+                    nh0[h][t] = rvalid ? xr[comp * G::TH + rp] : 0.f;
+                    if constexpr (MODE != FWD) nh1[h][t] = rvalid ? xr[(L::NCH + comp) * G::TH + rp] : 0.f;
+                    if constexpr (MODE == BWDQ) nry[h][t] = rvalid ? xr[(2 * L::NCH + comp) * G::TH + rp] : 0.f;
+                }
+        }
         const int64_t uoff = f2d::unit_base<CL>(a, unit);
         const int64_t soff = (int64_t)unit * a.P;
         const float c2 = a.c2;
@@ -570,8 +699,15 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         // and the gradient terms dS (k - q) are unchanged.
         if constexpr (DIST) {
 #pragma unroll
-            for (int c = 0; c < 16 * NT; ++c)
-                h0v[c] -= __int_as_float(__builtin_amdgcn_readlane(__float_as_int(nmu), c));
+            for (int c = 0; c < NCS; ++c) {
+                const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(nmu), c));
+                if constexpr (HALF) {
+                    const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(nmu), 16 + c));
+                    h0v[c] -= hsub ? m1 : m0;
+                } else {
+                    h0v[c] -= m0;
+                }
+            }
 #pragma unroll
             for (int h = 0; h < NT; ++h)
 #pragma unroll
@@ -617,15 +753,22 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         const unsigned b2 = KV ? __builtin_amdgcn_readfirstlane(xwords[2]) & 255u : 127u;
         // shifts of the staged tensors (k or q; v or dy) and of the register v
         const int s0 = shift_of(b0), s1 = shift_of(b1), s2 = KV ? shift_of(b2) : 0;
-        if (hslot >= 0) {
-            float n2 = 0.f;
-            if constexpr (DIST) {
+        // |k - mu|^2 of the staged pixel (HALF: the two sub-pixel threads of
+        // a pixel are adjacent lanes)
+        float n2 = 0.f;
+        if constexpr (DIST) {
 #pragma unroll
-                for (int c = 0; c < 16 * NT; ++c) n2 += h0v[c] * h0v[c];
-            }
+            for (int c = 0; c < NCS; ++c) n2 += h0v[c] * h0v[c];
+            if constexpr (HALF) n2 += __shfl_xor(n2, 1);
+        }
+        if (hslot >= 0) {
             char *const sl0 = lds + L::OT0 + hslot * SB;
             char *const sl1 = lds + L::OT1 + hslot * SB;
-            if constexpr (NT == 1) {
+            if constexpr (HALF) {
+                // this thread's sub-pixel at byte 64 hsub of the slot
+                if (s0 == 0) store_slot(sl0 + 64 * hsub, h0v); else store_slot<true>(sl0 + 64 * hsub, h0v, s0);
+                if (s1 == 0) store_slot(sl1 + 64 * hsub, h1v); else store_slot<true>(sl1 + 64 * hsub, h1v, s1);
+            } else if constexpr (NT == 1) {
                 if (s0 == 0) store_slot(sl0, h0v); else store_slot<true>(sl0, h0v, s0);
                 if (s1 == 0) store_slot(sl1, h1v); else store_slot<true>(sl1, h1v, s1);
             } else {
@@ -642,15 +785,17 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
                     if (s1 == 0) store_slot(sl1 + 64 * h, x1[h]); else store_slot<true>(sl1 + 64 * h, x1[h], s1);
                 }
             }
-            if constexpr (KV) {
-                // staged queries: A_q = -lse log2(e) [- c2 |q|^2 / 2], and
-                // -D in the scale of the dP product
-                reinterpret_cast<float *>(lds + L::OS0)[hsid] =
-                    -hs0 * kLog2e - (DIST ? 0.5f * c2 * n2 : 0.f);
-                reinterpret_cast<float *>(lds + L::OS1)[hsid] =
-                    -__builtin_amdgcn_ldexpf(hs1, s1 + s2);
-            } else if constexpr (DIST) {
-                reinterpret_cast<float *>(lds + L::OS0)[hsid] = -0.5f * c2 * n2;  // key bias
+            if (hsub == 0) {
+                if constexpr (KV) {
+                    // staged queries: A_q = -lse log2(e) [- c2 |q|^2 / 2], and
+                    // -D in the scale of the dP product
+                    reinterpret_cast<float *>(lds + L::OS0)[hsid] =
+                        -hs0 * kLog2e - (DIST ? 0.5f * c2 * n2 : 0.f);
+                    reinterpret_cast<float *>(lds + L::OS1)[hsid] =
+                        -__builtin_amdgcn_ldexpf(hs1, s1 + s2);
+                } else if constexpr (DIST) {
+                    reinterpret_cast<float *>(lds + L::OS0)[hsid] = -0.5f * c2 * n2;  // key bias
+                }
             }
         }
         // register operands (the score product's side pre-scaled by c2):
@@ -748,7 +893,14 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
 #pragma unroll
             for (int h = 0; h < NT; ++h)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) reg0[h][r] = __shfl((g & 2) ? nr0[h][4 + r] : nr0[h][r], srcl);
+                for (int r = 0; r < 4; ++r) {
+                    // (the two values pass through registers first: a select
+                    // of two array elements would become a load at a
+                    // lane-dependent index, putting nr0 in scratch memory)
+                    float lo = nr0[h][r], hi = nr0[h][4 + r];
+                    asm volatile("" : "+v"(lo), "+v"(hi));
+                    reg0[h][r] = __shfl((g & 2) ? hi : lo, srcl);
+                }
         }
         F2H_PHASE(const uint64_t ptc = __builtin_readcyclecounter();)
         __syncthreads();  // halo staged
@@ -761,7 +913,7 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
         // prefetch registers are dead between the staging and this point
         int xunit = unit, xh0 = h0, xw0 = w0;
         if (has_next) decode(nitem, xunit, xh0, xw0);
-        auto prefetch = [&]() {
+        auto prefetch = [&]() __attribute__((always_inline)) {
             load_stage(xunit, xh0, xw0);
             load_regs(xunit, xh0, xw0);
         };
@@ -1181,12 +1333,15 @@ __global__ __launch_bounds__(64 * 8 * grid_wh<NT>(), 1) void kernel2h(Args a) {
 #endif
 }
 
-template <int P, int NT, bool CPLX, bool DIST, int MODE, bool CL>
+template <int P, int NT, bool CPLX, bool DIST, int MODE, bool CL, bool ONE = false, bool WIDE = false>
 hipError_t launch2h(const Args &a0, int cus, hipStream_t s) {
-    using G = f2d::Geo<P, 1, grid_wh<NT>(), 8>;
-    constexpr int bytes = LGeo<P, NT, MODE, DIST>::bytes;
+    using G = HGeo<P, NT, ONE>;
+    static_assert(ONE || (G::TH == f2d::Geo<P, 1, grid_wh<NT>(), 8>::TH &&
+                          G::TW == f2d::Geo<P, 1, grid_wh<NT>(), 8>::TW),
+                  "2D tiles as the Float32 kernels'");
+    constexpr int bytes = LGeo<P, NT, MODE, DIST, ONE, WIDE>::bytes;
     static_assert(bytes <= (int)f2d::kLdsCap, "halo does not fit LDS");
-    auto kern = kernel2h<P, NT, CPLX, DIST, MODE, CL>;
+    auto kern = kernel2h<P, NT, CPLX, DIST, MODE, CL, ONE, WIDE>;
     // set once per instantiation (a function-local static is initialised
     // exactly once, also when several host threads launch at the same time)
     static const hipError_t attr = hipFuncSetAttribute(
@@ -1235,6 +1390,42 @@ hipError_t dispatch(int p, bool cplx, bool dist, const Args &a, int cus, hipStre
     return hipErrorNotSupported;
 }
 
+// Planar real signals whose length is a multiple of 4, on 16-byte aligned
+// tensors: staged and register rows loaded by 16-byte DMA into LDS
+inline bool wide_rows(const Args &a, bool cplx) {
+    if (cplx || a.cl || a.n1 % 4 != 0) return false;
+    uintptr_t bits = 0;
+    for (const float *p : {a.q, a.k, a.v, a.dy, a.y}) bits |= reinterpret_cast<uintptr_t>(p);
+    return (bits & 15) == 0;
+}
+
+// One-dimensional signals: windows 15 and 63, 16 or 32 real components per
+// head (the run-time-window kernel covers the others)
+template <int MODE, int NT>
+hipError_t dispatch1(int p, bool cplx, bool dist, const Args &a, int cus, hipStream_t s) {
+#define CIRCATT_F1H_CL(PP, CLL)                                                          \
+    {                                                                                    \
+        if (!CLL && wide_rows(a, cplx))                                                 \
+            return dist ? launch2h<PP, NT, false, true, MODE, false, true, true>(a, cus, s) \
+                        : launch2h<PP, NT, false, false, MODE, false, true, true>(a, cus, s); \
+        if (cplx) return dist ? launch2h<PP, NT, true, true, MODE, CLL, true>(a, cus, s)   \
+                              : launch2h<PP, NT, true, false, MODE, CLL, true>(a, cus, s); \
+        return dist ? launch2h<PP, NT, false, true, MODE, CLL, true>(a, cus, s)            \
+                    : launch2h<PP, NT, false, false, MODE, CLL, true>(a, cus, s);          \
+    }
+#define CIRCATT_F1H_CASE(PP)                                                             \
+    if (p == PP) {                                                                       \
+        if (a.cl) CIRCATT_F1H_CL(PP, true)                                               \
+        CIRCATT_F1H_CL(PP, false)                                                        \
+    }
+    CIRCATT_F1H_CASE(7)
+    CIRCATT_F1H_CASE(31)
+#undef CIRCATT_F1H_CASE
+#undef CIRCATT_F1H_CL
+    return hipErrorNotSupported;
+}
+inline bool supported1(int p, int ncr) { return (p == 7 || p == 31) && (ncr == 16 || ncr == 32); }
+
 }  // namespace f2h
 
 // 16 real components per head (fused2h_*.hip) and 32 (fused2h2_*.hip)
@@ -1244,5 +1435,13 @@ hipError_t launch_f2h_bwdkv(int p, bool cplx, bool dist, const f2d::Args &a, int
 hipError_t launch_f2h2_fwd(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
 hipError_t launch_f2h2_bwdq(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
 hipError_t launch_f2h2_bwdkv(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
+// one-dimensional signals (fused1h_*.hip: 16 real components per head,
+// fused1h2_*.hip: 32)
+hipError_t launch_f1h_fwd(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
+hipError_t launch_f1h_bwdq(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
+hipError_t launch_f1h_bwdkv(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
+hipError_t launch_f1h2_fwd(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
+hipError_t launch_f1h2_bwdq(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
+hipError_t launch_f1h2_bwdkv(int p, bool cplx, bool dist, const f2d::Args &a, int cus, hipStream_t s);
 
 }  // namespace circatt

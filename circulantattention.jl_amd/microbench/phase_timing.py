@@ -27,14 +27,17 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 F2H16 = ("fused2h_fwd.hip", "fused2h_bwdq.hip", "fused2h_bwdkv.hip")
 F2H32 = ("fused2h2_fwd.hip", "fused2h2_bwdq.hip", "fused2h2_bwdkv.hip")
-# name: (spatial n1, n2, channels, batch, heads, window, complex, sources, waves per workgroup)
-CONFIGS = {"cfg3": (256, 256, 64, 4, 4, 15, False, F2H16, 16),
-           "cfg5": (320, 320, 32, 2, 2, 11, True, F2H32, 8)}
+F1H32 = ("fused1h2_fwd.hip", "fused1h2_bwdq.hip", "fused1h2_bwdkv.hip")
+# name: (spatial n1, n2, channels, batch, heads, window, complex, sources, waves per workgroup,
+#        spatial dims, similarity kind)
+CONFIGS = {"cfg3": (256, 256, 64, 4, 4, 15, False, F2H16, 16, 2, 0),
+           "cfg5": (320, 320, 32, 2, 2, 11, True, F2H32, 8, 2, 0),
+           "cfg4b": (262144, 1, 32, 2, 1, 63, False, F1H32, 8, 1, 1)}
 F2H = F2H16
 
 
 def lib_path(no_prio: bool) -> str:
-    tag = "" if F2H is F2H16 else "32"
+    tag = "" if F2H is F2H16 else "32" if F2H is F2H32 else "1d"
     return os.path.join(HERE, f"libcircatt_phase{tag}_noprio.so" if no_prio else f"libcircatt_phase{tag}.so")
 
 
@@ -71,12 +74,12 @@ def run(no_prio: bool) -> None:
     for name, (res, args) in L.SIGNATURES.items():
         f = getattr(lib, name)
         f.restype, f.argtypes = res, args
-    n1, n2, C, B, nh, ws, cplx, _, nw = CONFIGS[CFG]
+    n1, n2, C, B, nh, ws, cplx, _, nw, nsp, kind = CONFIGS[CFG]
     P = n1 * n2
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(1003)
-    shape = (B, C, n2, n1)
+    shape = (B, C, n2, n1) if nsp == 2 else (B, C, n1)
     dt, DT = (torch.complex64, L.C32) if cplx else (torch.float32, L.F32)
     q, k, v, dy = (torch.randn(shape, device=dev, generator=g, dtype=dt) for _ in range(4))
     yb, dqb, dkb, dv = (torch.empty_like(q) for _ in range(4))
@@ -85,20 +88,20 @@ def run(no_prio: bool) -> None:
     lib.circatt_debug_set_phase_buffer.argtypes = [ctypes.c_void_p]
     lib.circatt_debug_set_phase_buffer(ptr(phase))
     lse = torch.empty((B * nh, P), device=dev)
-    wb = lib.circatt_fused_bwd_workspace_bytes(2, n1, n2, nh, B)
+    wb = lib.circatt_fused_bwd_workspace_bytes(nsp, n1, n2, nh, B)
     work = torch.empty((wb // 4,), device=dev)
     s = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
     def fwd():
-        L.check(lib.circatt_fused_fwd(0, DT, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k), ptr(v),
+        L.check(lib.circatt_fused_fwd(kind, DT, nsp, n1, n2, ws, C, nh, B, ptr(q), ptr(k), ptr(v),
                                       ptr(yb), ptr(lse), s))
 
     def bwd_dq():
-        L.check(lib.circatt_fused_bwd_dq(0, DT, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k), ptr(v),
+        L.check(lib.circatt_fused_bwd_dq(kind, DT, nsp, n1, n2, ws, C, nh, B, ptr(q), ptr(k), ptr(v),
                                          ptr(yb), ptr(dy), ptr(lse), ptr(dqb), ptr(work), wb, s))
 
     def bwd_dkdv():
-        L.check(lib.circatt_fused_bwd_dkdv(0, DT, 2, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
+        L.check(lib.circatt_fused_bwd_dkdv(kind, DT, nsp, n1, n2, ws, C, nh, B, ptr(q), ptr(k),
                                            ptr(v), ptr(dy), ptr(lse), ptr(dkb), ptr(dv), ptr(work),
                                            wb, s))
 

@@ -30,6 +30,8 @@ CASES = [
     ((20, 16), 64, 2, 2, 15, 0, False, "split"),    # Float32 matrix cores, 32 components at ws 15
     ((20, 16), 64, 2, 2, 7, 1, False, "f32"),       # Float32 matrix cores, 32 components
     ((150,), 32, 1, 2, 9, 0, False, "split"),       # run-time window, 1D
+    ((260,), 32, 2, 2, 15, 1, False, "split"),      # split-half, 1D, 16 components
+    ((300,), 64, 2, 1, 63, 0, True, "split"),       # split-half, 1D, ComplexF32 32 components
     ((40, 36), 16, 1, 1, 19, 1, False, "split"),    # run-time window, 2D ws 19
     ((18, 14), 128, 2, 1, 5, 0, False, "split"),    # run-time window, 64 components
 ]

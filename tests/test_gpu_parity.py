@@ -263,6 +263,19 @@ ATT_CASES = [
     ((5, 13), 11, 64, 1, 2, 114),
     ((13, 21), 11, 16, 1, 1, 115),
     ((30, 17), 3, 32, 1, 1, 116),
+    # one-dimensional split-half kernels (ws 15 and 63; 16 or 32 real
+    # components per head): partial tiles, signals shorter than a tile,
+    # windows that wrap more than once
+    ((200,), 15, 16, 2, 1, 117),
+    ((50,), 63, 16, 1, 1, 118),
+    ((1000,), 15, 32, 1, 2, 119),
+    ((37,), 15, 32, 2, 1, 120),
+    ((700,), 63, 64, 1, 2, 121),
+    # (real signals whose length is a multiple of 4 take the row-DMA loads:
+    # ws 63 with 16 components, ws 15 with 32, a signal shorter than the halo)
+    ((400,), 63, 16, 1, 1, 122),
+    ((104,), 15, 32, 1, 1, 123),
+    ((24,), 63, 16, 2, 1, 124),
 ]
 
 

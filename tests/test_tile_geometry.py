@@ -126,3 +126,116 @@ def test_banded_tile_order_is_a_bijection_with_compact_runs():
     # 64 consecutive tiles of a full band form an 8 x 8 block
     tiles = [banded_tile(t, 64, 64) for t in range(64 * 5, 64 * 6)]
     assert {h for h, _ in tiles} == set(range(8)) and len({w for _, w in tiles}) == 8
+
+
+# ---- one-dimensional signals (HGeo<P, NT, true>) ----
+
+def geo1(P, NT):
+    """The 1D geometry: 16 (16 real components) or 8 (32) wavefronts of 16
+    register pixels stacked along the line, 16x1 LDS blocks, one slot column."""
+    WH = 16 if NT == 1 else 8
+    TH = 16 * WH
+    NKH = (16 + 2 * P + 15) // 16
+    HH = TH + 2 * P
+    CR = 16 * (WH - 1) + 16 * NKH
+    SB = (32 * NT + 8) * 2
+    return dict(WH=WH, TH=TH, NKH=NKH, HH=HH, CR=CR, SB=SB, THREADS=64 * WH, LPX=CR)
+
+
+CASES1 = [(P, NT) for P in (7, 31) for NT in (1, 2)]
+
+
+def hmask1(P, bi, g, r, j):
+    """Lane mask bit of element 4 g + r of block bi for query j (fused2h_impl.h hmask, BR = 16)."""
+    kr = 16 * bi + 4 * g + r
+    return 0 <= kr - j <= 2 * P
+
+
+@pytest.mark.parametrize("P,NT", CASES1)
+def test_1d_blocks_cover_each_window_once(P, NT):
+    """Query j of a wavefront (pixel h0 + 16 wh + j) meets block bi's element e
+    at slot 16 wh + 16 bi + e, i.e. pixel h0 - P + 16 wh + 16 bi + e: window
+    offset 16 bi + e - P - j.  Under the lane masks every offset -P .. P occurs
+    exactly once per query."""
+    G = geo1(P, NT)
+    for j in range(16):
+        offs = [16 * bi + 4 * g + r - P - j
+                for bi in range(G["NKH"]) for g in range(4) for r in range(4) if hmask1(P, bi, g, r, j)]
+        assert sorted(offs) == list(range(-P, P + 1)), j
+
+
+@pytest.mark.parametrize("P,NT", CASES1)
+def test_1d_reads_stay_in_slots_and_halo_fits(P, NT):
+    G = geo1(P, NT)
+    # the last wavefront's last block ends inside the column; staged rows fit
+    assert 16 * (G["WH"] - 1) + 16 * G["NKH"] <= G["CR"]
+    assert G["HH"] <= G["CR"]
+    # every key of every window lies in a staged row: wavefront wh's query j
+    # reads rows 16 wh + j .. 16 wh + j + 2P
+    assert 16 * (G["WH"] - 1) + 15 + 2 * P < G["HH"]
+    assert G["HH"] <= G["THREADS"]  # one staged pixel per thread
+    for nscal in (0, 1, 2):
+        assert 2 * G["LPX"] * G["SB"] + nscal * G["LPX"] * 4 + 16 <= LDS_CAP
+
+
+@pytest.mark.parametrize("P,NT", CASES1)
+def test_1d_block_rows_read_conflict_free(P, NT):
+    """Score-type rows of a 16x1 block: 16 consecutive slots, an odd number of
+    16-byte units apart, fall on 16 distinct units of 256 bytes."""
+    G = geo1(P, NT)
+    units = {(j * G["SB"] // 16) % 16 for j in range(16)}
+    assert len(units) == 16
+
+
+# ---- one-dimensional planar rows by 16-byte DMA (LGeo WIDE) ----
+
+def wide1(P, NT, mode, dist):
+    """LDS layout of the row-DMA kernels (fused2h_impl.h LGeo, WIDE)."""
+    G = geo1(P, NT)
+    NCH = 16 * NT
+    XA = (4 - P % 4) % 4
+    NXS = (G["HH"] + XA + 3) // 4 * 4
+    NRT = {"fwd": 1, "bwdq": 3, "bwdkv": 2}[mode]
+    nscal = 2 if mode == "bwdkv" else (1 if dist else 0)
+    OX = 2 * G["LPX"] * G["SB"] + nscal * G["LPX"] * 4
+    OXS = OX + 16
+    OXR = OXS + 2 * NCH * NXS * 4
+    return dict(G, NCH=NCH, XA=XA, NXS=NXS, NRT=NRT, OXS=OXS, OXR=OXR,
+                bytes=OXR + NRT * NCH * G["TH"] * 4)
+
+
+@pytest.mark.parametrize("P,NT", CASES1)
+def test_1d_wide_rows_fit_and_align(P, NT):
+    for mode in ("fwd", "bwdq", "bwdkv"):
+        for dist in (False, True):
+            W = wide1(P, NT, mode, dist)
+            assert W["bytes"] <= LDS_CAP, (mode, dist)
+            # 16-byte DMA destinations: row starts and 256-pixel parts
+            assert W["OXS"] % 16 == 0 and W["OXR"] % 16 == 0 and W["NXS"] % 4 == 0
+            assert W["TH"] <= 256  # one instruction (64 lanes x 4 pixels) per register row
+            # the halo origin h0 - P moved back by XA is a multiple of 4
+            assert (P + W["XA"]) % 4 == 0 and W["NXS"] >= W["HH"] + W["XA"]
+
+
+@pytest.mark.parametrize("P,NT", CASES1)
+@pytest.mark.parametrize("n1", [4, 24, 100, 260, 1000, 4096])
+def test_1d_wide_staged_rows_hold_the_halo(P, NT, n1):
+    """Lane l of part m loads pixels o4 + 4 (64 m + l) .. + 3 (mod n1) into XS
+    positions 4 (64 m + l) ..; the staged pixel px then reads position
+    px + XA, which must hold pixel (h0 - P + px) mod n1, and no 4-pixel chunk
+    may straddle the wrap."""
+    W = wide1(P, NT, "fwd", False)
+    XA, NXS, TH, HH = W["XA"], W["NXS"], W["TH"], W["HH"]
+    for h0 in range(0, n1, TH):
+        hsh = (h0 - P) % n1            # the kernel's halo origin
+        o4 = hsh - XA if hsh >= XA else hsh - XA + n1
+        assert o4 % 4 == 0 and 0 <= o4 < n1
+        row = {}
+        for l4 in range(NXS // 4):
+            p4 = o4 + 4 * l4
+            p4 = (p4 - n1 if p4 >= n1 else p4) if n1 >= NXS else p4 % n1
+            assert p4 % 4 == 0 and p4 + 3 < n1
+            for e in range(4):
+                row[4 * l4 + e] = p4 + e
+        for px in range(HH):
+            assert row[px + XA] == (h0 - P + px) % n1, (h0, px)
