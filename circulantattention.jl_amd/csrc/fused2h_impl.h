@@ -145,6 +145,28 @@ __device__ __forceinline__ h4 ldtr(const char *p) {
         (__attribute__((address_space(3))) s4v *)(p));
     return __builtin_bit_cast(h4, v);
 }
+// 16-byte LDS-DMA load: each active lane's 16 bytes from byte voff of the
+// buffer rs to LDS byte lds + 16 lane (lds wave-uniform).  Inline assembly
+// rather than __builtin_amdgcn_raw_ptr_buffer_load_lds: after the builtin the
+// compiler waits for every load in flight before the next LDS read, as it
+// cannot tell the DMA rows from the slots the walk reads, which would expose
+// the whole prefetch at the start of each walk.  The callers wait for the rows
+// (vmcnt(0) and a barrier) before reading them.  (The compiler writes M0 for
+// the asm; one wait state then separates that write from the load.)
+typedef int i4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i4v dma_rsrc(const float *p, int bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(p);
+    return i4v{(int)(uint32_t)b, (int)((b >> 32) & 0xffffu), bytes, (int)f2d::kRsrcWord3};
+}
+__device__ __forceinline__ void dma16(i4v rs, const char *lds, int voff) {
+    typedef __attribute__((address_space(3))) const char *lcp;
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(
+        (unsigned)reinterpret_cast<uintptr_t>((lcp)lds));
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(rs), "{m0}"(m0)
+                 : "memory");
+}
 __device__ __forceinline__ h8 cat(h4 a, h4 b) {
     return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
@@ -520,20 +542,20 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
             constexpr int NW = G::THREADS / 64, KW = (NI + NW - 1) / NW;
             const int o4 = hsh >= L::XA ? hsh - L::XA : hsh - L::XA + a.n1;
             const bool bigx = a.n1 >= L::NXS;
+            const i4v d0 = dma_rsrc((KV ? a.q : a.k) + uoff, ubytes);
+            const i4v d1 = dma_rsrc((KV ? a.dy : a.v) + uoff, ubytes);
+            const int wvu = __builtin_amdgcn_readfirstlane(wv);
 #pragma unroll
             for (int kk = 0; kk < KW; ++kk) {
-                const int i = wv + NW * kk;
+                const int i = wvu + NW * kk;
                 if (i < NI) {
                     const int part = i % NPART, tc = i / NPART;
                     const int t = tc / L::NCH, c = tc - t * L::NCH;
                     const int l4 = 64 * part + lane;
                     int p4 = o4 + 4 * l4;
                     p4 = bigx ? (p4 >= a.n1 ? p4 - a.n1 : p4) : p4 % a.n1;
-                    typedef __attribute__((address_space(3))) void *lptr;
-                    char *const dst = lds + L::OXS + ((t * L::NCH + c) * L::NXS + 256 * part) * 4;
-                    if (l4 < L::NXS / 4)
-                        __builtin_amdgcn_raw_ptr_buffer_load_lds(t ? r1 : r0, (lptr)dst, 16,
-                                                                (p4 + c * a.P) * 4, 0, 0, 0);
+                    const char *const dst = lds + L::OXS + ((t * L::NCH + c) * L::NXS + 256 * part) * 4;
+                    if (l4 < L::NXS / 4) dma16(t ? d1 : d0, dst, (p4 + c * a.P) * 4);
                 }
             }
         }
@@ -599,17 +621,18 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
             // n1 belong to no register pixel)
             constexpr int NI = L::NRT * L::NCH;
             constexpr int NW = G::THREADS / 64, KW = (NI + NW - 1) / NW;
-            const auto ry = f2d::rsrc(a.y + uoff, ubytes);
+            const i4v d0 = dma_rsrc((KV ? a.k : a.q) + uoff, ubytes);
+            const i4v d1 = dma_rsrc((KV ? a.v : a.dy) + uoff, ubytes);
+            const i4v dy = dma_rsrc(a.y + uoff, ubytes);
+            const int wvu = __builtin_amdgcn_readfirstlane(wv);
 #pragma unroll
             for (int kk = 0; kk < KW; ++kk) {
-                const int i = wv + NW * kk;
+                const int i = wvu + NW * kk;
                 if (i < NI) {
                     const int rt = i / L::NCH, c = i - rt * L::NCH;
-                    typedef __attribute__((address_space(3))) void *lptr;
-                    char *const dst = lds + L::OXR + (rt * L::NCH + c) * G::TH * 4;
+                    const char *const dst = lds + L::OXR + (rt * L::NCH + c) * G::TH * 4;
                     if (lane < G::TH / 4)
-                        __builtin_amdgcn_raw_ptr_buffer_load_lds(rt == 0 ? r0 : rt == 1 ? r1 : ry, (lptr)dst,
-                                                                16, (h0 + 4 * lane + c * a.P) * 4, 0, 0, 0);
+                        dma16(rt == 0 ? d0 : rt == 1 ? d1 : dy, dst, (h0 + 4 * lane + c * a.P) * 4);
                 }
             }
         }
@@ -627,7 +650,7 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
         }
         if constexpr (MODE == BWDQ)
             nlse = f2d::bload(f2d::rsrc(a.lse + (int64_t)unit * a.P, a.P * 4), rpix * 4, 0);
-        if constexpr (DIST)
+        if constexpr (DIST && !WIDE)
             nmu = f2d::bload(f2d::rsrc(a.k + uoff, ubytes),
                              f2d::comp_off<CPLX, CL>(a, h0 + a.n1 * w0, lane & (16 * NT - 1)) * 4, 0);
     };
@@ -697,7 +720,20 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
         // and row term) is then formed from q - mu and k - mu, whose terms
         // scale with the spread of the data rather than its offset; |q - k|
         // and the gradient terms dS (k - q) are unchanged.
-        if constexpr (DIST) {
+        if constexpr (DIST && WIDE) {
+            // mu from the rows in LDS: k at the tile's first pixel, position
+            // P + XA of the staged k rows, or position 0 of the register k
+            // rows (key-centric pass)
+            constexpr int MS = MODE == BWDKV ? G::TH : L::NXS;
+            const float *const mu = reinterpret_cast<const float *>(lds + (MODE == BWDKV ? L::OXR : L::OXS)) +
+                                    (MODE == BWDKV ? 0 : P + L::XA);
+#pragma unroll
+            for (int c = 0; c < NCS; ++c) h0v[c] -= mu[(16 * hsub + c) * MS];
+#pragma unroll
+            for (int h = 0; h < NT; ++h)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) nh0[h][t] -= mu[(16 * h + 8 * (g & 1) + 4 * (g >> 1) + t) * MS];
+        } else if constexpr (DIST) {
 #pragma unroll
             for (int c = 0; c < NCS; ++c) {
                 const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(nmu), c));
