@@ -146,7 +146,7 @@ __device__ __forceinline__ h4 ldtr(const char *p) {
     return __builtin_bit_cast(h4, v);
 }
 // 16-byte LDS-DMA load: each active lane's 16 bytes from byte voff of the
-// buffer rs to LDS byte lds + 16 lane (lds wave-uniform).  Inline assembly
+// buffer rs to LDS byte m0 + 16 lane (m0 wave-uniform).  Inline assembly
 // rather than __builtin_amdgcn_raw_ptr_buffer_load_lds: after the builtin the
 // compiler waits for every load in flight before the next LDS read, as it
 // cannot tell the DMA rows from the slots the walk reads, which would expose
@@ -158,10 +158,7 @@ __device__ __forceinline__ i4v dma_rsrc(const float *p, int bytes) {
     const uint64_t b = reinterpret_cast<uint64_t>(p);
     return i4v{(int)(uint32_t)b, (int)((b >> 32) & 0xffffu), bytes, (int)f2d::kRsrcWord3};
 }
-__device__ __forceinline__ void dma16(i4v rs, const char *lds, int voff) {
-    typedef __attribute__((address_space(3))) const char *lcp;
-    const unsigned m0 = __builtin_amdgcn_readfirstlane(
-        (unsigned)reinterpret_cast<uintptr_t>((lcp)lds));
+__device__ __forceinline__ void dma16(i4v rs, unsigned m0, int voff) {
     asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                  :
                  : "v"(voff), "s"(rs), "{m0}"(m0)
@@ -452,6 +449,9 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
     static_assert(NT == 1 || NT == 2, "16 or 32 real components per head");
     static_assert(HH % 2 == 0, "row pairs");
     char *const lds = reinterpret_cast<char *>(circatt_lds2);
+    // LDS byte address of the array (the DMA loads' M0 base)
+    typedef __attribute__((address_space(3))) const char *lcp;
+    const unsigned lds0 = __builtin_amdgcn_readfirstlane((unsigned)reinterpret_cast<uintptr_t>((lcp)lds));
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int wh = wv % WH, ww = wv / WH;
@@ -534,28 +534,35 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
         const auto r1 = f2d::rsrc((KV ? a.dy : a.v) + uoff, ubytes);
         hslot = px < NPX ? kh + CR * kw : -1;
         if constexpr (WIDE) {
-            // this wavefront's share of the XS rows: instruction i = (tensor,
-            // channel, part of 256 pixels); lane l of part m loads pixels
-            // o4 + 4 (64 m + l) .. + 3 (mod n1: o4 and n1 are multiples of 4, so
-            // no chunk straddles the wrap)
-            constexpr int NPART = (L::NXS + 255) / 256, NI = 2 * L::NCH * NPART;
-            constexpr int NW = G::THREADS / 64, KW = (NI + NW - 1) / NW;
+            // XS rows: wavefront wv loads channels wv + NW cg of both tensors
+            // (every operand but the lane offset a per-wavefront base plus a
+            // constant: few scalar instructions per load); in part m of a row
+            // (256 pixels) lane l loads pixels o4 + 4 (64 m + l) .. + 3 (mod
+            // n1: o4 and n1 are multiples of 4, so no chunk straddles the wrap)
+            constexpr int NPART = (L::NXS + 255) / 256;
+            constexpr int NW = G::THREADS / 64, KC = L::NCH / NW;
+            static_assert(L::NCH % NW == 0, "whole channel groups per wavefront");
             const int o4 = hsh >= L::XA ? hsh - L::XA : hsh - L::XA + a.n1;
             const bool bigx = a.n1 >= L::NXS;
             const i4v d0 = dma_rsrc((KV ? a.q : a.k) + uoff, ubytes);
             const i4v d1 = dma_rsrc((KV ? a.dy : a.v) + uoff, ubytes);
             const int wvu = __builtin_amdgcn_readfirstlane(wv);
+            const unsigned m0w = lds0 + L::OXS + wvu * L::NXS * 4;
+            const int cstep = NW * a.P * 4;  // bytes between the channels of one wavefront
 #pragma unroll
-            for (int kk = 0; kk < KW; ++kk) {
-                const int i = wvu + NW * kk;
-                if (i < NI) {
-                    const int part = i % NPART, tc = i / NPART;
-                    const int t = tc / L::NCH, c = tc - t * L::NCH;
-                    const int l4 = 64 * part + lane;
-                    int p4 = o4 + 4 * l4;
-                    p4 = bigx ? (p4 >= a.n1 ? p4 - a.n1 : p4) : p4 % a.n1;
-                    const char *const dst = lds + L::OXS + ((t * L::NCH + c) * L::NXS + 256 * part) * 4;
-                    if (l4 < L::NXS / 4) dma16(t ? d1 : d0, dst, (p4 + c * a.P) * 4);
+            for (int part = 0; part < NPART; ++part) {
+                const int l4 = 64 * part + lane;
+                int p4 = o4 + 4 * l4;
+                p4 = bigx ? (p4 >= a.n1 ? p4 - a.n1 : p4) : p4 % a.n1;
+                const int vo = (p4 + wvu * a.P) * 4;
+                // (only the last part has idle lanes)
+                if (part + 1 < NPART || l4 < L::NXS / 4) {
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+#pragma unroll
+                        for (int cg = 0; cg < KC; ++cg)
+                            dma16(t ? d1 : d0, m0w + ((t * L::NCH + NW * cg) * L::NXS + 256 * part) * 4,
+                                  vo + cg * cstep);
                 }
             }
         }
@@ -616,24 +623,24 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
         const auto r0 = f2d::rsrc((KV ? a.k : a.q) + uoff, ubytes);
         const auto r1 = f2d::rsrc((KV ? a.v : a.dy) + uoff, ubytes);
         if constexpr (WIDE) {
-            // this wavefront's share of the XR rows: instruction i = (tensor,
-            // channel); lane l loads the tile's pixels h0 + 4l .. + 3 (those past
-            // n1 belong to no register pixel)
-            constexpr int NI = L::NRT * L::NCH;
-            constexpr int NW = G::THREADS / 64, KW = (NI + NW - 1) / NW;
+            // XR rows: wavefront wv loads channels wv + NW cg of each register
+            // tensor; lane l the tile's pixels h0 + 4l .. + 3 (those past n1
+            // belong to no register pixel)
+            constexpr int NW = G::THREADS / 64, KC = L::NCH / NW;
             const i4v d0 = dma_rsrc((KV ? a.k : a.q) + uoff, ubytes);
             const i4v d1 = dma_rsrc((KV ? a.v : a.dy) + uoff, ubytes);
             const i4v dy = dma_rsrc(a.y + uoff, ubytes);
             const int wvu = __builtin_amdgcn_readfirstlane(wv);
+            const unsigned m0r = lds0 + L::OXR + wvu * G::TH * 4;
+            const int vr = (h0 + 4 * lane + wvu * a.P) * 4;
+            const int cstep = NW * a.P * 4;
+            if (lane < G::TH / 4) {
 #pragma unroll
-            for (int kk = 0; kk < KW; ++kk) {
-                const int i = wvu + NW * kk;
-                if (i < NI) {
-                    const int rt = i / L::NCH, c = i - rt * L::NCH;
-                    const char *const dst = lds + L::OXR + (rt * L::NCH + c) * G::TH * 4;
-                    if (lane < G::TH / 4)
-                        dma16(rt == 0 ? d0 : rt == 1 ? d1 : dy, dst, (h0 + 4 * lane + c * a.P) * 4);
-                }
+                for (int rt = 0; rt < L::NRT; ++rt)
+#pragma unroll
+                    for (int cg = 0; cg < KC; ++cg)
+                        dma16(rt == 0 ? d0 : rt == 1 ? d1 : dy, m0r + ((rt * L::NCH + NW * cg) * G::TH) * 4,
+                              vr + cg * cstep);
             }
         }
 #pragma unroll
