@@ -431,13 +431,21 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
 #ifndef CIRCATT_F2H_BWD_FSTEP
 #define CIRCATT_F2H_BWD_FSTEP 1
 #endif
+    // Backward passes of 32-component 2D kernels (two wavefronts per SIMD,
+    // 64 staged values per thread): the next item's loads start at the
+    // second pair and spread over three (cfg5: query-centric pass 144 -> 140
+    // us, key-centric 170 -> 160 us against all loads at one pair, a quarter
+    // and half way through the walk); 16-component kernels keep one pair
+    // (spreading was 2% slower in their query-centric pass at cfg3)
+    constexpr bool SPREAD = !ONE && MODE != FWD && NT == 2;
     // forward with a reference maximum from the central block row (rows 8, 9
     // of the key region lie in every query's window when 2P >= 9)
     constexpr bool STREAM = MODE == FWD && P >= 5 && (BR == 4 || NKW == 2);
-    constexpr int PFP = STREAM                    ? 0
-                        : (MODE == FWD && NCH == 2) ? CHP - 1
-                        : MODE == BWDQ              ? NPAIR / CIRCATT_F2H_BWDQ_PFD
-                                                    : NPAIR / CIRCATT_F2H_BWD_PFD;
+    constexpr int PFP = STREAM                      ? 0
+                        : (MODE == FWD && NCH == 2)   ? CHP - 1
+                        : (SPREAD && NPAIR > 3)       ? 1
+                        : MODE == BWDQ                ? NPAIR / CIRCATT_F2H_BWDQ_PFD
+                                                      : NPAIR / CIRCATT_F2H_BWD_PFD;
     static_assert(PFP >= 0 && PFP < NPAIR, "the next item's loads must be issued in the walk");
     static_assert(NPX <= G::THREADS, "one staged pixel per thread");
     // HALF: two threads per staged pixel of 32 components, one sub-pixel of
@@ -523,7 +531,10 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
     // halos only: in 2D every wavefront or all but one stage pixels, and the
     // branch would split the walk's basic block around the prefetch)
     const bool stw = !ONE || (HALF ? 32 * wv : 64 * wv) < NPX;
-    auto load_stage = [&](int unit, int h0, int w0) __attribute__((always_inline)) {
+    // HP: -1 all of the staged loads, 0 / 1 the first / second half of the
+    // components (with the scalars in the first)
+    auto load_stage = [&](int unit, int h0, int w0, auto HP) __attribute__((always_inline)) {
+        constexpr int hp = decltype(HP)::value;
         // halo origin (h0 - P, w0 - P) mod (n1, n2), uniform
         int hsh = h0 - P, wsh = ONE ? 0 : w0 - P;
         while (hsh < 0) hsh += a.n1;
@@ -533,7 +544,7 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
         const auto r0 = f2d::rsrc((KV ? a.q : a.k) + uoff, ubytes);
         const auto r1 = f2d::rsrc((KV ? a.dy : a.v) + uoff, ubytes);
         hslot = px < NPX ? kh + CR * kw : -1;
-        if constexpr (WIDE) {
+        if constexpr (WIDE && hp != 1) {
             // XS rows: wavefront wv loads channels wv + NW cg of both tensors
             // (every operand but the lane offset a per-wavefront base plus a
             // constant: few scalar instructions per load); in part m of a row
@@ -590,7 +601,7 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
         } else if constexpr (CPLX) {
             const int vb = (f2d::pix_off<true, CL>(a, gp) + f2d::comp_soff<true, CL>(a, 16 * hsub)) * 4;
 #pragma unroll
-            for (int c = 0; c < NCS / 2; ++c) {
+            for (int c = hp == 1 ? NCS / 4 : 0; c < (hp == 0 ? NCS / 4 : NCS / 2); ++c) {
                 const int vo = vb, so = f2d::comp_soff<true, CL>(a, 2 * c) * 4;
                 const f2d::f2 x0 = f2d::bload2(r0, vo, so);
                 const f2d::f2 x1 = f2d::bload2(r1, vo, so);
@@ -602,13 +613,13 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
         } else {
             const int vb = (f2d::pix_off<false, CL>(a, gp) + f2d::comp_soff<false, CL>(a, 16 * hsub)) * 4;
 #pragma unroll
-            for (int c = 0; c < NCS; ++c) {
+            for (int c = hp == 1 ? NCS / 2 : 0; c < (hp == 0 ? NCS / 2 : NCS); ++c) {
                 const int vo = vb, so = f2d::comp_soff<false, CL>(a, c) * 4;
                 h0v[c] = f2d::bload(r0, vo, so);
                 h1v[c] = f2d::bload(r1, vo, so);
             }
         }
-        if constexpr (KV) {
+        if constexpr (KV && hp != 1) {
             const int64_t soff = (int64_t)unit * a.P;
             hs0 = f2d::bload(f2d::rsrc(a.lse + soff, a.P * 4), gp * 4, 0);
             hs1 = f2d::bload(f2d::rsrc(a.dbuf + soff, a.P * 4), gp * 4, 0);
@@ -684,7 +695,7 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
     }
     int unit, h0, w0;
     decode(item, unit, h0, w0);
-    load_stage(unit, h0, w0);
+    load_stage(unit, h0, w0, std::integral_constant<int, -1>{});
     load_regs(unit, h0, w0);
     __syncthreads();  // exchange words cleared before any item's maxima
 
@@ -957,8 +968,22 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
         int xunit = unit, xh0 = h0, xw0 = w0;
         if (has_next) decode(nitem, xunit, xh0, xw0);
         auto prefetch = [&]() __attribute__((always_inline)) {
-            load_stage(xunit, xh0, xw0);
+            load_stage(xunit, xh0, xw0, std::integral_constant<int, -1>{});
             load_regs(xunit, xh0, xw0);
+        };
+        // the same loads over three consecutive pairs from PFP: halves of the
+        // staged components, then the register operands (SPREAD)
+        auto prefetch_at = [&](auto PI) __attribute__((always_inline)) {
+            constexpr int pi = decltype(PI)::value;
+            if constexpr (!SPREAD) {
+                if (pi == PFP) prefetch();
+            } else {
+                constexpr int p1 = PFP + 1 < NPAIR ? PFP + 1 : PFP;
+                constexpr int p2 = p1 + 1 < NPAIR ? p1 + 1 : p1;
+                if constexpr (pi == PFP) load_stage(xunit, xh0, xw0, std::integral_constant<int, 0>{});
+                if constexpr (pi == p1) load_stage(xunit, xh0, xw0, std::integral_constant<int, 1>{});
+                if constexpr (pi == p2) load_regs(xunit, xh0, xw0);
+            }
         };
 
         // score-type product of block b (16 elements x 16 register pixels),
@@ -1252,7 +1277,7 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
                 if constexpr (pi % CIRCATT_F2H_BWD_FSTEP == 0) BLOCK_FENCE();
                 if constexpr (MODE == BWDQ) walk_prio<pi, NPAIR>();
                 if constexpr (MODE == BWDKV) walk_prio_tail<pi, NPAIR>();
-                if constexpr (pi == PFP) prefetch();
+                prefetch_at(PI);
                 float p[2][4], ds[2][4];
                 auto blk = [&](auto B, int u) {
                     constexpr int b = decltype(B)::value;
