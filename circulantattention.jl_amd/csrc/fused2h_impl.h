@@ -657,13 +657,35 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
 #pragma unroll
         for (int h = 0; h < NT && !WIDE; ++h) {
             const int vo = f2d::comp_off<CPLX, CL>(a, rpix, 16 * h + 8 * (g & 1) + 4 * (g >> 1)) * 4;
+            if constexpr (CPLX || CL) {
+                // components t, t + 1 adjacent (real and imaginary part, or
+                // channels-last): one 8-byte load per pair
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int so = f2d::comp_soff<CPLX, CL>(a, t) * 4;
-                nh0[h][t] = f2d::bload(r0, vo, so);
-                if constexpr (MODE != FWD) nh1[h][t] = f2d::bload(r1, vo, so);
-                // y beside dy, for D = <dy, y>
-                if constexpr (MODE == BWDQ) nry[h][t] = f2d::bload(f2d::rsrc(a.y + uoff, ubytes), vo, so);
+                for (int t = 0; t < 4; t += 2) {
+                    const int so = f2d::comp_soff<CPLX, CL>(a, t) * 4;
+                    const f2d::f2 x0 = f2d::bload2(r0, vo, so);
+                    nh0[h][t] = x0[0];
+                    nh0[h][t + 1] = x0[1];
+                    if constexpr (MODE != FWD) {
+                        const f2d::f2 x1 = f2d::bload2(r1, vo, so);
+                        nh1[h][t] = x1[0];
+                        nh1[h][t + 1] = x1[1];
+                    }
+                    if constexpr (MODE == BWDQ) {
+                        const f2d::f2 xy = f2d::bload2(f2d::rsrc(a.y + uoff, ubytes), vo, so);
+                        nry[h][t] = xy[0];
+                        nry[h][t + 1] = xy[1];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int so = f2d::comp_soff<CPLX, CL>(a, t) * 4;
+                    nh0[h][t] = f2d::bload(r0, vo, so);
+                    if constexpr (MODE != FWD) nh1[h][t] = f2d::bload(r1, vo, so);
+                    // y beside dy, for D = <dy, y>
+                    if constexpr (MODE == BWDQ) nry[h][t] = f2d::bload(f2d::rsrc(a.y + uoff, ubytes), vo, so);
+                }
             }
         }
         if constexpr (MODE == BWDQ)
