@@ -726,6 +726,20 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
         bool rvalid;
         int rpix;
         regpix(h0, w0, rvalid, rpix);
+        // output channels 16 h + 4 g + r, r = 0..3, of the register pixel;
+        // adjacent pairs (real and imaginary part, or channels-last) as one
+        // 8-byte store
+        auto put4 = [&](float *base, int h, const float (&x)[4]) {
+            if constexpr (CPLX || CL) {
+#pragma unroll
+                for (int r = 0; r < 4; r += 2)
+                    *reinterpret_cast<f2 *>(base + f2d::comp_off<CPLX, CL>(a, rpix, 16 * h + 4 * g + r)) =
+                        f2{x[r], x[r + 1]};
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) base[f2d::comp_off<CPLX, CL>(a, rpix, 16 * h + 4 * g + r)] = x[r];
+            }
+        };
         if constexpr (WIDE) {
             // the item's rows are in LDS once every wavefront's loads are
             // (vmcnt(0): the DMA writes count as this wavefront's loads)
@@ -1267,11 +1281,12 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
             if (rvalid) {
                 float *yb = a.yout + uoff;
 #pragma unroll
-                for (int h = 0; h < NT; ++h)
+                for (int h = 0; h < NT; ++h) {
+                    float x[4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        yb[f2d::comp_off<CPLX, CL>(a, rpix, 16 * h + 4 * g + r)] =
-                            __builtin_amdgcn_ldexpf(acc[h][r] * inv, -s1);
+                    for (int r = 0; r < 4; ++r) x[r] = __builtin_amdgcn_ldexpf(acc[h][r] * inv, -s1);
+                    put4(yb, h, x);
+                }
                 if (g == 0)
                     a.lse_out[soff + rpix] =
                         (m + __log2f(l)) * kLn2 - (DIST ? 0.5f * sq * a.scale : 0.f);
@@ -1379,29 +1394,35 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
                 if constexpr (!KV) {
                     float *ob = a.dq + uoff;
 #pragma unroll
-                    for (int h = 0; h < NT; ++h)
+                    for (int h = 0; h < NT; ++h) {
+                        float x[4];
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             // dS' = 2^(sd + s1) dS, k' = 2^s0 k
                             float val = __builtin_amdgcn_ldexpf(acc0[h][r], -(sd + s1 + s0));
                             if constexpr (DIST) val -= __builtin_amdgcn_ldexpf(cs, -(sd + s1)) * reg0[h][r];
-                            ob[f2d::comp_off<CPLX, CL>(a, rpix, 16 * h + 4 * g + r)] = val * a.scale;
+                            x[r] = val * a.scale;
                         }
+                        put4(ob, h, x);
+                    }
                     if (g == 0) a.dbuf[soff + rpix] = rowD;
                 } else {
                     float *vb = a.dv + uoff;
                     float *kbp = a.dk + uoff;
 #pragma unroll
-                    for (int h = 0; h < NT; ++h)
+                    for (int h = 0; h < NT; ++h) {
+                        float xv[4], xk[4];
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const int o = f2d::comp_off<CPLX, CL>(a, rpix, 16 * h + 4 * g + r);
                             // dy' = 2^s1 dy, dS' = 2^(s2 + s1) dS, q' = 2^s0 q
-                            vb[o] = __builtin_amdgcn_ldexpf(acc1[h][r], -s1);
+                            xv[r] = __builtin_amdgcn_ldexpf(acc1[h][r], -s1);
                             float val = __builtin_amdgcn_ldexpf(acc0[h][r], -(s2 + s1 + s0));
                             if constexpr (DIST) val -= __builtin_amdgcn_ldexpf(cs, -(s2 + s1)) * reg0[h][r];
-                            kbp[o] = val * a.scale;
+                            xk[r] = val * a.scale;
                         }
+                        put4(vb, h, xv);
+                        put4(kbp, h, xk);
+                    }
                 }
             }
         }
