@@ -64,8 +64,9 @@ def describe(name):
 
 
 SEEDS = {"cfg3": 1003, "cfg4a": 1004, "cfg4b": 1005, "cfg5": 1006}
-# the bound BASELINE.md gives each configuration (cfg4b, 1D with 32 channels
-# and a window of 63, is HBM-bound; the others are matrix-core bound)
+# the roofline each configuration is reported against: cfg4b (1D, 32
+# channels, a window of 63: 63 keys per query against 12 tensor reads and
+# writes per pixel) is HBM-bound, the 2D windows are matrix-core bound
 BOUND = {"cfg3": "mfma", "cfg4a": "mfma", "cfg4b": "hbm", "cfg5": "mfma"}
 
 
