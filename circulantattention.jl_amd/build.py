@@ -73,6 +73,45 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+def asan_runtime() -> str:
+    """Path of the compiler's shared AddressSanitizer runtime (with the
+    UndefinedBehaviorSanitizer handlers), which a process preloads to load a
+    library from build_host_sanitized()."""
+    clang = os.path.join(os.path.dirname(os.path.realpath(HIPCC)), "..", "llvm", "bin", "clang++")
+    if not os.path.exists(clang):
+        clang = shutil.which("amdclang++") or "/opt/rocm/llvm/bin/clang++"
+    res = subprocess.run([clang, "-print-file-name=libclang_rt.asan-x86_64.so"],
+                         capture_output=True, text=True, check=True)
+    return res.stdout.strip()
+
+
+def build_host_sanitized(out_dir: str) -> str:
+    """A copy of libcircatt in out_dir whose host code (api.cpp: the C ABI's
+    argument checks, workspace arithmetic and dispatch) is instrumented by
+    AddressSanitizer and UndefinedBehaviorSanitizer, without recovery; the
+    device code and the kernels' objects are those of build(), which must have
+    run.  The copy resolves the sanitizer runtime at load time, so the loading
+    process preloads asan_runtime().  Returns the library's path."""
+    objs = [os.path.join(OBJ, os.path.splitext(s)[0] + ".o") for s in SOURCES if s != "api.cpp"]
+    missing = [o for o in objs if not os.path.exists(o)]
+    if missing:
+        raise FileNotFoundError(f"in-tree objects not built: {missing[:3]}")
+    os.makedirs(out_dir, exist_ok=True)
+    api = os.path.join(out_dir, "api_sanitized.o")
+    san = ["-g", "-Xarch_host", "-fsanitize=address,undefined",
+           "-Xarch_host", "-fno-sanitize-recover=all", "-Xarch_host", "-fno-omit-frame-pointer"]
+    cmd = [HIPCC, "-x", "hip", *FLAGS, *san, "-c", os.path.join(CSRC, "api.cpp"), "-o", api]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for the sanitized api.cpp:\n{res.stderr}")
+    lib = os.path.join(out_dir, "libcircatt_host_sanitized.so")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", lib, api, *objs]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    return lib
+
+
 if __name__ == "__main__":
     build(verbose=True)
     sys.exit(0)
