@@ -417,8 +417,16 @@ def main():
         traffic = json.load(open(os.path.join(ROOT, tfile))).get(dom)
         traffic_src = (f"{tfile}: HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and "
                        f"WRITE_SIZE runs (not measured in this run)")
+    # BASELINE.json's metric names cfg3's shape; the other configurations get
+    # the same metric worded for their own
+    metric = base["metric"]
+    if args.config != "cfg3":
+        shape = (f"{dims[0]}²" if len(dims) == 2 and dims[0] == dims[1]
+                 else "×".join(str(d) for d in dims))
+        metric = (f"CircAtt fwd+bwd Mpixel/s ({shape}×{C}{' complex' if cplx else ''}, ws={ws}, "
+                  f"{nh} heads, B={B}); % of roofline")
     out = {
-        "metric": base["metric"],
+        "metric": metric,
         "value": round(mpix, 3),
         "unit": "Mpixel/s",
         "n_gpus": 1,
