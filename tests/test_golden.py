@@ -1,6 +1,6 @@
 """Golden vector from the reference itself: the README's picture of the
 128x96, ws = 15 Circulant (README.md:72-112), i.e. the sparsity pattern of
-BASELINE's README-quickstart configuration as the reference printed it.
+the README-quickstart configuration (cfg2) as the reference printed it.
 
 The oracle's pattern (and, in the GPU test, libcircatt's pattern) rendered by
 Julia's braille spy algorithm (tests/golden/spy.py) must reproduce the

@@ -312,7 +312,7 @@ def test_circulant_algebra_leftovers(ca, cuda):
 # full-size configurations
 # ---------------------------------------------------------------------------
 def test_cfg2_backward_full_size(ca, cuda):
-    """BASELINE cfg2 (README.md:55-71, 128x96x64x2, ws = 15) at full size, the
+    """Benchmark configuration cfg2 (README.md:55-71, 128x96x64x2, ws = 15) at full size, the
     unfused path: y, A and the gradients of q, k, v for an N(0,1) dy against
     the oracle (the forward alone is test_gpu_parity's)."""
     dims, ws, C, B = (128, 96), 15, 64, 2
@@ -330,7 +330,7 @@ def test_cfg2_backward_full_size(ca, cuda):
 
 
 FULL = {
-    # name: (dims, C, B, nheads, ws, kind, complex) as BASELINE.json
+    # name: (dims, C, B, nheads, ws, kind, complex) of the benchmark configurations
     "cfg4a": ((512, 512), 32, 1, 1, 31, 1, False),
     "cfg4b": ((262144,), 32, 2, 1, 63, 1, False),
     "cfg5": ((320, 320), 32, 2, 2, 11, 0, True),
@@ -339,7 +339,7 @@ FULL = {
 
 @pytest.mark.parametrize("name", list(FULL))
 def test_fused_matches_unfused_full_size(ca, cuda, name):
-    """BASELINE cfg4a, cfg4b and cfg5 at full size: the fused kernels agree
+    """Benchmark configurations cfg4a, cfg4b and cfg5 at full size: the fused kernels agree
     with the unfused composition (itself checked against the oracle by the
     reduced-size tests) for y and all gradients; rows of A sum to one."""
     dims, C, B, nh, ws, kind, cplx = FULL[name]
@@ -462,7 +462,7 @@ def test_transposed_attention_gradients(ca, cuda, mh, nsp, cplx, kind):
 
 
 def test_cfg5_composition_full_size(ca, cuda):
-    """BASELINE cfg5 / README.md:128-134 at full size (320x320, 32 complex
+    """Benchmark configuration cfg5 / README.md:128-134 at full size (320x320, 32 complex
     channels, B = 2, 2 heads, ws = 11): y, A = mh attention; u, B = mh
     attention of (y, y, y); C = A + m*B with m of Julia size (1, 1, 2, 2);
     w = C ⨷ u.  A, B, C and w against the oracle (the float64 C restatement,

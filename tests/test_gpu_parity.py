@@ -4,7 +4,7 @@ identical seeded inputs (float32 inputs, float64 oracle).
 Bar: CSR indices bit-exact; forward values within 1e-5 and gradients within
 1e-4 (max-norm relative error, conftest.rel_err).  Shapes mirror the
 reference's tests (test/rrule.jl:1-6: 8^S x 4 x 2, ws = 5; test/grad.jl:6-7,
-46-56: 10^S x 8 x 2, ws = 3, nheads = 2), BASELINE.json's configurations at
+46-56: 10^S x 8 x 2, ws = 3, nheads = 2), the benchmark configurations at
 sizes the oracle finishes in seconds, and the degenerate ws > N patterns.
 """
 import math
@@ -75,7 +75,7 @@ def test_pattern_bitexact(ca, cuda, dims, ws):
 
 
 def test_pattern_bitexact_cfg4a_full_size(ca, cuda):
-    """BASELINE cfg4a's pattern at full size: 512x512, ws = 31 (961 slots per
+    """Benchmark configuration cfg4a's pattern at full size: 512x512, ws = 31 (961 slots per
     row, 251,920,384 entries), rowPtr and colVal bit-exact."""
     from circulant_attention import _lib as L
     from circulant_attention._functions import ptr, stream_ptr
@@ -241,7 +241,7 @@ ATT_CASES = [
     ((8, 8), 5, 4, 2, 1, 101),
     ((10,), 3, 8, 2, 2, 102),     # test/grad.jl shapes
     ((10, 10), 3, 8, 2, 2, 103),
-    ((32, 32), 7, 16, 1, 1, 1001),  # BASELINE cfg1
+    ((32, 32), 7, 16, 1, 1, 1001),  # benchmark configuration cfg1
     ((12, 10), 3, 4, 2, 1, 104),  # non-square
     ((4, 4), 5, 4, 2, 1, 105),    # ws > N
     ((4,), 5, 4, 2, 1, 106),
@@ -447,7 +447,7 @@ def test_mh_attention_ignores_simfun(ca, cuda):
 
 
 def test_composition_cfg5_style(ca, cuda):
-    """README.md:128-134 / BASELINE cfg5 (reduced): C = A + m*B, w = C ⨷ u."""
+    """README.md:128-134 / benchmark configuration cfg5 (reduced): C = A + m*B, w = C ⨷ u."""
     dims, ws, Cc, Bb, nh = (20, 16), 11, 32, 2, 2
     shape = shape_of(dims, Cc, Bb)
     q, k, v = (seeded(400 + i, shape, True) for i in range(3))
@@ -571,7 +571,7 @@ def test_adjacency_apply_chain_matches_oracle(ca, cuda):
 # ---------------------------------------------------------------------------
 
 def test_cfg2_unfused_full_size(ca, cuda):
-    """BASELINE cfg2 (README quickstart): unfused forward returning A at full
+    """Benchmark configuration cfg2 (README quickstart): unfused forward returning A at full
     size, y and A against the oracle; CSR indices bit-exact."""
     dims, ws, C, B = (128, 96), 15, 64, 2
     q, k, v = (seeded(1002 + 10 * i, shape_of(dims, C, B)) for i in range(3))
@@ -584,7 +584,7 @@ def test_cfg2_unfused_full_size(ca, cuda):
 
 
 def test_cfg3_fused_matches_unfused_full_size(ca, cuda):
-    """BASELINE cfg3 at full size (256x256x64x4, 4 heads, ws=15): the fused
+    """Benchmark configuration cfg3 at full size (256x256x64x4, 4 heads, ws=15): the fused
     kernels agree with the unfused composition (itself checked against the
     oracle above) for y and all gradients; rows of A sum to one."""
     dims, ws, C, B, nh = (256, 256), 15, 64, 4, 4
