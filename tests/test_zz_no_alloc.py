@@ -31,7 +31,7 @@ def test_noalloc_rejects_beyond_scratch():
 CASES = [
     [((48, 40), 64, 2, 4, 15, 0, False), ((20, 16), 64, 1, 4, 15, 0, False)],  # split-half
     [((30, 22), 32, 2, 1, 7, 1, True), ((9, 7), 32, 1, 1, 7, 1, True)],        # Float32 MFMA
-    [((300,), 32, 2, 1, 63, 1, False), ((70,), 32, 1, 1, 63, 1, False)],        # 1D, generic
+    [((300,), 32, 2, 1, 63, 1, False), ((70,), 32, 1, 1, 63, 1, False)],        # 1D split-half: row DMA, then per-pixel loads
     [((28, 20), 32, 2, 2, 11, 0, True), ((9, 7), 32, 1, 2, 11, 0, True)],      # split-half, 32 components
 ]
 
