@@ -334,11 +334,16 @@ struct HGeo {
     static constexpr int wrow(int wh) { return ONE ? 16 * wh : 8 * wh; }
     static constexpr int sbslot(int b) { return sidx(BR * (b / NKW), BC * (b % NKW)); }
     // central pair of the streamed forward: two blocks of the block row that
-    // holds key rows 8, 9 (in every query's window when 2P >= 9)
-    static constexpr int PCENT = (8 / BR) * NKW / 2;
+    // holds key rows 8, 9 (in every query's window when 2P >= 9); ONE: the
+    // pair of keys 32 PCENT .. 32 PCENT + 31 of the 16 + 2P key region
+    static constexpr int PCENT = ONE ? (8 + P) / 32 : (8 / BR) * NKW / 2;
     static_assert(wrow(WH - 1) + BR * NKH <= CR, "a wavefront's blocks stay within their column's slots");
     static_assert(HH <= CR, "the staged rows fit the column");
     static_assert((8 / BR) * NKW % 2 == 0, "the central pair lies in one block row");
+    // (ONE) query j of a wavefront has region keys j .. j + 2P in its window:
+    // the central pair's keys meet every one of those windows
+    static_assert(!ONE || (32 * PCENT <= 2 * P && 32 * PCENT + 31 >= 15 && 2 * PCENT < NBLK),
+                  "the central pair holds a key of every query's window");
 };
 static_assert(HGeo<5, 2>::LPX == 520 && HGeo<5, 2>::NBLK == 15, "4x4 blocks at ws 11");
 static_assert(HGeo<7, 1>::LPX == f2d::Geo<7, 1, 2, 8>::LPX && HGeo<7, 1>::NBLK == f2d::Geo<7, 1, 2, 8>::NBLK,
@@ -438,9 +443,10 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
     // and half way through the walk); 16-component kernels keep one pair
     // (spreading was 2% slower in their query-centric pass at cfg3)
     constexpr bool SPREAD = !ONE && MODE != FWD && NT == 2;
-    // forward with a reference maximum from the central block row (rows 8, 9
-    // of the key region lie in every query's window when 2P >= 9)
-    constexpr bool STREAM = MODE == FWD && P >= 5 && (BR == 4 || NKW == 2);
+    // forward with a reference maximum from the central block pair (2D: rows
+    // 8, 9 of the key region lie in every query's window when 2P >= 9; ONE:
+    // the pair PCENT meets every window)
+    constexpr bool STREAM = MODE == FWD && P >= 5 && (BR == 4 || NKW == 2 || ONE);
     constexpr int PFP = STREAM                      ? 0
                         : (MODE == FWD && NCH == 2)   ? CHP - 1
                         : (SPREAD && NPAIR > 3)       ? 1
@@ -1183,8 +1189,9 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
             auto apply = [&](auto PI, const f4 (&sv)[2]) { return apply_ops(load_ops(PI), sv); };
             // Scores relative to a reference maximum m, folded into the MFMA's
             // initial accumulator.  The first walk takes m from the central
-            // pair PC (block row 4: rows 8, 9 of the key region lie in every
-            // query's window when 2P >= 9, so m is finite) and has no branch;
+            // pair PC (2D: block row 4, rows 8, 9 of the key region lie in every
+            // query's window when 2P >= 9; ONE: a pair that meets every
+            // query's window; so m is finite) and has no branch;
             // if a pair's probabilities sum past 2^8 in some lane (a score
             // more than 8 above m, in log2 units, where the halves could
             // overflow), the item is redone with m the exact row maximum from

@@ -82,6 +82,10 @@ CASES = [((40, 24), 15, 64, 1, 4), ((20, 18), 11, 16, 2, 1), ((17, 13), 7, 32, 1
 # 32 real components per head (the 8x16-tile kernels), every window they cover
 CASES32 = [((20, 18), 11, 32, 2, 1), ((17, 13), 7, 64, 1, 2), ((12, 10), 5, 32, 1, 1),
            ((9, 11), 3, 64, 1, 2)]
+# one-dimensional signals (the 1D split-half kernels: windows 15 and 63, 16 and
+# 32 real components per head; lengths that are and are not multiples of 4
+# select the row DMA or the per-pixel loads for real signals)
+CASES1D = [((300,), 63, 32, 1, 2), ((258,), 15, 16, 2, 1), ((260,), 63, 32, 2, 1), ((130,), 15, 64, 1, 2)]
 MAGS = [1e-7, 1e-5, 1e-3, 1e2, 1e4]
 
 
@@ -101,6 +105,15 @@ def test_fused_across_magnitudes(ca, cuda, case, which, mag, cplx, kind):
 @pytest.mark.parametrize("kind", [0, 1])
 def test_fused_across_magnitudes_32(ca, cuda, case, which, mag, cplx, kind):
     _across_magnitudes(ca, cuda, case, which, mag, cplx, kind, 50)
+
+
+@pytest.mark.parametrize("case", CASES1D, ids=lambda c: f"{c[0]}-ws{c[1]}-C{c[2]}-h{c[4]}")
+@pytest.mark.parametrize("which", ["v_dy", "q_k", "all"])
+@pytest.mark.parametrize("mag", MAGS)
+@pytest.mark.parametrize("cplx", [False, True])
+@pytest.mark.parametrize("kind", [0, 1])
+def test_fused_across_magnitudes_1d(ca, cuda, case, which, mag, cplx, kind):
+    _across_magnitudes(ca, cuda, case, which, mag, cplx, kind, 80)
 
 
 def _across_magnitudes(ca, cuda, case, which, mag, cplx, kind, seed0):
@@ -209,6 +222,53 @@ def test_fused_forward_redo_path_32(ca, cuda, kind):
     q, k, v, dy = (seeded(3700 + i + 5 * kind, shape) for i in range(4))
     q, k = q * np.float32(2.5), k * np.float32(2.5)
     assert central_gap(kind, q, k, ws, nh, tile_h=8, crows=4, ccols=8) > 8.5
+    y, dq, dk, dv = fused(ca, cuda, kind, q, k, v, dy, ws, nh)
+    yr, _ = O.attention_fwd(kind, *(f64(a) for a in (q, k, v)), ws, nh)
+    gr = O.attention_bwd(kind, *(f64(a) for a in (q, k, v, dy)), ws, nh)
+    assert rel_err(y, yr) < TOL_FWD
+    for name, g, r in zip(("dq", "dk", "dv"), (dq, dk, dv), gr):
+        assert rel_err(g, r) < TOL_GRAD, (name, rel_err(g, r))
+
+
+def central_gap_1d(kind, q, k, ws, nh, tile):
+    """central_gap for one-dimensional signals: the wavefront of query r holds
+    the 16 queries from r - r % 16 and its key region starts P pixels before
+    them; the central pair is that region's keys 32 pc .. 32 pc + 31,
+    pc = (8 + P) // 32, on tiles of `tile` pixels (256 for 16 real components
+    per head, 128 for 32)."""
+    (n1,) = O.spatial_dims(q)
+    P = (ws - 1) // 2
+    pc = (8 + P) // 32
+    qf, kf = O._flat(q, nh), O._flat(k, nh)
+    dh = qf.shape[1]
+    S = O.similarity(kind, f64(qf), f64(kf), (n1,), ws, 1.0 / math.sqrt(dh))
+    S = S.reshape(qf.shape[0], n1, ws) * (1.0 / math.log(2.0))
+    _, colval = O.pattern((n1,), ws, 1)
+    cols = colval.reshape(n1, -1) - 1
+    best = -np.inf
+    for r in range(n1):
+        start = r - r % tile + 16 * ((r % tile) // 16) - P + 32 * pc
+        cset = {(start + d) % n1 for d in range(32)}
+        central = np.array([c in cset for c in cols[r]])
+        gap = S[:, r, :].max(axis=1) - np.where(central, S[:, r, :], -np.inf).max(axis=1)
+        best = max(best, float(gap.max()))
+    return best
+
+
+@pytest.mark.parametrize("case", [((400,), 32, 2, 256), ((300,), 32, 1, 128)],
+                         ids=["16-components", "32-components"])
+@pytest.mark.parametrize("kind", [0, 1])
+def test_fused_forward_redo_path_1d(ca, cuda, case, kind):
+    """The redo path of the one-dimensional forward at window 63 (reference
+    maximum from the central pair of a wavefront's 78-key region), q and k
+    scaled by 2.5 so that scores more than 8 above it occur; checked on the
+    CPU first, then the GPU result against the oracle."""
+    dims, C, nh, tile = case
+    ws, B = 63, 1
+    shape = (B, C, *reversed(dims))
+    q, k, v, dy = (seeded(3800 + i + 5 * kind + dims[0], shape) for i in range(4))
+    q, k = q * np.float32(2.5), k * np.float32(2.5)
+    assert central_gap_1d(kind, q, k, ws, nh, tile) > 8.5
     y, dq, dk, dv = fused(ca, cuda, kind, q, k, v, dy, ws, nh)
     yr, _ = O.attention_fwd(kind, *(f64(a) for a in (q, k, v)), ws, nh)
     gr = O.attention_bwd(kind, *(f64(a) for a in (q, k, v, dy)), ws, nh)
