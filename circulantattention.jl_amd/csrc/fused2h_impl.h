@@ -334,9 +334,11 @@ struct HGeo {
     static constexpr int wrow(int wh) { return ONE ? 16 * wh : 8 * wh; }
     static constexpr int sbslot(int b) { return sidx(BR * (b / NKW), BC * (b % NKW)); }
     // central pair of the streamed forward: two blocks of the block row that
-    // holds key rows 8, 9 (in every query's window when 2P >= 9); ONE: the
-    // pair of keys 32 PCENT .. 32 PCENT + 31 of the 16 + 2P key region
-    static constexpr int PCENT = ONE ? (8 + P) / 32 : (8 / BR) * NKW / 2;
+    // holds key rows 8, 9 (in every query's window when 2P >= 9); for smaller
+    // windows the two block rows that hold key row 7 (4..7 with 2x8 blocks,
+    // 0..7 with 4x4); ONE: the pair of keys 32 PCENT .. 32 PCENT + 31 of the
+    // 16 + 2P key region
+    static constexpr int PCENT = ONE ? (8 + P) / 32 : P >= 5 ? (8 / BR) * NKW / 2 : 7 / (2 * BR);
     static_assert(wrow(WH - 1) + BR * NKH <= CR, "a wavefront's blocks stay within their column's slots");
     static_assert(HH <= CR, "the staged rows fit the column");
     static_assert((8 / BR) * NKW % 2 == 0, "the central pair lies in one block row");
@@ -344,6 +346,18 @@ struct HGeo {
     // the central pair's keys meet every one of those windows
     static_assert(!ONE || (32 * PCENT <= 2 * P && 32 * PCENT + 31 >= 15 && 2 * PCENT < NBLK),
                   "the central pair holds a key of every query's window");
+    // (2D) query (i, j) of a wavefront's 8x2 block has region rows i .. i + 2P
+    // and columns j .. j + 2P in its window: the central pair's rows and
+    // columns (one rectangle) meet every one of them
+    static constexpr bool central_ok() {
+        const int b0 = 2 * PCENT, b1 = 2 * PCENT + 1 < NBLK ? 2 * PCENT + 1 : 2 * PCENT;
+        const int ra = BR * (b0 / NKW), rb = BR * (b1 / NKW), ca = BC * (b0 % NKW), cb = BC * (b1 % NKW);
+        const int r0 = ra < rb ? ra : rb, r1 = (ra < rb ? rb : ra) + BR - 1;
+        const int c0 = ca < cb ? ca : cb, c1 = (ca < cb ? cb : ca) + BC - 1;
+        const bool rect = ra == rb || ca == cb;
+        return rect && 2 * PCENT < NBLK && r0 <= 2 * P && r1 >= 7 && c0 <= 2 * P && c1 >= 1;
+    }
+    static_assert(ONE || central_ok(), "the central pair holds a key of every query's window");
 };
 static_assert(HGeo<5, 2>::LPX == 520 && HGeo<5, 2>::NBLK == 15, "4x4 blocks at ws 11");
 static_assert(HGeo<7, 1>::LPX == f2d::Geo<7, 1, 2, 8>::LPX && HGeo<7, 1>::NBLK == f2d::Geo<7, 1, 2, 8>::NBLK,
@@ -443,10 +457,9 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
     // and half way through the walk); 16-component kernels keep one pair
     // (spreading was 2% slower in their query-centric pass at cfg3)
     constexpr bool SPREAD = !ONE && MODE != FWD && NT == 2;
-    // forward with a reference maximum from the central block pair (2D: rows
-    // 8, 9 of the key region lie in every query's window when 2P >= 9; ONE:
-    // the pair PCENT meets every window)
-    constexpr bool STREAM = MODE == FWD && P >= 5 && (BR == 4 || NKW == 2 || ONE);
+    // every forward takes its reference maximum from the central block pair
+    // PCENT, which holds a key of every query's window
+    constexpr bool STREAM = MODE == FWD;
     constexpr int PFP = STREAM                      ? 0
                         : (MODE == FWD && NCH == 2)   ? CHP - 1
                         : (SPREAD && NPAIR > 3)       ? 1
@@ -1189,9 +1202,8 @@ __global__ __launch_bounds__((HGeo<P, NT, ONE>::THREADS), 1) void kernel2h(Args 
             auto apply = [&](auto PI, const f4 (&sv)[2]) { return apply_ops(load_ops(PI), sv); };
             // Scores relative to a reference maximum m, folded into the MFMA's
             // initial accumulator.  The first walk takes m from the central
-            // pair PC (2D: block row 4, rows 8, 9 of the key region lie in every
-            // query's window when 2P >= 9; ONE: a pair that meets every
-            // query's window; so m is finite) and has no branch;
+            // pair PC (it holds a key of every query's window, so m is
+            // finite) and has no branch;
             // if a pair's probabilities sum past 2^8 in some lane (a score
             // more than 8 above m, in log2 units, where the halves could
             // overflow), the item is redone with m the exact row maximum from

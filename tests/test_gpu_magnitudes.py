@@ -162,13 +162,14 @@ def test_fused_at_the_reference_loss_scale(ca, cuda, kind):
         assert rel_err(g, r) < TOL_GRAD, (name, rel_err(g, r))
 
 
-def central_gap(kind, q, k, ws, nh, tile_h=16, tile_w=16, crows=2, ccols=16):
+def central_gap(kind, q, k, ws, nh, tile_h=16, tile_w=16, crows=2, ccols=16, crow0=8):
     """Largest (over queries) of max_window(s) - max_central(s) in log2 units,
     where the central keys are the block pair the split-half forward takes its
-    reference maximum from: crows halo rows from tile row 8 wh + 8 - P of the
-    query's wavefront and ccols halo columns from 2 ww - P (2 x 16 for 2x8 LDS
-    blocks; 4 x 8 for the 4x4 blocks of 32 real components at ws 11), on tiles
-    of tile_h x tile_w pixels (16 x 16, or 8 x 16 for 32 real components)."""
+    reference maximum from: crows halo rows from tile row 8 wh + crow0 - P of
+    the query's wavefront and ccols halo columns from 2 ww - P (rows 8, 9 x 16
+    columns for 2x8 LDS blocks at ws 15; 8..11 x 8 for the 4x4 blocks at ws 11;
+    4..7 x 8 for 2x8 blocks at ws 5 and 7; 0..7 x 4 for 4x4 blocks at ws 3), on
+    tiles of tile_h x tile_w pixels (16 x 16, or 8 x 16 for 32 real components)."""
     dims = O.spatial_dims(q)
     n1, n2 = dims
     P = (ws - 1) // 2
@@ -183,7 +184,7 @@ def central_gap(kind, q, k, ws, nh, tile_h=16, tile_w=16, crows=2, ccols=16):
         h, w = r % n1, r // n1
         th, tw = h % tile_h, w % tile_w
         wh, ww = th // 8, tw // 2
-        rows = {(h - th + 8 * wh + 8 - P + d) % n1 for d in range(crows)}
+        rows = {(h - th + 8 * wh + crow0 - P + d) % n1 for d in range(crows)}
         cset = {(w - tw + 2 * ww - P + d) % n2 for d in range(ccols)}
         central = np.array([(c % n1) in rows and (c // n1) in cset for c in cols[r]])
         gap = S[:, r, :].max(axis=1) - np.where(central, S[:, r, :], -np.inf).max(axis=1)
@@ -191,20 +192,24 @@ def central_gap(kind, q, k, ws, nh, tile_h=16, tile_w=16, crows=2, ccols=16):
     return best
 
 
-@pytest.mark.parametrize("ws", [11, 15])
+# the central pair of each window: (first row, rows, columns) of the key region
+CENTRAL = {3: (0, 8, 4), 5: (4, 4, 8), 7: (4, 4, 8), 11: (8, 4, 8), 15: (8, 2, 16)}
+
+
+@pytest.mark.parametrize("ws", [3, 5, 7, 11, 15])
 @pytest.mark.parametrize("kind", [0, 1])
 def test_fused_forward_redo_path(ca, cuda, ws, kind):
-    """For windows of 11 and 15 the split-half forward takes its softmax
-    reference maximum from a central block pair and redoes an item with the
-    exact row maximum when some score passes it by more than 8 (log2 units).
-    q and k scaled by 2.5 make such scores common; the test first checks on
-    the CPU that they occur, then the GPU result against the oracle."""
+    """The split-half forward takes its softmax reference maximum from a
+    central block pair and redoes an item with the exact row maximum when
+    some score passes it by more than 8 (log2 units).  q and k scaled by 2.5
+    make such scores common; the test first checks on the CPU that they
+    occur, then the GPU result against the oracle."""
     dims, C, B, nh = (40, 24), 32, 1, 2
     shape = (B, C, *reversed(dims))
     q, k, v, dy = (seeded(3600 + i + ws + 5 * kind, shape) for i in range(4))
     q, k = q * np.float32(2.5), k * np.float32(2.5)
-    crows, ccols = (4, 8) if ws == 11 else (2, 16)  # 4x4 LDS blocks at ws 11, 2x8 at 15
-    assert central_gap(kind, q, k, ws, nh, crows=crows, ccols=ccols) > 8.5
+    crow0, crows, ccols = CENTRAL[ws]
+    assert central_gap(kind, q, k, ws, nh, crows=crows, ccols=ccols, crow0=crow0) > 8.5
     y, dq, dk, dv = fused(ca, cuda, kind, q, k, v, dy, ws, nh)
     yr, _ = O.attention_fwd(kind, *(f64(a) for a in (q, k, v)), ws, nh)
     gr = O.attention_bwd(kind, *(f64(a) for a in (q, k, v, dy)), ws, nh)
@@ -213,15 +218,17 @@ def test_fused_forward_redo_path(ca, cuda, ws, kind):
         assert rel_err(g, r) < TOL_GRAD, (name, rel_err(g, r))
 
 
+@pytest.mark.parametrize("ws", [3, 7, 11])
 @pytest.mark.parametrize("kind", [0, 1])
-def test_fused_forward_redo_path_32(ca, cuda, kind):
+def test_fused_forward_redo_path_32(ca, cuda, ws, kind):
     """The redo path of the forward for 32 real components per head (8x16
-    tiles, 4x4 LDS blocks, window 11), q and k scaled by 2.5 as above."""
-    dims, C, B, nh, ws = (40, 24), 64, 1, 2, 11
+    tiles), q and k scaled by 2.5 as above."""
+    dims, C, B, nh = (40, 24), 64, 1, 2
     shape = (B, C, *reversed(dims))
-    q, k, v, dy = (seeded(3700 + i + 5 * kind, shape) for i in range(4))
+    q, k, v, dy = (seeded(3700 + i + 5 * kind + ws, shape) for i in range(4))
     q, k = q * np.float32(2.5), k * np.float32(2.5)
-    assert central_gap(kind, q, k, ws, nh, tile_h=8, crows=4, ccols=8) > 8.5
+    crow0, crows, ccols = CENTRAL[ws]
+    assert central_gap(kind, q, k, ws, nh, tile_h=8, crows=crows, ccols=ccols, crow0=crow0) > 8.5
     y, dq, dk, dv = fused(ca, cuda, kind, q, k, v, dy, ws, nh)
     yr, _ = O.attention_fwd(kind, *(f64(a) for a in (q, k, v)), ws, nh)
     gr = O.attention_bwd(kind, *(f64(a) for a in (q, k, v, dy)), ws, nh)
